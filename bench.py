@@ -1,0 +1,211 @@
+"""Throughput of the MI355X swin2sr backend on the north-star workload.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (BASELINE.json metric): Swin2SR classical x4, fp32, a 256x256 RGB
+input upscaled to 1024x1024, whole image, one GPU. Weights are random-init by
+the benchmark's rules (seed 3; there is no published checkpoint offline) and
+the input is config 2's generator (8 random 2-D sinusoids + N(0, 4^2) noise,
+clipped to u8) at 256x256, seed 3. A step is one whole-image forward
+(s2s_forward_device: padding, 36 Swin blocks, 6 RSTB closes, the head, the
+denormalise/crop) from an HBM-resident mean-adjusted input to an HBM-resident
+output.
+
+One JSON line on stdout. `roofline` is for the kernel with the largest share
+of device time in the timed region, timed there with HIP events on the
+library's own stream; `cpu_baseline` is this repository's C restatement of the
+crate's CPU path (oracle/, OpenMP over the host cores) on a bounded sample.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__ as ge  # noqa: E402
+
+METRIC = "output Mpix/s classical-x4 256²→1024² fp32 @1 GPU; % MFMA / HBM roofline"
+MFMA_FP32_PEAK = 157.3e12   # MI355X dense fp32 matrix, FLOP/s (AMD spec)
+HBM_PEAK = 8.0e12           # MI355X HBM3E, B/s (AMD spec)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_work(arch, h, w):
+    """Algorithmic work per launch of each named kernel: (bound, flops, bytes).
+    FLOPs count 2 per multiply-add over the real (unpadded) GEMM extents on the
+    padded plane; bytes are the minimum unique fp32 reads + writes."""
+    win, C, s, F = arch.window, arch.embed, arch.scale, arch.feat
+    hp, wp = (h // win + 1) * win, (w // win + 1) * win
+    P = hp * wp
+    Hd = arch.mlp_ratio * C
+    f = 4
+    work = {
+        "qkv": ("mfma", 2 * P * 3 * C * C, f * P * (C + 3 * C)),
+        "window_attention": ("mfma", 4 * P * win * win * C, f * P * (3 * C + C)),
+        "proj_ln_res": ("mfma", 2 * P * C * C, f * P * 3 * C),
+        "fc1_gelu": ("mfma", 2 * P * Hd * C, f * P * (C + Hd)),
+        "fc2_ln_res": ("mfma", 2 * P * C * Hd, f * P * (Hd + 2 * C)),
+        "conv3x3_stage": ("mfma", 2 * P * C * 9 * C, f * P * 2 * C),
+        "conv1x1_res": ("mfma", 2 * P * C * C, f * P * 3 * C),
+        "conv_first": ("mfma", 2 * P * C * 27, f * P * (4 + C)),
+        "patch_embed_ln": ("mfma", 2 * P * C * C, f * P * 2 * C),
+        "conv_after_body_res": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),
+        "conv_before_upsample": ("mfma", 2 * P * F * 9 * C, f * P * (C + F)),
+        "layernorm": ("hbm", 10 * P * C, f * P * 2 * C),
+        "pad_input": ("hbm", 0, f * (3 * h * w + 4 * P)),
+        "conv_last_finish": ("hbm", 2 * (h * s) * (w * s) * 3 * 9 * F,
+                             f * ((hp * s) * (wp * s) * F + 3 * h * s * w * s)),
+    }
+    px = P
+    for o in range(arch.octaves):
+        work[f"conv3x3_shuffle2_o{o}"] = ("mfma", 2 * px * 4 * F * 9 * F, f * px * 5 * F)
+        px *= 4
+    return work
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    if a summary for this kernel is committed under profiles/."""
+    p = ROOT / "profiles" / f"{kernel}_traffic.md"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(M, orc, arch, weights, sample):
+    """The oracle (C restatement of the crate's CPU path) on `sample` x `sample`."""
+    img = M.to_unit(M.input_sinusoids(sample, sample, seed=3))
+    x = M.adjust(arch, img)
+    warm = M.adjust(arch, M.to_unit(M.input_sinusoids(32, 32, seed=3)))
+    orc.forward(arch, weights, 32, 32, warm)
+    t0 = time.perf_counter()
+    orc.forward(arch, weights, sample, sample, x)
+    dt = time.perf_counter() - t0
+    out_px = (sample * arch.scale) ** 2
+    return {
+        "value": round(out_px / dt / 1e6, 5),
+        "unit": "Mpix/s",
+        "cores": int(orc.lib().orc_threads()),
+        "kind": "port",
+        "sample": (f"one classical-x4 {sample}x{sample}->{sample * arch.scale}x{sample * arch.scale}"
+                   f" whole-image forward (same weights and input generator), after a 32x32"
+                   f" warm-up; {dt:.2f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--size", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=128)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this backend runs a whole image on one device and has "
+              "no multi-GPU path (see DESIGN.md for how it would shard); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    pkg = ge.load_package()
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    h = w = args.size
+    t0 = time.perf_counter()
+    weights = M.make_weights(arch, seed=3)
+    img = M.to_unit(M.input_sinusoids(h, w, seed=3))
+    x = M.adjust(arch, img)
+    log(f"bench: weights + input generated in {time.perf_counter() - t0:.1f} s")
+
+    be = pkg.HipBackend(arch, weights)
+    name, gfx = pkg.device_info()
+    log(f"bench: device {name} {gfx}; uploaded {be.uploaded_bytes() / 2**20:.1f} MiB")
+    din = hip.DeviceBuffer.from_array(x)
+    s = arch.scale
+    dout = hip.DeviceBuffer(3 * h * s * w * s)
+    stream = be.stream()
+
+    for _ in range(args.warmup):
+        be.forward_device(h, w, din.ptr, dout.ptr)
+    hip.stream_synchronize(stream)
+    log(f"bench: {args.warmup} warm-up steps done")
+
+    # timed region: K whole-image forwards, per-kernel events on the library stream
+    be.profile(True)
+    be.profile_reset()
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        be.forward_device(h, w, din.ptr, dout.ptr)
+    hip.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    out = dout.download((3, h * s, w * s))
+    assert np.isfinite(out).all(), "non-finite output"
+    value = (h * s) * (w * s) / 1e6 / (ms_per_step / 1e3)
+    log(f"bench: {args.steps} steps, {ms_per_step:.3f} ms/step, {value:.3f} output Mpix/s")
+
+    work = kernel_work(arch, h, w)
+    rows = {}
+    for k in work:
+        ms, n = be.profile_query(k)
+        if n:
+            rows[k] = (ms, n)
+    total_dev = sum(ms for ms, _ in rows.values())
+    for k, (ms, n) in sorted(rows.items(), key=lambda kv: -kv[1][0]):
+        bound, fl, by = work[k]
+        avg = ms / n
+        rate = (fl / (avg / 1e3) / 1e12) if bound == "mfma" else (by / (avg / 1e3) / 1e9)
+        unit = "TFLOP/s" if bound == "mfma" else "GB/s"
+        log(f"  {k:24s} {n:5d} launches {avg:9.4f} ms avg {100 * ms / total_dev:5.1f}% "
+            f"{rate:9.2f} {unit}")
+    dom = max(rows, key=lambda k: rows[k][0])
+    bound, fl, by = work[dom]
+    avg_s = rows[dom][0] / rows[dom][1] / 1e3
+    if bound == "mfma":
+        achieved, peak, unit = fl / avg_s / 1e12, MFMA_FP32_PEAK / 1e12, "TFLOP/s"
+    else:
+        achieved, peak, unit = by / avg_s / 1e9, HBM_PEAK / 1e9, "GB/s"
+    roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(dom),
+                "kernel": dom, "avg_ms": round(avg_s * 1e3, 4),
+                "work_per_launch": fl if bound == "mfma" else by,
+                "device_ms_per_step": round(total_dev / args.steps, 3)}
+
+    result = {
+        "metric": METRIC, "value": round(value, 4), "unit": "Mpix/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init weights seed 3, config-2 sinusoid input seed 3)",
+        "config": {"workload": f"classical-x4 {h}x{w}->{h * s}x{w * s} whole-image forward",
+                   "embed": arch.embed, "depths": arch.depths, "heads": arch.heads,
+                   "window": arch.window, "padded_plane": [(h // 8 + 1) * 8, (w // 8 + 1) * 8],
+                   "parallelism": "1 GPU"},
+        "roofline": roofline,
+    }
+    be.profile(False)
+    be.close()
+    if not args.no_cpu:
+        orc = ge._load_oracle()
+        log(f"bench: cpu baseline on {orc.lib().orc_threads()} threads ...")
+        result["cpu_baseline"] = cpu_baseline(M, orc, arch, weights, args.cpu_sample)
+        log(f"bench: cpu {result['cpu_baseline']}")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,228 @@
+/* swin2sr_hip.h - the C ABI of the MI355X (gfx950) swin2sr backend.
+ *
+ * This is the drop-in boundary for the device half of the swin2sr crate: every
+ * entry point below replaces one thing the crate's CUDA backend does today
+ * (`src/gpu.rs` over `src/cuda.rs` over `lightgpu::vm`), and each declaration
+ * names the reference interface it stands in for. The Rust side binds these
+ * with `extern "C"` (the binding a maintainer adds is shown in INTEGRATION.md
+ * at the repository root); the C++ harnesses and the Python tests bind the same
+ * symbols.
+ *
+ * Conventions, all of them inherited from the crate's `Backend` contract:
+ *  - Every call that can fail returns int: 0 = ok, non-zero = error, and
+ *    `s2s_last_error()` holds the message (thread-local, owned by the library).
+ *    An allocation failure's message contains "out of memory", which is what
+ *    `run_with_fallback`'s `is_out_of_memory` keys its tile-halving retry on
+ *    (reference src/main.rs:655-662).
+ *  - Images at the boundary are planar `[3][h][w]` f32. The forward input is
+ *    MEAN-ADJUSTED by the caller (`Pre::adjust`, reference src/backend.rs:76-86)
+ *    and the output is denormalised and cropped, `[3][h*scale][w*scale]`.
+ *  - One context = one HIP stream = one host thread at a time (the reference's
+ *    `Backend` takes `&mut self`, src/backend.rs:29-49). No internal threads.
+ *  - Weights are borrowed for the duration of `s2s_create` only; they are
+ *    copied (and re-laid-out) onto the device there.
+ */
+#ifndef SWIN2SR_HIP_H
+#define SWIN2SR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Every symbol below is exported even when the library is built with hidden
+ * default visibility. */
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility push(default)
+#endif
+
+/* The reconstruction head (reference src/weights.rs:19-29, `Upsampler`). */
+enum s2s_upsampler {
+    S2S_PIXELSHUFFLE = 0,        /* classical SR: conv+lrelu, (conv3x3 + shuffle2) per octave, conv_last */
+    S2S_PIXELSHUFFLE_DIRECT = 1, /* lightweight SR: one conv to 3*s^2 + pixel_shuffle(s) */
+    S2S_NEAREST_CONV = 2,        /* real-world SR: two nearest x2 + conv + lrelu(0.2) */
+    S2S_PIXELSHUFFLE_AUX = 3     /* compressed SR: pixelshuffle + bicubic branch + aux image */
+};
+
+#define S2S_MAX_STAGES 16
+
+/* The architecture the checkpoint's `__metadata__` describes
+ * (reference src/weights.rs:66-137: task, upsampler, scale, window_size,
+ * embed_dim, num_heads, mlp_ratio, depths, img_range, rgb_mean). */
+typedef struct s2s_arch {
+    int upsampler;              /* enum s2s_upsampler */
+    int scale;
+    int window;
+    int embed;
+    int heads;                  /* head_dim = embed / heads */
+    int mlp_ratio;
+    int n_stages;
+    int depths[S2S_MAX_STAGES]; /* blocks per RSTB stage */
+    float img_range;
+    float mean[3];
+} s2s_arch;
+
+/* One named f32 tensor of the crate's checkpoint (tensor names and shapes as
+ * `Weights::validate` checks them, reference src/weights.rs:142-235).
+ * `data` is row-major in the checkpoint's (torch) layout. */
+typedef struct s2s_tensor {
+    const char *name;
+    const float *data;
+    int ndim;
+    int64_t shape[4];
+} s2s_tensor;
+
+typedef struct s2s_ctx s2s_ctx;
+
+/* ---- construction ------------------------------------------------------ */
+
+/* Replaces `Gpu::new(&Weights)` (reference src/gpu.rs:101-125): opens the
+ * device, creates the context's stream, validates the tensor set against
+ * `arch` and uploads it once, re-laid-out for the kernels. */
+int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors,
+               s2s_ctx **out);
+
+/* Frees every device allocation the context owns (the reference frees on
+ * `Drop` of `Gpu`/`Acts`, src/gpu.rs:41-81). NULL is ignored. */
+void s2s_destroy(s2s_ctx *ctx);
+
+/* `Backend::name` (reference src/gpu.rs:737-739 returns "cuda"): "hip". */
+const char *s2s_name(void);
+
+/* `gpu::uploaded_bytes` (reference src/gpu.rs:792-799): the bytes the
+ * context holds on the device for the weights. */
+uint64_t s2s_uploaded_bytes(const s2s_ctx *ctx);
+
+/* ---- the forward pass ---------------------------------------------------- */
+
+/* `Backend::forward` for the device (reference src/gpu.rs:741-754 and
+ * `forward_plan`, :462-583). `in_adjusted` is host `[3][h][w]`, mean-adjusted;
+ * `out` is caller-owned host `[3][h*scale][w*scale]`. Buffers are planned per
+ * (h, w) and reused while the size repeats. Synchronous: returns when the
+ * download has completed. */
+int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out);
+
+/* The same pass on device-resident buffers (no host copies): `d_in` is a
+ * device `[3][h][w]` mean-adjusted plane, `d_out` a device
+ * `[3][h*scale][w*scale]` buffer. Enqueued on the context's stream and NOT
+ * synchronised; `s2s_stream` / `s2s_sync` order it. No reference counterpart:
+ * the crate always hands over host slices; this is the entry a caller with
+ * inputs already in HBM (the throughput harness) uses. */
+int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
+
+/* `Backend::aux` (reference src/gpu.rs:756-758): the last forward's secondary
+ * image, denormalised, at the PADDED plane's geometry `[3][hp][wp]`. `*n` is 0
+ * (and `*ptr` NULL) when the head makes none. Valid until the next forward. */
+int s2s_aux(s2s_ctx *ctx, const float **ptr, size_t *n);
+
+/* ---- errors and device queries ------------------------------------------ */
+
+/* The message of the last failed call on this thread ("" if none). */
+const char *s2s_last_error(void);
+
+/* `vm::device()` (reference src/main.rs:169,516-517): the device name and its
+ * architecture string ("gfx950..." here, where the crate prints sm_xx). */
+int s2s_device_info(char *name, size_t name_cap, char *arch, size_t arch_cap);
+
+/* `vm::vram()` (reference src/main.rs:461): free and total device bytes. */
+int s2s_vram(uint64_t *free_bytes, uint64_t *total_bytes);
+
+/* `vm::sync()` (reference src/main.rs:342): waits for all device work. */
+int s2s_sync(void);
+
+/* The context's hipStream_t, as an opaque pointer (for callers that enqueue
+ * their own work or timing events around `s2s_forward_device`). */
+void *s2s_stream(s2s_ctx *ctx);
+
+/* ---- profiling ----------------------------------------------------------- */
+
+/* The per-launch event profiler of reference src/cuda.rs:109-140,156-259,
+ * switched on by SWIN2SR_PROFILE_GPU at `s2s_create` or by this call. While on,
+ * every kernel launch is bracketed by a hipEvent pair on the context stream. */
+int s2s_profile_enable(s2s_ctx *ctx, int on);
+
+/* Clears the accumulated profile rows. */
+int s2s_profile_reset(s2s_ctx *ctx);
+
+/* `Profile::report(total_wall_ms)` (reference src/cuda.rs:239-259): prints one
+ * row per (kernel, grid, block) to stderr, after synchronising the stream. */
+int s2s_profile_report(s2s_ctx *ctx, float wall_ms);
+
+/* Totals for one kernel name over all its rows: summed device milliseconds and
+ * launch count (after synchronising). Unknown names give 0 and 0. */
+int s2s_profile_query(s2s_ctx *ctx, const char *kernel, double *total_ms, int *launches);
+
+/* ---- the single-RSTB path (config 1 micro-bench) -------------------------- */
+
+/* One residual Swin transformer block group (stage `stage` of the checkpoint:
+ * its blocks, then conv3x3, 1x1 and the stage residual), on an explicit
+ * `hp x wp` plane (both multiples of the window; NOT re-padded), channel-last
+ * `[hp*wp][embed]` device buffers. In place is allowed (d_in == d_out).
+ * Reference: the stage loop of src/gpu.rs:481-529 / src/cpu.rs:1516-1581. */
+int s2s_rstb_device(s2s_ctx *ctx, int stage, int hp, int wp, const float *d_in, float *d_out);
+
+/* ---- per-op test entry points -------------------------------------------- */
+/* The device half of `gpu::selftest` (reference src/gpu.rs:889-1265): each runs
+ * one kernel on host buffers (uploads, launches, downloads, synchronises) so a
+ * harness can hold it against the CPU definition. Planes here are CHANNEL-LAST
+ * `[h*w][c]` (the layout this backend keeps activations in); token tables are
+ * in plane order. */
+
+/* `Plan::index` / `Plan::region` (reference src/plan.rs:72-108) as the device
+ * computes them: for every (window wi, token t) of a `hp x wp` plane,
+ * `yx[(wi*n+t)*2+{0,1}]` = plane (y, x) read at `shift`, and
+ * `reg[(wi*n+t)*2+{0,1}]` = the mask band (row, column). */
+int s2s_test_window_map(int hp, int wp, int win, int shift, int32_t *yx, uint8_t *reg);
+
+/* Window attention (reference cpu::attention, src/cpu.rs:1244-1402): `qkv` is
+ * `[hp*wp][3*c]` in plane order (q | k | v per pixel), `cpb` the `[n*n][heads]`
+ * table in the checkpoint's layout, `logit_scale` `[heads]`. `out` is
+ * `[hp*wp][c]`. Window must be 8 (n = 64), head_dim <= 32. */
+int s2s_test_attention(int hp, int wp, int win, int heads, int head_dim, int shift,
+                       const float *qkv, const float *logit_scale, const float *cpb,
+                       float *out);
+
+/* The device CPB table from the MLP weights (reference tools/convert.py:141-167):
+ * `out` is `[n*n][heads]`, 16*sigmoid(MLP(log-spaced coords)) gathered. */
+int s2s_test_cpb_table(int win, int heads, const float *w0 /*[512][2]*/,
+                       const float *b0 /*[512]*/, const float *w2 /*[heads][512]*/,
+                       float *out);
+
+/* Token GEMM with an epilogue (reference cpu::linear, src/cpu.rs:607-625, and
+ * the ops the build fuses behind it). `x` is `[rows][c_in]`, `w` `[c_out][c_in]`,
+ * `bias` `[c_out]` (NULL = zero). `res` `[rows][c_out]` is read by the
+ * residual epilogues; `ln_w`/`ln_b` `[c_out]` by the LayerNorm ones.
+ * epilogue: 0 store, 1 erf-GELU, 2 += res, 3 LayerNorm, 4 res + LayerNorm,
+ * 5 LeakyReLU(slope). LayerNorm epilogues need c_out <= 192. */
+int s2s_test_linear(int rows, int c_in, int c_out, const float *x, const float *w,
+                    const float *bias, int epilogue, const float *res, const float *ln_w,
+                    const float *ln_b, float slope, float *out);
+
+/* Channel LayerNorm over `[hw][c]` (reference cpu::channel_layer_norm,
+ * src/cpu.rs:1019-1073), optionally `y = res + LN(x)` when `res` is non-NULL. */
+int s2s_test_ln_residual(int hw, int c, const float *x, const float *ln_w, const float *ln_b,
+                         const float *res, float *out);
+
+/* 3x3 stride-1 zero-pad-1 convolution (reference cpu::conv3x3, src/cpu.rs:
+ * 400-414) on a channel-last `[h*w][c_in]` plane, weights `[c_out][c_in][3][3]`,
+ * output `[h*w][c_out]`. epilogue: 0 store, 2 += res, 5 LeakyReLU(slope). */
+int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
+                     const float *bias, int epilogue, const float *res, float slope, float *out);
+
+/* The head's fused conv3x3 + pixel_shuffle(2) (reference cpu::conv3x3_shuffle2,
+ * src/cpu.rs:502-542): weights `[4*feat][c_in][3][3]`, output channel-last
+ * `[(2h)*(2w)][feat]`. */
+int s2s_test_conv3x3_shuffle2(int h, int w, int c_in, int feat, const float *x,
+                              const float *wgt, const float *bias, float *out);
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWIN2SR_HIP_H */

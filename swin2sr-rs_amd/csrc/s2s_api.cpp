@@ -1,0 +1,856 @@
+// s2s_api.cpp - the C ABI of include/swin2sr_hip.h: context, weight upload,
+// per-size buffer planning, the forward graph, the event profiler and the
+// per-op test entry points.
+//
+// The graph is the reference's (src/gpu.rs:462-583 / src/cpu.rs:1437-1685) on
+// channel-last planes, with the elementwise ops folded into the GEMM epilogues:
+//   block (src/gpu.rs:485-522):  qkv = x Wqkv^T + [qb|0|vb]
+//                                o   = window_attention(qkv, shift)
+//                                x1  = x  + LN1(o Wp^T + bp)
+//                                x2  = x1 + LN2(gelu(x1 W1^T + b1) W2^T + b2)
+//   RSTB close (:526-528):       x   = conv1x1(conv3x3(blocks(x))) + x
+//   frame (:471-542):            conv_first -> patch_embed(1x1 + LN) -> stages
+//                                -> LN -> conv_after_body + conv_first output
+//   classical head (:601-623):   conv+lrelu(0.01), (conv3x3 + shuffle2) per
+//                                octave, conv_last + finish (denormalise, crop)
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/swin2sr_hip.h"
+#include "s2s_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const std::string &m) {
+    g_err = m;
+    return -1;
+}
+
+std::string hip_msg(const char *what, hipError_t e) {
+    std::string m = std::string(what) + " failed: " + hipGetErrorName(e) + " (" +
+                    hipGetErrorString(e) + ")";
+    // run_with_fallback retries only on "out of memory" (reference
+    // src/main.rs:655-662); make sure the phrase is there for the OOM code.
+    if (e == hipErrorOutOfMemory && m.find("out of memory") == std::string::npos)
+        m += ": out of memory";
+    return m;
+}
+
+#define HIPCHK(what, expr)                                        \
+    do {                                                          \
+        hipError_t e_ = (expr);                                   \
+        if (e_ != hipSuccess) return fail(hip_msg((what), e_));   \
+    } while (0)
+
+int round4(int v) { return (v + 3) / 4 * 4; }
+
+struct BlockW {
+    float *wqkv = nullptr, *bqkv = nullptr, *wproj = nullptr, *bproj = nullptr;
+    float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+    float *w1 = nullptr, *b1 = nullptr, *w2 = nullptr, *b2 = nullptr;
+    float *ls = nullptr, *cpbt = nullptr;
+};
+
+struct StageW {
+    std::vector<BlockW> blocks;
+    float *conv_w = nullptr, *conv_b = nullptr, *pe_w = nullptr, *pe_b = nullptr;
+};
+
+struct ProfKey {
+    std::string name;
+    unsigned g[3], b[3];
+    bool operator<(const ProfKey &o) const {
+        return std::tie(name, g[0], g[1], g[2], b[0], b[1], b[2]) <
+               std::tie(o.name, o.g[0], o.g[1], o.g[2], o.b[0], o.b[1], o.b[2]);
+    }
+};
+struct ProfRow {
+    int calls = 0;
+    double ms = 0.0;
+};
+struct Pending {
+    ProfKey key;
+    hipEvent_t e0, e1;
+};
+
+}  // namespace
+
+int s2s_fail(const char *msg) { return fail(msg ? msg : "unknown error"); }
+
+struct s2s_ctx {
+    s2s_arch arch{};
+    int c = 0, hd = 0, hidden = 0, feat = 0, octaves = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void *> weight_allocs;
+    uint64_t uploaded = 0;
+
+    float *cf_w = nullptr, *cf_b = nullptr;  // conv_first [C][9*4]
+    float *pe_w = nullptr, *pe_b = nullptr, *pe_nw = nullptr, *pe_nb = nullptr;
+    float *norm_w = nullptr, *norm_b = nullptr;
+    float *cab_w = nullptr, *cab_b = nullptr;  // conv_after_body [C][9*C]
+    std::vector<StageW> stages;
+    float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C]
+    std::vector<float *> up_w, up_b;           // octave convs, shuffle-permuted [4F][9*F]
+    float *last_w = nullptr, *last_b = nullptr;  // conv_last [9][F][3]
+
+    // buffers planned for one padded plane (hp, wp)
+    int bhp = 0, bwp = 0;
+    std::vector<void *> body_allocs;
+    float *cur = nullptr, *wk = nullptr, *tmp = nullptr, *body = nullptr;
+    float *qkv = nullptr, *o = nullptr, *hid = nullptr;
+    // head / io buffers planned for one image (h, w)
+    int ih = 0, iw = 0;
+    std::vector<void *> head_allocs;
+    float *in_dev = nullptr, *in4 = nullptr, *out_dev = nullptr;
+    std::vector<float *> fplanes;  // F0 .. F_octaves
+
+    bool prof = false;
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> free_events;
+    std::map<ProfKey, ProfRow> rows;
+
+    std::vector<float> aux_host;
+
+    ~s2s_ctx();
+    int upload(const std::vector<float> &host, float **dev);
+    int alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what);
+    int plan_body(int hp, int wp);
+    int plan_image(int h, int w);
+    hipEvent_t event();
+    int drain();
+    template <typename F>
+    int run(const char *name, dim3 grid, dim3 block, F &&launch);
+    int gemm(const char *name, const GemmArgs &g, int aload, int epi);
+    int block_fwd(const BlockW &b, int hp, int wp, int shift, const float *x_in, float *x_out);
+    int stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out);
+    int forward_device(int h, int w, const float *d_in, float *d_out);
+};
+
+namespace {
+
+void free_list(std::vector<void *> &l) {
+    for (void *p : l) (void)hipFree(p);
+    l.clear();
+}
+
+}  // namespace
+
+s2s_ctx::~s2s_ctx() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto &p : pending) {
+        (void)hipEventDestroy(p.e0);
+        (void)hipEventDestroy(p.e1);
+    }
+    for (auto e : free_events) (void)hipEventDestroy(e);
+    free_list(head_allocs);
+    free_list(body_allocs);
+    free_list(weight_allocs);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
+    float *p = nullptr;
+    HIPCHK("hipMalloc(weights)", hipMalloc(&p, std::max<size_t>(host.size(), 1) * sizeof(float)));
+    weight_allocs.push_back(p);
+    HIPCHK("hipMemcpy(weights)",
+           hipMemcpy(p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice));
+    uploaded += host.size() * sizeof(float);
+    *dev = p;
+    return 0;
+}
+
+int s2s_ctx::alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what) {
+    float *p = nullptr;
+    hipError_t e = hipMalloc(&p, std::max<size_t>(floats, 1) * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(std::string("hipMalloc(") + what + ", " +
+                    std::to_string(floats * sizeof(float)) + " bytes) failed: " +
+                    hipGetErrorString(e) + (e == hipErrorOutOfMemory ? " (out of memory)" : ""));
+    }
+    list.push_back(p);
+    *dev = p;
+    return 0;
+}
+
+// Body buffers for a padded plane: the activation, the in-stage working copy,
+// the conv scratch, conv_first's output (the body skip), qkv, the attention
+// output and the MLP hidden layer. Reused while the plane size repeats
+// (reference Gpu::forward rebuilds Acts only on a size change, src/gpu.rs:741-750).
+int s2s_ctx::plan_body(int hp, int wp) {
+    if (hp == bhp && wp == bwp) return 0;
+    if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
+    free_list(body_allocs);
+    bhp = bwp = 0;
+    const size_t P = (size_t)hp * wp;
+    if (alloc(body_allocs, P * c, &cur, "cur") || alloc(body_allocs, P * c, &wk, "work") ||
+        alloc(body_allocs, P * c, &tmp, "tmp") || alloc(body_allocs, P * c, &body, "body") ||
+        alloc(body_allocs, P * 3 * c, &qkv, "qkv") || alloc(body_allocs, P * c, &o, "attn") ||
+        alloc(body_allocs, P * hidden, &hid, "mlp")) {
+        free_list(body_allocs);
+        return -1;
+    }
+    bhp = hp;
+    bwp = wp;
+    return 0;
+}
+
+int s2s_ctx::plan_image(int h, int w) {
+    const int win = arch.window;
+    const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
+    if (plan_body(hp, wp)) return -1;
+    if (h == ih && w == iw) return 0;
+    if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
+    free_list(head_allocs);
+    fplanes.clear();
+    ih = iw = 0;
+    const size_t P = (size_t)hp * wp;
+    const int s = arch.scale;
+    int rc = alloc(head_allocs, (size_t)3 * h * w, &in_dev, "input") ||
+             alloc(head_allocs, P * 4, &in4, "padded input") ||
+             alloc(head_allocs, (size_t)3 * h * s * w * s, &out_dev, "output");
+    size_t px = P;
+    for (int o_ = 0; rc == 0 && o_ <= octaves; ++o_) {
+        float *f = nullptr;
+        rc = alloc(head_allocs, px * feat, &f, "head plane");
+        fplanes.push_back(f);
+        px *= 4;
+    }
+    if (rc) {
+        free_list(head_allocs);
+        fplanes.clear();
+        return -1;
+    }
+    ih = h;
+    iw = w;
+    return 0;
+}
+
+hipEvent_t s2s_ctx::event() {
+    if (!free_events.empty()) {
+        hipEvent_t e = free_events.back();
+        free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+int s2s_ctx::drain() {
+    if (pending.empty()) return 0;
+    HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
+    for (auto &p : pending) {
+        float ms = 0.f;
+        HIPCHK("hipEventElapsedTime", hipEventElapsedTime(&ms, p.e0, p.e1));
+        ProfRow &r = rows[p.key];
+        r.calls += 1;
+        r.ms += ms;
+        free_events.push_back(p.e0);
+        free_events.push_back(p.e1);
+    }
+    pending.clear();
+    return 0;
+}
+
+// One launch, bracketed by an event pair when profiling (reference
+// Cuda::run, src/cuda.rs:109-140).
+template <typename F>
+int s2s_ctx::run(const char *name, dim3 grid, dim3 block, F &&launch) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (prof) {
+        e0 = event();
+        e1 = event();
+        if (!e0 || !e1) return fail("hipEventCreate failed");
+        HIPCHK("hipEventRecord", hipEventRecord(e0, stream));
+    }
+    hipError_t e = launch();
+    if (e != hipSuccess) return fail(hip_msg(name, e));
+    if (prof) {
+        HIPCHK("hipEventRecord", hipEventRecord(e1, stream));
+        pending.push_back(Pending{ProfKey{name, {grid.x, grid.y, grid.z}, {block.x, block.y, block.z}},
+                                  e0, e1});
+        if (pending.size() > 4096) return drain();
+    }
+    return 0;
+}
+
+int s2s_ctx::gemm(const char *name, const GemmArgs &g, int aload, int epi) {
+    unsigned gx, gy;
+    gemm_grid(g, epi, &gx, &gy);
+    return run(name, dim3(gx, gy, 1), dim3(256, 1, 1),
+               [&] { return launch_gemm(g, aload, epi, stream); });
+}
+
+namespace {
+
+GemmArgs rows_gemm(const float *A, int lda, const float *B, int ldb, const float *bias, float *out,
+                   int ldo, int M, int N, int K) {
+    GemmArgs g{};
+    g.A = A;
+    g.lda = lda;
+    g.B = B;
+    g.ldb = ldb;
+    g.bias = bias;
+    g.out = out;
+    g.ldo = ldo;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    return g;
+}
+
+GemmArgs conv_gemm(const float *in, int H, int W, int cin, const float *wt, const float *bias,
+                   float *out, int ldo, int N) {
+    GemmArgs g{};
+    g.A = in;
+    g.H = H;
+    g.W = W;
+    g.cin = cin;
+    g.B = wt;
+    g.ldb = 9 * cin;
+    g.bias = bias;
+    g.out = out;
+    g.ldo = ldo;
+    g.M = H * W;
+    g.N = N;
+    g.K = 9 * cin;
+    return g;
+}
+
+}  // namespace
+
+// One post-norm Swin V2 block (reference src/gpu.rs:485-522), x_in -> x_out
+// (x_out may equal x_in).
+int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *x_in,
+                       float *x_out) {
+    const int P = hp * wp;
+    GemmArgs g = rows_gemm(x_in, c, b.wqkv, c, b.bqkv, qkv, 3 * c, P, 3 * c, c);
+    if (gemm("qkv", g, ALOAD_ROWS, EPI_STORE)) return -1;
+
+    AttnArgs a{};
+    a.qkv = qkv;
+    a.cpbt = b.cpbt;
+    a.logit_scale = b.ls;
+    a.out = o;
+    a.hp = hp;
+    a.wp = wp;
+    a.nww = wp / arch.window;
+    a.nw = (hp / arch.window) * a.nww;
+    a.heads = arch.heads;
+    a.head_dim = hd;
+    a.c = c;
+    a.shift = shift;
+    unsigned ag = (unsigned)((a.nw * a.heads + 3) / 4);
+    if (run("window_attention", dim3(ag), dim3(256),
+            [&] { return launch_attention(a, stream, nullptr); }))
+        return -1;
+
+    g = rows_gemm(o, c, b.wproj, c, b.bproj, x_out, c, P, c, c);
+    g.res = x_in;
+    g.ldr = c;
+    g.ln_w = b.n1w;
+    g.ln_b = b.n1b;
+    if (gemm("proj_ln_res", g, ALOAD_ROWS, EPI_LN_RES)) return -1;
+
+    g = rows_gemm(x_out, c, b.w1, c, b.b1, hid, hidden, P, hidden, c);
+    if (gemm("fc1_gelu", g, ALOAD_ROWS, EPI_GELU)) return -1;
+
+    g = rows_gemm(hid, hidden, b.w2, hidden, b.b2, x_out, c, P, c, hidden);
+    g.res = x_out;
+    g.ldr = c;
+    g.ln_w = b.n2w;
+    g.ln_b = b.n2b;
+    return gemm("fc2_ln_res", g, ALOAD_ROWS, EPI_LN_RES);
+}
+
+// One RSTB stage (reference src/gpu.rs:481-529): blocks, conv3x3, 1x1, + x_in.
+int s2s_ctx::stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out) {
+    const StageW &st = stages[s];
+    const int P = hp * wp;
+    const float *src = x_in;
+    for (size_t bi = 0; bi < st.blocks.size(); ++bi) {
+        const int shift = (bi % 2 == 1) ? arch.window / 2 : 0;
+        if (block_fwd(st.blocks[bi], hp, wp, shift, src, wk)) return -1;
+        src = wk;
+    }
+    GemmArgs g = conv_gemm(src, hp, wp, c, st.conv_w, st.conv_b, tmp, c, c);
+    if (gemm("conv3x3_stage", g, ALOAD_IM2COL, EPI_STORE)) return -1;
+    g = rows_gemm(tmp, c, st.pe_w, c, st.pe_b, x_out, c, P, c, c);
+    g.res = x_in;
+    g.ldr = c;
+    return gemm("conv1x1_res", g, ALOAD_ROWS, EPI_RES);
+}
+
+int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
+    const int win = arch.window;
+    if (h < win || w < win)
+        return fail(std::to_string(h) + "x" + std::to_string(w) + " is smaller than one " +
+                    std::to_string(win) + "x" + std::to_string(win) +
+                    " window. The reference pads to the NEXT window multiple by concatenating "
+                    "the image with its own mirror, which for an image shorter than a window "
+                    "falls through to a different padding rule this engine does not implement.");
+    if (arch.upsampler != S2S_PIXELSHUFFLE)
+        return fail("this device backend implements the pixelshuffle head; upsampler " +
+                    std::to_string(arch.upsampler) + " is not built yet");
+    if (plan_image(h, w)) return -1;
+    const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
+    const int P = hp * wp;
+    if (run("pad_input", dim3((P + 255) / 256), dim3(256),
+            [&] { return launch_pad_input(d_in, in4, h, w, hp, wp, stream); }))
+        return -1;
+    GemmArgs g = conv_gemm(in4, hp, wp, 4, cf_w, cf_b, body, c, c);
+    if (gemm("conv_first", g, ALOAD_IM2COL, EPI_STORE)) return -1;
+    g = rows_gemm(body, c, pe_w, c, pe_b, cur, c, P, c, c);
+    g.ln_w = pe_nw;
+    g.ln_b = pe_nb;
+    if (gemm("patch_embed_ln", g, ALOAD_ROWS, EPI_LN)) return -1;
+    for (int s = 0; s < arch.n_stages; ++s)
+        if (stage_fwd(s, hp, wp, cur, cur)) return -1;
+    if (run("layernorm", dim3((P + 15) / 16), dim3(256),
+            [&] { return launch_layernorm(cur, norm_w, norm_b, nullptr, tmp, P, c, stream); }))
+        return -1;
+    g = conv_gemm(tmp, hp, wp, c, cab_w, cab_b, cur, c, c);
+    g.res = body;
+    g.ldr = c;
+    if (gemm("conv_after_body_res", g, ALOAD_IM2COL, EPI_RES)) return -1;
+    g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
+    g.slope = 0.01f;
+    if (gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+    int H = hp, W = wp;
+    for (int oc = 0; oc < octaves; ++oc) {
+        g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
+        g.feat = feat;
+        const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
+        if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
+        H *= 2;
+        W *= 2;
+    }
+    const int s = arch.scale;
+    const int oh = h * s, ow = w * s;
+    return run("conv_last_finish", dim3((ow + 63) / 64, (oh + 3) / 4), dim3(256), [&] {
+        return launch_conv_last_finish(fplanes[octaves], last_w, last_b, d_out, H, W, feat, oh,
+                                       ow, arch.img_range, arch.mean, stream);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Weight set: lookup, validation and re-layout.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct TensorSet {
+    const s2s_tensor *t;
+    size_t n;
+    const s2s_tensor *find(const std::string &name) const {
+        for (size_t i = 0; i < n; ++i)
+            if (t[i].name && name == t[i].name) return &t[i];
+        return nullptr;
+    }
+    size_t numel(const s2s_tensor *x) const {
+        size_t v = 1;
+        for (int d = 0; d < x->ndim; ++d) v *= (size_t)x->shape[d];
+        return v;
+    }
+    // The tensor, or an error naming it and the shape expected (the reference
+    // refuses a checkpoint the same way, src/weights.rs:142-235).
+    int get(const std::string &name, std::vector<int64_t> shape, const s2s_tensor **out) const {
+        const s2s_tensor *x = find(name);
+        if (!x) return fail("weight `" + name + "` is missing from the tensor set");
+        bool ok = x->ndim == (int)shape.size();
+        for (int d = 0; ok && d < x->ndim; ++d) ok = x->shape[d] == shape[d];
+        if (!ok) {
+            std::string got, want;
+            for (int d = 0; d < x->ndim; ++d) got += (d ? "," : "") + std::to_string(x->shape[d]);
+            for (size_t d = 0; d < shape.size(); ++d)
+                want += (d ? "," : "") + std::to_string(shape[d]);
+            return fail("weight `" + name + "` is [" + got + "], the architecture implies [" +
+                        want + "]");
+        }
+        *out = x;
+        return 0;
+    }
+};
+
+std::vector<float> vec_of(const s2s_tensor *x, size_t n) { return std::vector<float>(x->data, x->data + n); }
+
+// [co][ci][3][3] -> [co][tap][ci_pad] (tap = ky*3+kx, ci zero-padded to 4)
+std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vector<int> *perm) {
+    const int cp = round4(ci);
+    std::vector<float> out((size_t)co * 9 * cp, 0.f);
+    for (int o = 0; o < co; ++o) {
+        const int dst = perm ? (*perm)[o] : o;
+        for (int i = 0; i < ci; ++i)
+            for (int t = 0; t < 9; ++t)
+                out[((size_t)dst * 9 + t) * cp + i] = w[((size_t)o * ci + i) * 9 + t];
+    }
+    return out;
+}
+
+// co = 4ch + 2dy + dx  ->  row (2dy+dx)*feat + ch, so a 32-column tile of the
+// GEMM is 32 consecutive output channels of one sub-pixel (coalesced stores).
+std::vector<int> shuffle_perm(int feat) {
+    std::vector<int> p(4 * feat);
+    for (int co = 0; co < 4 * feat; ++co) p[co] = (co % 4) * feat + co / 4;
+    return p;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Exported ABI
+// ---------------------------------------------------------------------------
+
+extern "C" {
+
+const char *s2s_last_error(void) { return g_err.c_str(); }
+
+const char *s2s_name(void) { return "hip"; }
+
+int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors, s2s_ctx **out) {
+    if (!arch || !tensors || !out) return fail("s2s_create: null argument");
+    *out = nullptr;
+    const s2s_arch &A = *arch;
+    if (A.embed <= 0 || A.heads <= 0 || A.embed % A.heads != 0)
+        return fail("embed_dim must be a positive multiple of num_heads");
+    if (A.embed % 4 != 0) return fail("embed_dim must be a multiple of 4 for the device kernels");
+    if (A.window != 8)
+        return fail("window " + std::to_string(A.window) +
+                    ": the device attention kernel is built for 8x8 windows (64 tokens), the "
+                    "size of every released checkpoint");
+    if (A.embed / A.heads > 32)
+        return fail("head_dim " + std::to_string(A.embed / A.heads) +
+                    " exceeds the attention kernel's 32 (every released checkpoint has <= 30)");
+    if (A.n_stages < 0 || A.n_stages > S2S_MAX_STAGES) return fail("bad stage count");
+    if (A.upsampler != S2S_PIXELSHUFFLE && A.upsampler != S2S_PIXELSHUFFLE_DIRECT &&
+        A.upsampler != S2S_NEAREST_CONV && A.upsampler != S2S_PIXELSHUFFLE_AUX)
+        return fail("unknown upsampler " + std::to_string(A.upsampler));
+
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0)
+        return fail(std::string("no HIP device: ") + (e == hipSuccess ? "count 0" : hipGetErrorString(e)));
+
+    int dev = 0;
+    HIPCHK("hipGetDevice", hipGetDevice(&dev));
+    s2s_ctx *ctx = new s2s_ctx();
+    ctx->arch = A;
+    ctx->c = A.embed;
+    ctx->hd = A.embed / A.heads;
+    ctx->hidden = A.mlp_ratio * A.embed;
+    ctx->device = dev;
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(hip_msg("hipStreamCreate", e));
+    }
+    const char *pe = getenv("SWIN2SR_PROFILE_GPU");
+    ctx->prof = pe && *pe && strcmp(pe, "0") != 0;
+
+    TensorSet ts{tensors, n_tensors};
+    const int C = A.embed, H2 = A.mlp_ratio * C, NH = A.heads, win = A.window, n = win * win;
+    const s2s_tensor *x;
+    int rc = 0;
+    auto up = [&](const std::string &name, std::vector<int64_t> shape, float **dst) -> int {
+        if (ts.get(name, shape, &x)) return -1;
+        return ctx->upload(vec_of(x, ts.numel(x)), dst);
+    };
+    auto upconv = [&](const std::string &name, int co, int ci, float **dst,
+                      const std::vector<int> *perm) -> int {
+        if (ts.get(name, {co, ci, 3, 3}, &x)) return -1;
+        return ctx->upload(conv_relayout(x->data, co, ci, perm), dst);
+    };
+
+    rc = rc || upconv("conv_first.weight", C, 3, &ctx->cf_w, nullptr);
+    rc = rc || up("conv_first.bias", {C}, &ctx->cf_b);
+    rc = rc || up("patch_embed.proj.weight", {C, C, 1, 1}, &ctx->pe_w);
+    rc = rc || up("patch_embed.proj.bias", {C}, &ctx->pe_b);
+    rc = rc || up("patch_embed.norm.weight", {C}, &ctx->pe_nw);
+    rc = rc || up("patch_embed.norm.bias", {C}, &ctx->pe_nb);
+    rc = rc || up("norm.weight", {C}, &ctx->norm_w);
+    rc = rc || up("norm.bias", {C}, &ctx->norm_b);
+    rc = rc || upconv("conv_after_body.weight", C, C, &ctx->cab_w, nullptr);
+    rc = rc || up("conv_after_body.bias", {C}, &ctx->cab_b);
+
+    // cpb scratch: the [heads][(2w-1)^2] MLP output before the gather
+    float *cpb_tab = nullptr;
+    if (!rc) rc = ctx->alloc(ctx->weight_allocs, (size_t)NH * (2 * win - 1) * (2 * win - 1),
+                             &cpb_tab, "cpb table");
+
+    ctx->stages.resize(A.n_stages);
+    for (int s = 0; !rc && s < A.n_stages; ++s) {
+        StageW &st = ctx->stages[s];
+        const std::string sp = "layers." + std::to_string(s) + ".";
+        rc = rc || upconv(sp + "conv.weight", C, C, &st.conv_w, nullptr);
+        rc = rc || up(sp + "conv.bias", {C}, &st.conv_b);
+        rc = rc || up(sp + "patch_embed.proj.weight", {C, C, 1, 1}, &st.pe_w);
+        rc = rc || up(sp + "patch_embed.proj.bias", {C}, &st.pe_b);
+        st.blocks.resize(A.depths[s]);
+        for (int b = 0; !rc && b < A.depths[s]; ++b) {
+            BlockW &bw = st.blocks[b];
+            const std::string p = sp + "residual_group.blocks." + std::to_string(b) + ".";
+            const s2s_tensor *wq, *wk_, *wv, *qb, *vb;
+            rc = rc || ts.get(p + "attn.qkv.wq", {C, C}, &wq);
+            rc = rc || ts.get(p + "attn.qkv.wk", {C, C}, &wk_);
+            rc = rc || ts.get(p + "attn.qkv.wv", {C, C}, &wv);
+            rc = rc || ts.get(p + "attn.qkv.q_bias", {C}, &qb);
+            rc = rc || ts.get(p + "attn.qkv.v_bias", {C}, &vb);
+            if (rc) break;
+            // the fused [3C][C] projection and its [q_bias | 0 | v_bias] bias
+            // (reference tools/convert.py:122-138; k has no bias)
+            std::vector<float> wqkv((size_t)3 * C * C), bqkv((size_t)3 * C, 0.f);
+            std::copy(wq->data, wq->data + (size_t)C * C, wqkv.begin());
+            std::copy(wk_->data, wk_->data + (size_t)C * C, wqkv.begin() + (size_t)C * C);
+            std::copy(wv->data, wv->data + (size_t)C * C, wqkv.begin() + (size_t)2 * C * C);
+            std::copy(qb->data, qb->data + C, bqkv.begin());
+            std::copy(vb->data, vb->data + C, bqkv.begin() + 2 * C);
+            rc = rc || ctx->upload(wqkv, &bw.wqkv) || ctx->upload(bqkv, &bw.bqkv);
+            const s2s_tensor *lsx;
+            rc = rc || ts.get(p + "attn.logit_scale", {NH, 1, 1}, &lsx);
+            if (rc) break;
+            rc = ctx->upload(vec_of(lsx, NH), &bw.ls);
+            rc = rc || up(p + "attn.proj.weight", {C, C}, &bw.wproj);
+            rc = rc || up(p + "attn.proj.bias", {C}, &bw.bproj);
+            rc = rc || up(p + "norm1.weight", {C}, &bw.n1w);
+            rc = rc || up(p + "norm1.bias", {C}, &bw.n1b);
+            rc = rc || up(p + "norm2.weight", {C}, &bw.n2w);
+            rc = rc || up(p + "norm2.bias", {C}, &bw.n2b);
+            rc = rc || up(p + "mlp.fc1.weight", {H2, C}, &bw.w1);
+            rc = rc || up(p + "mlp.fc1.bias", {H2}, &bw.b1);
+            rc = rc || up(p + "mlp.fc2.weight", {C, H2}, &bw.w2);
+            rc = rc || up(p + "mlp.fc2.bias", {C}, &bw.b2);
+            if (rc) break;
+            // The bias table. From the MLP when the set carries it (computed on
+            // the device: 16*sigmoid of Linear-ReLU-Linear on the log-spaced
+            // coordinates, gathered); otherwise from the converter's cpb_pre.
+            rc = ctx->alloc(ctx->weight_allocs, (size_t)NH * n * n, &bw.cpbt, "cpb");
+            if (rc) break;
+            ctx->uploaded += (uint64_t)NH * n * n * sizeof(float);
+            const s2s_tensor *m0 = ts.find(p + "attn.cpb_mlp.0.weight");
+            if (m0) {
+                const s2s_tensor *w0, *b0, *w2;
+                rc = rc || ts.get(p + "attn.cpb_mlp.0.weight", {512, 2}, &w0);
+                rc = rc || ts.get(p + "attn.cpb_mlp.0.bias", {512}, &b0);
+                rc = rc || ts.get(p + "attn.cpb_mlp.2.weight", {NH, 512}, &w2);
+                if (rc) break;
+                float *dw0, *db0, *dw2;
+                std::vector<void *> tmpl;
+                rc = ctx->alloc(tmpl, 1024, &dw0, "cpb w0") || ctx->alloc(tmpl, 512, &db0, "cpb b0") ||
+                     ctx->alloc(tmpl, (size_t)NH * 512, &dw2, "cpb w2");
+                if (!rc) {
+                    hipError_t le = hipMemcpy(dw0, w0->data, 1024 * 4, hipMemcpyHostToDevice);
+                    if (le == hipSuccess)
+                        le = hipMemcpy(db0, b0->data, 512 * 4, hipMemcpyHostToDevice);
+                    if (le == hipSuccess)
+                        le = hipMemcpy(dw2, w2->data, (size_t)NH * 512 * 4, hipMemcpyHostToDevice);
+                    if (le == hipSuccess)
+                        le = launch_cpb(dw0, db0, dw2, cpb_tab, bw.cpbt, win, NH, ctx->stream);
+                    if (le == hipSuccess) le = hipStreamSynchronize(ctx->stream);
+                    if (le != hipSuccess) rc = fail(hip_msg("cpb table", le));
+                }
+                free_list(tmpl);
+            } else {
+                const s2s_tensor *cp;
+                rc = ts.get(p + "attn.cpb_pre", {(int64_t)n * n, NH}, &cp);
+                if (rc) break;
+                std::vector<float> t((size_t)NH * n * n);
+                for (int q = 0; q < n; ++q)
+                    for (int k = 0; k < n; ++k)
+                        for (int hh = 0; hh < NH; ++hh)
+                            t[((size_t)hh * n + q) * n + k] = cp->data[((size_t)q * n + k) * NH + hh];
+                if (hipMemcpy(bw.cpbt, t.data(), t.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+                    rc = fail("hipMemcpy(cpb) failed");
+            }
+        }
+    }
+
+    if (!rc && (A.upsampler == S2S_PIXELSHUFFLE || A.upsampler == S2S_PIXELSHUFFLE_AUX)) {
+        const s2s_tensor *cb = ts.find("conv_before_upsample.0.weight");
+        if (!cb || cb->ndim != 4 || cb->shape[0] <= 0 || cb->shape[0] % 4 != 0)
+            rc = fail("weight `conv_before_upsample.0.weight` is missing or not [feat][C][3][3] "
+                      "with feat a multiple of 4");
+        if (!rc) rc = ts.get("conv_before_upsample.0.weight", {cb->shape[0], C, 3, 3}, &cb);
+        if (!rc) {
+            const int F = (int)cb->shape[0];
+            ctx->feat = F;
+            int oct = 0;
+            while ((1 << oct) < A.scale) ++oct;
+            ctx->octaves = oct;
+            rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
+            rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
+            std::vector<int> perm = shuffle_perm(F);
+            for (int o = 0; !rc && o < oct; ++o) {
+                const s2s_tensor *uw, *ub;
+                const std::string base = "upsample." + std::to_string(2 * o);
+                rc = rc || ts.get(base + ".weight", {4 * F, F, 3, 3}, &uw);
+                rc = rc || ts.get(base + ".bias", {4 * F}, &ub);
+                if (rc) break;
+                float *dw, *db;
+                std::vector<float> bb(4 * F);
+                for (int co = 0; co < 4 * F; ++co) bb[perm[co]] = ub->data[co];
+                rc = ctx->upload(conv_relayout(uw->data, 4 * F, F, &perm), &dw) || ctx->upload(bb, &db);
+                ctx->up_w.push_back(dw);
+                ctx->up_b.push_back(db);
+            }
+            const s2s_tensor *lw;
+            rc = rc || ts.get("conv_last.weight", {3, F, 3, 3}, &lw);
+            if (!rc) {
+                std::vector<float> t((size_t)9 * F * 3);
+                for (int co = 0; co < 3; ++co)
+                    for (int ci = 0; ci < F; ++ci)
+                        for (int tap = 0; tap < 9; ++tap)
+                            t[((size_t)tap * F + ci) * 3 + co] = lw->data[((size_t)co * F + ci) * 9 + tap];
+                rc = ctx->upload(t, &ctx->last_w);
+            }
+            rc = rc || up("conv_last.bias", {3}, &ctx->last_b);
+        }
+    }
+    if (rc) {
+        std::string keep = g_err;
+        delete ctx;
+        g_err = keep;
+        return -1;
+    }
+    *out = ctx;
+    return 0;
+}
+
+void s2s_destroy(s2s_ctx *ctx) { delete ctx; }
+
+uint64_t s2s_uploaded_bytes(const s2s_ctx *ctx) { return ctx ? ctx->uploaded : 0; }
+
+int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out) {
+    if (!ctx) return fail("null context");
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    return ctx->forward_device(h, w, d_in, d_out);
+}
+
+int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out) {
+    if (!ctx || !in_adjusted || !out) return fail("s2s_forward: null argument");
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    if (h < ctx->arch.window || w < ctx->arch.window) return ctx->forward_device(h, w, nullptr, nullptr);
+    if (ctx->plan_image(h, w)) return -1;
+    const int s = ctx->arch.scale;
+    const size_t nin = (size_t)3 * h * w, nout = (size_t)3 * h * s * w * s;
+    HIPCHK("hipMemcpyAsync(input)", hipMemcpyAsync(ctx->in_dev, in_adjusted, nin * 4,
+                                                   hipMemcpyHostToDevice, ctx->stream));
+    if (ctx->forward_device(h, w, ctx->in_dev, ctx->out_dev)) return -1;
+    HIPCHK("hipMemcpyAsync(output)", hipMemcpyAsync(out, ctx->out_dev, nout * 4,
+                                                    hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK("hipStreamSynchronize", hipStreamSynchronize(ctx->stream));
+    ctx->aux_host.clear();
+    return 0;
+}
+
+int s2s_aux(s2s_ctx *ctx, const float **ptr, size_t *n) {
+    if (!ctx || !ptr || !n) return fail("s2s_aux: null argument");
+    if (ctx->aux_host.empty()) {
+        *ptr = nullptr;
+        *n = 0;
+    } else {
+        *ptr = ctx->aux_host.data();
+        *n = ctx->aux_host.size();
+    }
+    return 0;
+}
+
+int s2s_rstb_device(s2s_ctx *ctx, int stage, int hp, int wp, const float *d_in, float *d_out) {
+    if (!ctx) return fail("null context");
+    if (stage < 0 || stage >= ctx->arch.n_stages) return fail("stage out of range");
+    if (hp % ctx->arch.window || wp % ctx->arch.window || hp <= 0 || wp <= 0)
+        return fail("the plane must be a positive multiple of the window in both directions");
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    if (ctx->plan_body(hp, wp)) return -1;
+    return ctx->stage_fwd(stage, hp, wp, d_in, d_out);
+}
+
+int s2s_device_info(char *name, size_t name_cap, char *arch, size_t arch_cap) {
+    int dev = 0;
+    HIPCHK("hipGetDevice", hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    HIPCHK("hipGetDeviceProperties", hipGetDeviceProperties(&p, dev));
+    if (name && name_cap) snprintf(name, name_cap, "%s", p.name);
+    if (arch && arch_cap) snprintf(arch, arch_cap, "%s", p.gcnArchName);
+    return 0;
+}
+
+int s2s_vram(uint64_t *free_bytes, uint64_t *total_bytes) {
+    size_t f = 0, t = 0;
+    HIPCHK("hipMemGetInfo", hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return 0;
+}
+
+int s2s_sync(void) {
+    HIPCHK("hipDeviceSynchronize", hipDeviceSynchronize());
+    return 0;
+}
+
+void *s2s_stream(s2s_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int s2s_profile_enable(s2s_ctx *ctx, int on) {
+    if (!ctx) return fail("null context");
+    if (!on && ctx->drain()) return -1;
+    ctx->prof = on != 0;
+    return 0;
+}
+
+int s2s_profile_reset(s2s_ctx *ctx) {
+    if (!ctx) return fail("null context");
+    if (ctx->drain()) return -1;
+    ctx->rows.clear();
+    return 0;
+}
+
+int s2s_profile_report(s2s_ctx *ctx, float wall_ms) {
+    if (!ctx) return fail("null context");
+    if (ctx->drain()) return -1;
+    std::vector<std::pair<ProfKey, ProfRow>> v(ctx->rows.begin(), ctx->rows.end());
+    std::sort(v.begin(), v.end(), [](const auto &a, const auto &b) { return a.second.ms > b.second.ms; });
+    double total = 0;
+    for (auto &r : v) total += r.second.ms;
+    fprintf(stderr, "gpu profile (%zu rows, %.3f ms in kernels, wall %.3f ms):\n", v.size(), total,
+            wall_ms);
+    fprintf(stderr, "  %-24s %-16s %-12s %7s %11s %10s %6s\n", "kernel", "grid", "block", "calls",
+            "total ms", "avg ms", "%wall");
+    for (auto &r : v) {
+        char g[48], b[48];
+        snprintf(g, sizeof g, "%u,%u,%u", r.first.g[0], r.first.g[1], r.first.g[2]);
+        snprintf(b, sizeof b, "%u,%u,%u", r.first.b[0], r.first.b[1], r.first.b[2]);
+        fprintf(stderr, "  %-24s %-16s %-12s %7d %11.3f %10.4f %6.1f\n", r.first.name.c_str(), g, b,
+                r.second.calls, r.second.ms, r.second.ms / r.second.calls,
+                wall_ms > 0 ? 100.0 * r.second.ms / wall_ms : 0.0);
+    }
+    return 0;
+}
+
+int s2s_profile_query(s2s_ctx *ctx, const char *kernel, double *total_ms, int *launches) {
+    if (!ctx || !kernel) return fail("null argument");
+    if (ctx->drain()) return -1;
+    double ms = 0;
+    int calls = 0;
+    for (auto &r : ctx->rows)
+        if (r.first.name == kernel) {
+            ms += r.second.ms;
+            calls += r.second.calls;
+        }
+    if (total_ms) *total_ms = ms;
+    if (launches) *launches = calls;
+    return 0;
+}
+
+}  // extern "C"

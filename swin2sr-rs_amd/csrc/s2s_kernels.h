@@ -1,0 +1,67 @@
+// s2s_kernels.h - argument blocks and launchers of the gfx950 kernels
+// (s2s_kernels.hip). Host code in s2s_api.cpp plans buffers and calls these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+enum { ALOAD_ROWS = 0, ALOAD_IM2COL = 1 };
+enum {
+    EPI_STORE = 0,   // out = acc + bias
+    EPI_GELU = 1,    // out = gelu_erf(acc + bias)
+    EPI_RES = 2,     // out = acc + bias + res
+    EPI_LN = 3,      // out = LayerNorm(acc + bias)             (N <= 192)
+    EPI_LN_RES = 4,  // out = res + LayerNorm(acc + bias)       (N <= 192)
+    EPI_LRELU = 5,   // out = leaky_relu(acc + bias, slope)
+    EPI_SHUFFLE = 6  // pixel_shuffle(2) store into a 2H x 2W channel-last plane
+};
+
+struct GemmArgs {
+    // A operand: ALOAD_ROWS -> A[m*lda + k]; ALOAD_IM2COL -> the 3x3 im2col
+    // view of the channel-last plane A[H*W][cin], k = tap*cin + ci.
+    const float *A;
+    int lda;
+    int H, W, cin;
+    // B operand: weight rows B[n*ldb + k].
+    const float *B;
+    int ldb;
+    const float *bias;  // [N] or null
+    float *out;
+    int ldo;
+    const float *res;  // residual [M][ldr]
+    int ldr;
+    const float *ln_w, *ln_b;
+    float slope;
+    int feat;  // EPI_SHUFFLE: output channels (N = 4*feat)
+    int M, N, K;
+};
+
+struct AttnArgs {
+    const float *qkv;          // [hp*wp][3c] plane order: q | k | v
+    const float *cpbt;         // [heads][64][64]
+    const float *logit_scale;  // [heads]
+    float *out;                // [hp*wp][c]
+    int hp, wp, nww, nw;
+    int heads, head_dim, c;
+    int shift;
+};
+
+hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st);
+void gemm_grid(const GemmArgs &g, int epi, unsigned *gx, unsigned *gy);
+const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi);
+hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out);
+hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
+                            hipStream_t st);
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,
+                            float *out, int P, int C, hipStream_t st);
+hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
+                                   float *out, int H, int W, int feat, int oh, int ow,
+                                   float img_range, const float *mean, hipStream_t st);
+hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *tab, float *cpbt,
+                      int win, int heads, hipStream_t st);
+hipError_t launch_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *reg,
+                             hipStream_t st);
+
+// The ABI's thread-local error slot (defined in s2s_api.cpp): records `msg`
+// for s2s_last_error() and returns -1. Internal to the library.
+__attribute__((visibility("hidden"))) int s2s_fail(const char *msg);

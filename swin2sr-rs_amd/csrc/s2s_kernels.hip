@@ -1,0 +1,752 @@
+// s2s_kernels.hip - the swin2sr hot path as CDNA4 (gfx950) kernels.
+//
+// ACTIVATIONS ARE CHANNEL-LAST: a plane is `[hp*wp][c]`, one token per pixel,
+// row-major in the plane. That one choice removes the reference's window
+// gather and scatter copies (reference cuda/swin2sr.cu:99-154): every per-token
+// op (the projections, LayerNorm, the MLP, the residuals) runs on the plane in
+// raster order, and only window attention needs the cyclic-shift window map,
+// which it evaluates in registers when it reads its 64 tokens and again when it
+// writes them back (reference src/plan.rs:72-108).
+//
+// Dense contractions run on `v_mfma_f32_32x32x2f32` (fp32 in, fp32 accumulate):
+//   - k_gemm: token GEMMs (qkv, proj, fc1, fc2, the 1x1 convs) and the 3x3
+//     convolutions as implicit GEMMs (im2col done by the operand loader), with
+//     the elementwise work fused into the epilogue: bias, erf-GELU, residual
+//     add, LeakyReLU, LayerNorm (+ residual) over the full 180-wide row, and the
+//     pixel-shuffle store of the head's octaves.
+//   - k_attention: one wavefront per (window, head) computes S^T = K Q^T and
+//     O^T = V^T P^T on MFMA with the softmax in registers between them.
+// Memory-bound leftovers (input padding, the standalone final LayerNorm and
+// the 64->3 conv_last with the crop/denormalisation) are plain streaming
+// kernels.
+//
+// MFMA 32x32x2 f32 lane layout (checked on the device): lane l supplies
+// A[l%32][l/32] and B[l/32][l%32]; accumulator register r of lane l holds
+// D[8*(r/4) + 4*(l/32) + r%4][l%32].
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "s2s_kernels.h"
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+#define MFMA32(a, b, c) __builtin_amdgcn_mfma_f32_32x32x2f32((a), (b), (c), 0, 0, 0)
+
+__device__ __forceinline__ float gelu_erf(float v) {
+    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+// ---------------------------------------------------------------------------
+// k_gemm: out[m][n] = epi( sum_k A[m][k] * B[n][k] + bias[n] )
+//
+// A rows are tokens: either a plain row-major matrix (ALOAD_ROWS) or the 3x3
+// im2col view of a channel-last plane (ALOAD_IM2COL: k = tap*cin + ci, taps
+// outside the plane read zero, which is the reference's zero padding).
+// B is a weight in torch layout [n][k] (k contiguous).
+//
+// A workgroup computes an MT x NT tile with 4 wavefronts laid out WM x WN;
+// each wave owns (MT/WM) x (NT/WN) as 32x32 MFMA tiles. K is walked in chunks
+// of 32 staged through LDS (row stride 36 floats: rows land 36 banks apart, so
+// the float2 operand reads of a wave are conflict-free), with the next chunk's
+// global loads in flight while the current chunk is multiplied.
+//
+// Within a chunk, lane half h (= lane/32) reads k = 4kk + 2h + {0,1} as one
+// float2 and feeds the two halves to two MFMAs: the A and B operands of a lane
+// half always name the same k, so the pair of MFMAs sums over all four k of
+// the group. (This permutes the reduction order, not the result.)
+// ---------------------------------------------------------------------------
+
+#define KC 32
+#define LDS_S 36
+
+template <int ALOAD>
+__device__ __forceinline__ float4 load_a4(const GemmArgs &g, int m, int k) {
+    float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m >= g.M || k >= g.K) return z;
+    if (ALOAD == ALOAD_ROWS) {
+        return *reinterpret_cast<const float4 *>(g.A + (size_t)m * g.lda + k);
+    } else {
+        const int tap = k / g.cin;
+        const int ci = k - tap * g.cin;
+        const int y = m / g.W;
+        const int x = m - y * g.W;
+        const int sy = y + tap / 3 - 1;
+        const int sx = x + tap % 3 - 1;
+        if (sy < 0 || sy >= g.H || sx < 0 || sx >= g.W) return z;
+        return *reinterpret_cast<const float4 *>(g.A + ((size_t)sy * g.W + sx) * g.cin + ci);
+    }
+}
+
+__device__ __forceinline__ float4 load_b4(const GemmArgs &g, int n, int k) {
+    if (n >= g.N || k >= g.K) return make_float4(0.f, 0.f, 0.f, 0.f);
+    return *reinterpret_cast<const float4 *>(g.B + (size_t)n * g.ldb + k);
+}
+
+template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    static_assert(WM * WN == 4, "four wavefronts");
+    constexpr int WTM = MT / WM / 32;
+    constexpr int WTN = NT / WN / 32;
+    static_assert(WTM * WM * 32 == MT && WTN * WN * 32 == NT, "tile shape");
+    constexpr int AV = MT * (KC / 4) / 256;
+    constexpr int BV = NT * (KC / 4) / 256;
+    static_assert(AV * 256 == MT * (KC / 4) && BV * 256 == NT * (KC / 4), "loader shape");
+
+    __shared__ float As[MT * LDS_S];
+    __shared__ float Bs[NT * LDS_S];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    const int m0 = blockIdx.x * MT;
+    const int n0 = blockIdx.y * NT;
+    const int lr = lane & 31;
+    const int lh = lane >> 5;
+
+    f16v acc[WTM][WTN];
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    float4 ra[AV], rb[BV];
+    const int nk = (g.K + KC - 1) / KC;
+
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < AV; ++i) {
+            const int idx = tid + i * 256;
+            ra[i] = load_a4<ALOAD>(g, m0 + (idx >> 3), k0 + (idx & 7) * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            const int idx = tid + i * 256;
+            rb[i] = load_b4(g, n0 + (idx >> 3), k0 + (idx & 7) * 4);
+        }
+    };
+
+    load_chunk(0);
+    for (int kc = 0; kc < nk; ++kc) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < AV; ++i) {
+            const int idx = tid + i * 256;
+            *reinterpret_cast<float4 *>(&As[(idx >> 3) * LDS_S + (idx & 7) * 4]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            const int idx = tid + i * 256;
+            *reinterpret_cast<float4 *>(&Bs[(idx >> 3) * LDS_S + (idx & 7) * 4]) = rb[i];
+        }
+        __syncthreads();
+        if (kc + 1 < nk) load_chunk((kc + 1) * KC);
+#pragma unroll
+        for (int kk = 0; kk < KC / 4; ++kk) {
+            float2 a[WTM], b[WTN];
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+                a[i] = *reinterpret_cast<const float2 *>(
+                    &As[((wm * WTM + i) * 32 + lr) * LDS_S + kk * 4 + lh * 2]);
+#pragma unroll
+            for (int j = 0; j < WTN; ++j)
+                b[j] = *reinterpret_cast<const float2 *>(
+                    &Bs[((wn * WTN + j) * 32 + lr) * LDS_S + kk * 4 + lh * 2]);
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) acc[i][j] = MFMA32(a[i].x, b[j].x, acc[i][j]);
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) acc[i][j] = MFMA32(a[i].y, b[j].y, acc[i][j]);
+        }
+    }
+
+    // ---- epilogue ----------------------------------------------------------
+    if (EPI == EPI_LN || EPI == EPI_LN_RES) {
+        // The whole row is inside this workgroup (host guarantees N <= NT and
+        // one column block). Per-row partial sums: over this lane's WTN
+        // columns, then across the 32 lanes of the half, then across the WN
+        // waves through LDS. Single-pass statistics, as the reference's
+        // channel LayerNorm computes them.
+        __syncthreads();
+        float *red = As;  // [WN][MT][2]
+        float bias_v[WTN], lnw[WTN], lnb[WTN];
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = n0 + (wn * WTN + j) * 32 + lr;
+            const bool ok = n < g.N;
+            bias_v[j] = (ok && g.bias) ? g.bias[n] : 0.f;
+            lnw[j] = ok ? g.ln_w[n] : 0.f;
+            lnb[j] = ok ? g.ln_b[n] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) {
+                    const int n = n0 + (wn * WTN + j) * 32 + lr;
+                    const float v = (n < g.N) ? acc[i][j][r] + bias_v[j] : 0.f;
+                    acc[i][j][r] = v;
+                    s1 += v;
+                    s2 += v * v;
+                }
+#pragma unroll
+                for (int o = 16; o >= 1; o >>= 1) {
+                    s1 += __shfl_xor(s1, o, 64);
+                    s2 += __shfl_xor(s2, o, 64);
+                }
+                const int rl = (wm * WTM + i) * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (lr == 0) {
+                    red[(wn * MT + rl) * 2 + 0] = s1;
+                    red[(wn * MT + rl) * 2 + 1] = s2;
+                }
+            }
+        }
+        __syncthreads();
+        const float invn = 1.0f / (float)g.N;
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = (wm * WTM + i) * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+                for (int q = 0; q < WN; ++q) {
+                    s1 += red[(q * MT + rl) * 2 + 0];
+                    s2 += red[(q * MT + rl) * 2 + 1];
+                }
+                const float mean = s1 * invn;
+                float var = s2 * invn - mean * mean;
+                var = var > 0.f ? var : 0.f;
+                const float rstd = 1.0f / sqrtf(var + 1e-5f);
+                const int m = m0 + rl;
+                if (m >= g.M) continue;
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) {
+                    const int n = n0 + (wn * WTN + j) * 32 + lr;
+                    if (n >= g.N) continue;
+                    float y = (acc[i][j][r] - mean) * rstd * lnw[j] + lnb[j];
+                    if (EPI == EPI_LN_RES) y += g.res[(size_t)m * g.ldr + n];
+                    g.out[(size_t)m * g.ldo + n] = y;
+                }
+            }
+        }
+        return;
+    }
+
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+        const int n = n0 + (wn * WTN + j) * 32 + lr;
+        if (n >= g.N) continue;
+        const float bv = g.bias ? g.bias[n] : 0.f;
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + (wm * WTM + i) * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (m >= g.M) continue;
+                float v = acc[i][j][r] + bv;
+                if (EPI == EPI_GELU) v = gelu_erf(v);
+                if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
+                if (EPI == EPI_RES) v += g.res[(size_t)m * g.ldr + n];
+                if (EPI == EPI_SHUFFLE) {
+                    // n is the permuted output channel (2dy+dx)*feat + ch; m a
+                    // pixel of the H x W plane; the store lands in the 2H x 2W
+                    // channel-last plane (pixel_shuffle(2)).
+                    const int q = n / g.feat;
+                    const int ch = n - q * g.feat;
+                    const int y = m / g.W;
+                    const int x = m - y * g.W;
+                    const size_t op = (size_t)(2 * y + (q >> 1)) * (2 * g.W) + (2 * x + (q & 1));
+                    g.out[op * g.feat + ch] = v;
+                } else {
+                    g.out[(size_t)m * g.ldo + n] = v;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The shifted-window maps (reference src/plan.rs:72-108), shared by the
+// attention kernel and the map test kernel so the tested code is the code
+// that runs. Window side 8.
+//
+// win_pixel: window (wh, ww), token t = 8i + j reads plane pixel
+//   ((8wh + i + shift) mod hp, (8ww + j + shift) mod wp)  - torch.roll(-shift).
+// win_band:  the mask band of a token on the ROLLED (unwrapped) coordinate a:
+//   0 if a + 8 < len, 1 if a + shift < len, else 2     - calculate_mask's slices.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int win_pixel(int wh, int ww, int t, int shift, int hp, int wp) {
+    int y = wh * 8 + (t >> 3) + shift;
+    int x = ww * 8 + (t & 7) + shift;
+    if (y >= hp) y -= hp;  // shift < 8 <= hp: one subtraction is the modulo
+    if (x >= wp) x -= wp;
+    return y * wp + x;
+}
+
+__device__ __forceinline__ int win_band(int a, int len, int shift) {
+    return (a + 8 < len) ? 0 : ((a + shift < len) ? 1 : 2);
+}
+
+__global__ void k_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *reg) {
+    const int nww = wp / 8, nw = (hp / 8) * nww;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nw * 64) return;
+    const int wi = i >> 6, t = i & 63;
+    const int wh = wi / nww, ww = wi - (wi / nww) * nww;
+    const int p = win_pixel(wh, ww, t, shift, hp, wp);
+    yx[2 * i] = p / wp;
+    yx[2 * i + 1] = p - (p / wp) * wp;
+    reg[2 * i] = (uint8_t)win_band(wh * 8 + (t >> 3), hp, shift);
+    reg[2 * i + 1] = (uint8_t)win_band(ww * 8 + (t & 7), wp, shift);
+}
+
+// ---------------------------------------------------------------------------
+// k_attention: scaled-cosine window attention, one wavefront per (window, head).
+//
+// reference cpu::attention (src/cpu.rs:1244-1402) / ss_attention
+// (cuda/swin2sr.cu:182-323): s = (q.k)/(|q||k|) * exp(min(ls, ln 100))
+// + cpb[h][q][k] - 100*[band(q) != band(k)] (shifted blocks only); max-
+// subtracted softmax over the 64 keys; out = sum_k p_k v_k. No 1/sqrt(d).
+//
+// The 64 tokens of window wi are read straight from the channel-last qkv
+// plane [P][3c] at plane pixel index(wi, t, shift) (the roll is the modulo),
+// and the output rows go back to the same pixels: the partition and its
+// reverse are index math, never copies.
+//
+// Lane l = (r = l%32, hh = l/32). The wave holds, per 32-token tile, q and k
+// head rows split in d halves: lane (r, hh) keeps d = 16*hh .. 16*hh+15 of
+// token 32*tile + r (zero past head_dim), pre-scaled by exp(ls)/|q| and 1/|k|.
+//   S^T = K Q^T : A = K (rows = keys), B = Q^T (cols = queries); the MFMA
+//                 k-step j of lane half hh is d = 16*hh + j.
+//   softmax    : a query is a lane column; its 64 keys are 2 tiles x 16
+//                registers x the two lane halves -> one xor-32 exchange.
+//   O^T = V^T P^T : B = P^T straight from the S^T accumulators (register
+//                 4a+b of tile kt is key 32kt + 8a + 4hh + b), A = V^T loaded
+//                 per key row (lane r reads d = r).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wave_id >= g.nw * g.heads) return;
+    const int wi = wave_id / g.heads;
+    const int h = wave_id - wi * g.heads;
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31;
+    const int hh = lane >> 5;
+    const int wh = wi / g.nww;
+    const int ww = wi - wh * g.nww;
+    const int shift = g.shift;
+    const int hd = g.head_dim;
+    const size_t ld = (size_t)3 * g.c;
+
+    auto pix = [&](int t) -> int { return win_pixel(wh, ww, t, shift, g.hp, g.wp); };
+
+    const float ls = __expf(fminf(g.logit_scale[h], 4.605170185988092f));
+
+    float qv[2][16], kv[2][16];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+        const float *row = g.qkv + (size_t)pix(32 * t2 + r) * ld + h * hd;
+        float qs = 0.f, ks = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int d = 16 * hh + j;
+            const float a = d < hd ? row[d] : 0.f;
+            const float b = d < hd ? row[g.c + d] : 0.f;
+            qv[t2][j] = a;
+            kv[t2][j] = b;
+            qs += a * a;
+            ks += b * b;
+        }
+        qs += __shfl_xor(qs, 32, 64);
+        ks += __shfl_xor(ks, 32, 64);
+        const float qn = fmaxf(sqrtf(qs), 1e-12f);
+        const float kn = fmaxf(sqrtf(ks), 1e-12f);
+        const float qsc = ls / qn;
+        const float ksc = 1.0f / kn;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            qv[t2][j] *= qsc;
+            kv[t2][j] *= ksc;
+        }
+    }
+
+    f16v s[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[a][b][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) s[kt][qt] = MFMA32(kv[kt][j], qv[qt][j], s[kt][qt]);
+
+    // Bias table [head][query][key] and the shift mask. A key's band only
+    // depends on its row (t/8) and column (t%8) inside the window.
+    const float *cpb = g.cpbt + (size_t)h * 64 * 64;
+    int bq_y[2], bq_x[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int t = 32 * qt + r;
+        bq_y[qt] = win_band(wh * 8 + (t >> 3), g.hp, shift);
+        bq_x[qt] = win_band(ww * 8 + (t & 7), g.wp, shift);
+    }
+    float inv[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qtok = 32 * qt + r;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const int k0 = 32 * kt + 8 * a + 4 * hh;
+                const float4 bias4 = *reinterpret_cast<const float4 *>(cpb + qtok * 64 + k0);
+                const float bb[4] = {bias4.x, bias4.y, bias4.z, bias4.w};
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int key = k0 + b;
+                    float v = s[kt][qt][4 * a + b] + bb[b];
+                    if (shift) {
+                        const int by = win_band(wh * 8 + (key >> 3), g.hp, shift);
+                        const int bx = win_band(ww * 8 + (key & 7), g.wp, shift);
+                        if (by != bq_y[qt] || bx != bq_x[qt]) v -= 100.f;
+                    }
+                    s[kt][qt][4 * a + b] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float sum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = __expf(s[kt][qt][e] - mx);
+                s[kt][qt][e] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 32, 64);
+        inv[qt] = 1.0f / sum;
+    }
+
+    f16v o[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[qt][e] = 0.f;
+    const float *vbase = g.qkv + 2 * g.c + h * hd + r;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int key = 32 * kt + 8 * a + 4 * hh + b;
+                const float v = (r < hd) ? vbase[(size_t)pix(key) * ld] : 0.f;
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) o[qt] = MFMA32(v, s[kt][qt][4 * a + b], o[qt]);
+            }
+
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        float *orow = g.out + (size_t)pix(32 * qt + r) * g.c + h * hd;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
+            if (d < hd) orow[d] = o[qt][e] * inv[qt];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming kernels.
+// ---------------------------------------------------------------------------
+
+// reference src/plan.rs:116-140 (pad_reflect) fused with the layout change:
+// [3][h][w] -> channel-last [hp*wp][4] (channel 3 = 0, so the conv_first
+// operand loads are float4). The mirror is of the whole plane: sy = 2h-1-y.
+__global__ void k_pad_input(const float *__restrict__ in, float *__restrict__ out, int h, int w,
+                            int hp, int wp) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hp * wp) return;
+    const int y = i / wp, x = i - (i / wp) * wp;
+    const int sy = y < h ? y : 2 * h - 1 - min(y, 2 * h - 1);
+    const int sx = x < w ? x : 2 * w - 1 - min(x, 2 * w - 1);
+    const size_t hw = (size_t)h * w;
+    const size_t s = (size_t)sy * w + sx;
+    *reinterpret_cast<float4 *>(out + (size_t)i * 4) =
+        make_float4(in[s], in[hw + s], in[2 * hw + s], 0.f);
+}
+
+// Channel LayerNorm over a channel-last plane (reference cpu::channel_layer_norm,
+// src/cpu.rs:1019-1073, single-pass statistics): 16 lanes per pixel, float4.
+// Optional residual: out = res + LN(x).
+__global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x,
+                                                   const float *__restrict__ w,
+                                                   const float *__restrict__ b,
+                                                   const float *__restrict__ res,
+                                                   float *__restrict__ out, int P, int C) {
+    const int pix = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int l = threadIdx.x & 15;
+    const int nv = C >> 2;
+    float4 v[4];
+    float s1 = 0.f, s2 = 0.f;
+    const bool live = pix < P;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = l + 16 * i;
+        if (live && q < nv) {
+            v[i] = *reinterpret_cast<const float4 *>(x + (size_t)pix * C + 4 * q);
+            s1 += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+            s2 += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+        } else {
+            v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+        s1 += __shfl_xor(s1, o, 16);
+        s2 += __shfl_xor(s2, o, 16);
+    }
+    if (!live) return;
+    const float mean = s1 / (float)C;
+    float var = s2 / (float)C - mean * mean;
+    var = var > 0.f ? var : 0.f;
+    const float rstd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = l + 16 * i;
+        if (q >= nv) continue;
+        const float4 ww = *reinterpret_cast<const float4 *>(w + 4 * q);
+        const float4 bb = *reinterpret_cast<const float4 *>(b + 4 * q);
+        float4 y;
+        y.x = (v[i].x - mean) * rstd * ww.x + bb.x;
+        y.y = (v[i].y - mean) * rstd * ww.y + bb.y;
+        y.z = (v[i].z - mean) * rstd * ww.z + bb.z;
+        y.w = (v[i].w - mean) * rstd * ww.w + bb.w;
+        if (res) {
+            const float4 rr = *reinterpret_cast<const float4 *>(res + (size_t)pix * C + 4 * q);
+            y.x += rr.x;
+            y.y += rr.y;
+            y.z += rr.z;
+            y.w += rr.w;
+        }
+        *reinterpret_cast<float4 *>(out + (size_t)pix * C + 4 * q) = y;
+    }
+}
+
+// conv_last (feat -> 3, 3x3, zero pad) fused with the reference's host
+// epilogue cpu::finish (src/cpu.rs:1925-1941): y/img_range + mean, cropped to
+// the unpadded output, written planar [3][oh][ow]. One thread per kept pixel;
+// weights are read as wave-uniform (scalar) loads, layout [tap][ci][3].
+__global__ __launch_bounds__(256) void k_conv_last_finish(const float *__restrict__ in,
+                                                          const float *__restrict__ wt,
+                                                          const float *__restrict__ bias,
+                                                          float *__restrict__ out, int H, int W,
+                                                          int feat, int oh, int ow,
+                                                          float inv_range, float m0, float m1,
+                                                          float m2) {
+    const int x = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int y = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (x >= ow || y >= oh) return;
+    float a0 = bias[0], a1 = bias[1], a2 = bias[2];
+    for (int tap = 0; tap < 9; ++tap) {
+        const int sy = y + tap / 3 - 1, sx = x + tap % 3 - 1;
+        if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
+        const float *src = in + ((size_t)sy * W + sx) * feat;
+        const float *wk = wt + tap * feat * 3;
+        for (int ci = 0; ci < feat; ci += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + ci);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                a0 += wk[(ci + u) * 3 + 0] * vv[u];
+                a1 += wk[(ci + u) * 3 + 1] * vv[u];
+                a2 += wk[(ci + u) * 3 + 2] * vv[u];
+            }
+        }
+    }
+    const size_t plane = (size_t)oh * ow, o = (size_t)y * ow + x;
+    out[o] = a0 * inv_range + m0;
+    out[plane + o] = a1 * inv_range + m1;
+    out[2 * plane + o] = a2 * inv_range + m2;
+}
+
+// The continuous position bias table (reference tools/convert.py:141-167 and
+// network_swin2sr.py:101-136), built on the device from the cpb_mlp weights:
+// one workgroup per relative offset (dy, dx) in [-(win-1), win-1]^2, the
+// 512-wide hidden layer in LDS, then one lane per head. tab is [heads][side^2].
+__global__ __launch_bounds__(256) void k_cpb_mlp(const float *__restrict__ w0,
+                                                 const float *__restrict__ b0,
+                                                 const float *__restrict__ w2,
+                                                 float *__restrict__ tab, int win, int heads) {
+    __shared__ float hid[512];
+    const int side = 2 * win - 1;
+    const int e = blockIdx.x;
+    const int a = e / side, b = e - (e / side) * side;
+    float co[2] = {(float)(a - (win - 1)), (float)(b - (win - 1))};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        float v = co[k] / (float)(win - 1);
+        v = v * 8.0f;
+        const float sg = v > 0.f ? 1.f : (v < 0.f ? -1.f : 0.f);
+        co[k] = sg * log2f(fabsf(v) + 1.0f) / 3.0f;
+    }
+    for (int j = threadIdx.x; j < 512; j += blockDim.x) {
+        const float hv = co[0] * w0[j * 2] + co[1] * w0[j * 2 + 1] + b0[j];
+        hid[j] = hv > 0.f ? hv : 0.f;
+    }
+    __syncthreads();
+    // one wavefront per head: lanes stride the hidden layer, then reduce
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int hh = wave; hh < heads; hh += 4) {
+        float acc = 0.f;
+        for (int j = lane; j < 512; j += 64) acc += hid[j] * w2[hh * 512 + j];
+        for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (lane == 0) tab[hh * side * side + e] = acc;
+    }
+}
+
+// Gather the table to [heads][n][n] (query-major, key contiguous) through the
+// relative position index (yq-yk+win-1)*(2win-1) + (xq-xk+win-1), with 16*sigmoid.
+__global__ void k_cpb_gather(const float *__restrict__ tab, float *__restrict__ cpbt, int win,
+                             int heads) {
+    const int n = win * win, side = 2 * win - 1;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= heads * n * n) return;
+    const int h = i / (n * n), qk = i - h * n * n;
+    const int q = qk / n, k = qk - (qk / n) * n;
+    const int idx = ((q / win) - (k / win) + win - 1) * side + ((q % win) - (k % win) + win - 1);
+    const float v = tab[h * side * side + idx];
+    cpbt[i] = 16.0f / (1.0f + expf(-v));
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launchers (one per kernel family; the GEMM shapes are chosen here).
+// ---------------------------------------------------------------------------
+
+template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
+static hipError_t run_gemm_t(const GemmArgs &g, hipStream_t st) {
+    dim3 grid((g.M + MT - 1) / MT, (g.N + NT - 1) / NT);
+    hipLaunchKernelGGL((k_gemm<MT, NT, WM, WN, ALOAD, EPI>), grid, dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+
+template <int MT, int NT, int WM, int WN, int ALOAD>
+static hipError_t run_gemm_e(const GemmArgs &g, int epi, hipStream_t st) {
+    switch (epi) {
+    case EPI_STORE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_STORE>(g, st);
+    case EPI_GELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_GELU>(g, st);
+    case EPI_RES: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_RES>(g, st);
+    case EPI_LN: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN>(g, st);
+    case EPI_LN_RES: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN_RES>(g, st);
+    case EPI_LRELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
+    case EPI_SHUFFLE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_SHUFFLE>(g, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
+    (void)g;
+    static const char *names[2][7] = {
+        {"gemm_rows_store", "gemm_rows_gelu", "gemm_rows_res", "gemm_rows_ln", "gemm_rows_ln_res",
+         "gemm_rows_lrelu", "gemm_rows_shuffle"},
+        {"conv3x3_store", "conv3x3_gelu", "conv3x3_res", "conv3x3_ln", "conv3x3_ln_res",
+         "conv3x3_lrelu", "conv3x3_shuffle"}};
+    return names[aload == ALOAD_IM2COL][epi];
+}
+
+void gemm_grid(const GemmArgs &g, int epi, unsigned *gx, unsigned *gy) {
+    int MT = 128, NT = 192;
+    if (epi != EPI_LN && epi != EPI_LN_RES) {
+        if (g.N <= 64) NT = 64;
+        else if (epi == EPI_SHUFFLE) NT = 128;
+    }
+    *gx = (unsigned)((g.M + MT - 1) / MT);
+    *gy = (unsigned)((g.N + NT - 1) / NT);
+}
+
+hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
+    // Column tile: 192 (6 MFMA tiles) covers the 180-wide rows in one
+    // workgroup (LayerNorm epilogues need that) with 6.7% padding; 64 for the
+    // head's 64-wide conv; 128 for the shuffle octaves (256 = 2 x 128).
+    if (epi == EPI_LN || epi == EPI_LN_RES) {
+        if (g.N > 192) return hipErrorInvalidValue;
+        return aload == ALOAD_ROWS ? run_gemm_e<128, 192, 2, 2, ALOAD_ROWS>(g, epi, st)
+                                   : run_gemm_e<128, 192, 2, 2, ALOAD_IM2COL>(g, epi, st);
+    }
+    if (g.N <= 64)
+        return aload == ALOAD_ROWS ? run_gemm_e<128, 64, 4, 1, ALOAD_ROWS>(g, epi, st)
+                                   : run_gemm_e<128, 64, 4, 1, ALOAD_IM2COL>(g, epi, st);
+    if (epi == EPI_SHUFFLE)
+        return aload == ALOAD_ROWS ? run_gemm_e<128, 128, 2, 2, ALOAD_ROWS>(g, epi, st)
+                                   : run_gemm_e<128, 128, 2, 2, ALOAD_IM2COL>(g, epi, st);
+    return aload == ALOAD_ROWS ? run_gemm_e<128, 192, 2, 2, ALOAD_ROWS>(g, epi, st)
+                               : run_gemm_e<128, 192, 2, 2, ALOAD_IM2COL>(g, epi, st);
+}
+
+hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out) {
+    const unsigned grid = (unsigned)((g.nw * g.heads + 3) / 4);
+    if (grid_out) *grid_out = grid;
+    hipLaunchKernelGGL(k_attention, dim3(grid), dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
+                            hipStream_t st) {
+    const int n = hp * wp;
+    hipLaunchKernelGGL(k_pad_input, dim3((n + 255) / 256), dim3(256), 0, st, in, out, h, w, hp,
+                       wp);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,
+                            float *out, int P, int C, hipStream_t st) {
+    hipLaunchKernelGGL(k_layernorm, dim3((P + 15) / 16), dim3(256), 0, st, x, w, b, res, out, P,
+                       C);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
+                                   float *out, int H, int W, int feat, int oh, int ow,
+                                   float img_range, const float *mean, hipStream_t st) {
+    dim3 grid((ow + 63) / 64, (oh + 3) / 4);
+    hipLaunchKernelGGL(k_conv_last_finish, grid, dim3(256), 0, st, in, wt, bias, out, H, W, feat,
+                       oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+    return hipGetLastError();
+}
+
+hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *tab, float *cpbt,
+                      int win, int heads, hipStream_t st) {
+    const int side = 2 * win - 1, n = win * win;
+    hipLaunchKernelGGL(k_cpb_mlp, dim3(side * side), dim3(256), 0, st, w0, b0, w2, tab, win,
+                       heads);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int total = heads * n * n;
+    hipLaunchKernelGGL(k_cpb_gather, dim3((total + 255) / 256), dim3(256), 0, st, tab, cpbt, win,
+                       heads);
+    return hipGetLastError();
+}
+
+hipError_t launch_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *reg,
+                             hipStream_t st) {
+    const int total = (hp / 8) * (wp / 8) * 64;
+    hipLaunchKernelGGL(k_window_map, dim3((total + 255) / 256), dim3(256), 0, st, hp, wp, shift,
+                       yx, reg);
+    return hipGetLastError();
+}

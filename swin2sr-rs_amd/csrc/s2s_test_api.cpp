@@ -1,0 +1,275 @@
+// s2s_test_api.cpp - the per-op test entry points of include/swin2sr_hip.h
+// (the device half of the reference's gpu::selftest, src/gpu.rs:889-1265).
+// Each uploads host operands, runs ONE kernel of the production path on the
+// null stream, downloads and synchronises. They reuse the production launchers
+// so the tested code is the code the forward runs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/swin2sr_hip.h"
+#include "s2s_kernels.h"
+
+namespace {
+
+// Scoped device allocations: everything is freed on return, success or not.
+struct Dev {
+    std::vector<void *> ptrs;
+    ~Dev() {
+        for (void *p : ptrs) (void)hipFree(p);
+    }
+    template <typename T>
+    T *alloc(size_t n) {
+        void *p = nullptr;
+        if (hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)) != hipSuccess) return nullptr;
+        ptrs.push_back(p);
+        return static_cast<T *>(p);
+    }
+    template <typename T>
+    T *up(const T *host, size_t n) {
+        T *d = alloc<T>(n);
+        if (d && host && hipMemcpy(d, host, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+            return nullptr;
+        return d;
+    }
+};
+
+int round4(int v) { return (v + 3) / 4 * 4; }
+
+// channel-pad [rows][c] -> [rows][cp] with zeros
+std::vector<float> pad_rows(const float *x, size_t rows, int c, int cp) {
+    std::vector<float> o(rows * (size_t)cp, 0.f);
+    for (size_t r = 0; r < rows; ++r) std::memcpy(&o[r * cp], x + r * c, sizeof(float) * c);
+    return o;
+}
+
+std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vector<int> *perm) {
+    const int cp = round4(ci);
+    std::vector<float> out((size_t)co * 9 * cp, 0.f);
+    for (int o = 0; o < co; ++o) {
+        const int dst = perm ? (*perm)[o] : o;
+        for (int i = 0; i < ci; ++i)
+            for (int t = 0; t < 9; ++t)
+                out[((size_t)dst * 9 + t) * cp + i] = w[((size_t)o * ci + i) * 9 + t];
+    }
+    return out;
+}
+
+}  // namespace
+
+namespace {
+
+int fail(const std::string &m) { return s2s_fail(m.c_str()); }
+
+int finish(hipError_t e, const char *what) {
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(std::string(what) + " failed: " + hipGetErrorString(e));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int s2s_test_window_map(int hp, int wp, int win, int shift, int32_t *yx, uint8_t *reg) {
+    if (win != 8) return fail("the device window map is built for 8x8 windows");
+    if (hp % 8 || wp % 8 || hp <= 0 || wp <= 0) return fail("plane must be a multiple of 8");
+    if (shift < 0 || shift >= 8) return fail("shift must be in [0, 8)");
+    const size_t n = (size_t)(hp / 8) * (wp / 8) * 64;
+    Dev d;
+    int32_t *dyx = d.alloc<int32_t>(2 * n);
+    uint8_t *dreg = d.alloc<uint8_t>(2 * n);
+    if (!dyx || !dreg) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_window_map(hp, wp, shift, dyx, dreg, 0);
+    if (int rc = finish(e, "k_window_map")) return rc;
+    if (hipMemcpy(yx, dyx, 2 * n * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(reg, dreg, 2 * n, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
+int s2s_test_attention(int hp, int wp, int win, int heads, int head_dim, int shift,
+                       const float *qkv, const float *logit_scale, const float *cpb, float *out) {
+    if (win != 8) return fail("the device attention kernel is built for 8x8 windows");
+    if (head_dim > 32 || head_dim <= 0) return fail("head_dim must be in [1, 32]");
+    if (hp % 8 || wp % 8) return fail("plane must be a multiple of 8");
+    const int c = heads * head_dim;
+    if (c % 4) return fail("heads*head_dim must be a multiple of 4");
+    const size_t P = (size_t)hp * wp;
+    const int n = 64;
+    std::vector<float> cpbt((size_t)heads * n * n);
+    for (int q = 0; q < n; ++q)
+        for (int k = 0; k < n; ++k)
+            for (int h = 0; h < heads; ++h)
+                cpbt[((size_t)h * n + q) * n + k] = cpb[((size_t)q * n + k) * heads + h];
+    Dev d;
+    AttnArgs a{};
+    a.qkv = d.up(qkv, P * 3 * c);
+    a.cpbt = d.up(cpbt.data(), cpbt.size());
+    a.logit_scale = d.up(logit_scale, heads);
+    a.out = d.alloc<float>(P * c);
+    if (!a.qkv || !a.cpbt || !a.logit_scale || !a.out) return fail("hipMalloc failed: out of memory");
+    a.hp = hp;
+    a.wp = wp;
+    a.nww = wp / 8;
+    a.nw = (hp / 8) * (wp / 8);
+    a.heads = heads;
+    a.head_dim = head_dim;
+    a.c = c;
+    a.shift = shift;
+    hipError_t e = launch_attention(a, 0, nullptr);
+    if (int rc = finish(e, "k_attention")) return rc;
+    if (hipMemcpy(out, a.out, P * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
+int s2s_test_cpb_table(int win, int heads, const float *w0, const float *b0, const float *w2,
+                       float *out) {
+    if (win < 2) return fail("window must be >= 2");
+    const int n = win * win, side = 2 * win - 1;
+    Dev d;
+    const float *dw0 = d.up(w0, 1024), *db0 = d.up(b0, 512), *dw2 = d.up(w2, (size_t)heads * 512);
+    float *tab = d.alloc<float>((size_t)heads * side * side);
+    float *cpbt = d.alloc<float>((size_t)heads * n * n);
+    if (!dw0 || !db0 || !dw2 || !tab || !cpbt) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_cpb(dw0, db0, dw2, tab, cpbt, win, heads, 0);
+    if (int rc = finish(e, "k_cpb")) return rc;
+    std::vector<float> t((size_t)heads * n * n);
+    if (hipMemcpy(t.data(), cpbt, t.size() * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    for (int q = 0; q < n; ++q)
+        for (int k = 0; k < n; ++k)
+            for (int h = 0; h < heads; ++h)
+                out[((size_t)q * n + k) * heads + h] = t[((size_t)h * n + q) * n + k];
+    return 0;
+}
+
+int s2s_test_linear(int rows, int c_in, int c_out, const float *x, const float *w,
+                    const float *bias, int epilogue, const float *res, const float *ln_w,
+                    const float *ln_b, float slope, float *out) {
+    static const int map[6] = {EPI_STORE, EPI_GELU, EPI_RES, EPI_LN, EPI_LN_RES, EPI_LRELU};
+    if (epilogue < 0 || epilogue > 5) return fail("epilogue must be 0..5");
+    const int epi = map[epilogue];
+    if ((epi == EPI_LN || epi == EPI_LN_RES) && c_out > 192)
+        return fail("LayerNorm epilogues need c_out <= 192");
+    if ((epi == EPI_RES || epi == EPI_LN_RES) && !res) return fail("residual epilogue needs res");
+    if ((epi == EPI_LN || epi == EPI_LN_RES) && (!ln_w || !ln_b)) return fail("LN needs ln_w/ln_b");
+    const int kp = round4(c_in);
+    std::vector<float> xp = pad_rows(x, rows, c_in, kp), wp = pad_rows(w, c_out, c_in, kp);
+    Dev d;
+    GemmArgs g{};
+    g.A = d.up(xp.data(), xp.size());
+    g.lda = kp;
+    g.B = d.up(wp.data(), wp.size());
+    g.ldb = kp;
+    g.bias = bias ? d.up(bias, c_out) : nullptr;
+    float *dout = d.alloc<float>((size_t)rows * c_out);
+    g.out = dout;
+    g.ldo = c_out;
+    g.res = res ? d.up(res, (size_t)rows * c_out) : nullptr;
+    g.ldr = c_out;
+    g.ln_w = ln_w ? d.up(ln_w, c_out) : nullptr;
+    g.ln_b = ln_b ? d.up(ln_b, c_out) : nullptr;
+    g.slope = slope;
+    g.M = rows;
+    g.N = c_out;
+    g.K = kp;
+    if (!g.A || !g.B || !dout) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_gemm(g, ALOAD_ROWS, epi, 0);
+    if (int rc = finish(e, "k_gemm")) return rc;
+    if (hipMemcpy(out, dout, (size_t)rows * c_out * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
+int s2s_test_ln_residual(int hw, int c, const float *x, const float *ln_w, const float *ln_b,
+                         const float *res, float *out) {
+    if (c % 4 || c > 256) return fail("the LayerNorm kernel needs c % 4 == 0 and c <= 256");
+    Dev d;
+    const float *dx = d.up(x, (size_t)hw * c), *dw = d.up(ln_w, c), *db = d.up(ln_b, c);
+    const float *dr = res ? d.up(res, (size_t)hw * c) : nullptr;
+    float *dy = d.alloc<float>((size_t)hw * c);
+    if (!dx || !dw || !db || !dy || (res && !dr)) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_layernorm(dx, dw, db, dr, dy, hw, c, 0);
+    if (int rc = finish(e, "k_layernorm")) return rc;
+    if (hipMemcpy(out, dy, (size_t)hw * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
+int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
+                     const float *bias, int epilogue, const float *res, float slope, float *out) {
+    int epi;
+    if (epilogue == 0) epi = EPI_STORE;
+    else if (epilogue == 2) epi = EPI_RES;
+    else if (epilogue == 5) epi = EPI_LRELU;
+    else return fail("conv3x3 epilogue must be 0, 2 or 5");
+    if (epi == EPI_RES && !res) return fail("residual epilogue needs res");
+    const int cp = round4(c_in);
+    const size_t P = (size_t)h * w;
+    std::vector<float> xp = pad_rows(x, P, c_in, cp);
+    std::vector<float> wt = conv_relayout(wgt, c_out, c_in, nullptr);
+    Dev d;
+    GemmArgs g{};
+    g.A = d.up(xp.data(), xp.size());
+    g.H = h;
+    g.W = w;
+    g.cin = cp;
+    g.B = d.up(wt.data(), wt.size());
+    g.ldb = 9 * cp;
+    g.bias = bias ? d.up(bias, c_out) : nullptr;
+    float *dout = d.alloc<float>(P * c_out);
+    g.out = dout;
+    g.ldo = c_out;
+    g.res = res ? d.up(res, P * c_out) : nullptr;
+    g.ldr = c_out;
+    g.slope = slope;
+    g.M = (int)P;
+    g.N = c_out;
+    g.K = 9 * cp;
+    if (!g.A || !g.B || !dout) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_gemm(g, ALOAD_IM2COL, epi, 0);
+    if (int rc = finish(e, "k_gemm(conv3x3)")) return rc;
+    if (hipMemcpy(out, dout, P * c_out * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
+int s2s_test_conv3x3_shuffle2(int h, int w, int c_in, int feat, const float *x,
+                              const float *wgt, const float *bias, float *out) {
+    const int cp = round4(c_in);
+    const size_t P = (size_t)h * w;
+    std::vector<int> perm(4 * feat);
+    for (int co = 0; co < 4 * feat; ++co) perm[co] = (co % 4) * feat + co / 4;
+    std::vector<float> xp = pad_rows(x, P, c_in, cp);
+    std::vector<float> wt = conv_relayout(wgt, 4 * feat, c_in, &perm);
+    std::vector<float> bp(4 * feat);
+    for (int co = 0; co < 4 * feat; ++co) bp[perm[co]] = bias[co];
+    Dev d;
+    GemmArgs g{};
+    g.A = d.up(xp.data(), xp.size());
+    g.H = h;
+    g.W = w;
+    g.cin = cp;
+    g.B = d.up(wt.data(), wt.size());
+    g.ldb = 9 * cp;
+    g.bias = d.up(bp.data(), bp.size());
+    float *dout = d.alloc<float>(P * 4 * feat);
+    g.out = dout;
+    g.feat = feat;
+    g.M = (int)P;
+    g.N = 4 * feat;
+    g.K = 9 * cp;
+    if (!g.A || !g.B || !g.bias || !dout) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_gemm(g, ALOAD_IM2COL, EPI_SHUFFLE, 0);
+    if (int rc = finish(e, "k_gemm(conv3x3_shuffle2)")) return rc;
+    if (hipMemcpy(out, dout, P * 4 * feat * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
+}  // extern "C"
