@@ -69,12 +69,14 @@ def test_attention(pkg, orc, heads, hd, shift, hp, wp):
     vmax = max(1.0, float(np.abs(v).max()))
     err = np.abs(got - want).max()
     assert err < 2e-5 * vmax, err
-    # against exact float64 math the device kernel is tighter still
+    # against exact float64 math: fp32 cosines carry ~1.2e-7 relative error, which
+    # the temperature exp(min(ls, ln 100)) multiplies into the logits
     qw, kw, vw = (R.shifted_windows(t, 8, shift) for t in (q, k, v))
     mids = R.mask_regions(hp, wp, 8, shift) if shift else None
     exact = R.window_attention(qw, kw, vw, ls, cpb, mids)
     exact = nchw_to_hwc(R.unshift_windows(exact, 8, shift, hp, wp))
-    assert np.abs(got - exact).max() < 5e-6 * vmax
+    temp = float(np.exp(min(ls.max(), np.log(100.0))))
+    assert np.abs(got - exact).max() < vmax * (5e-6 + 1.2e-7 * temp)
 
 
 def test_cpb_table(pkg, orc):
