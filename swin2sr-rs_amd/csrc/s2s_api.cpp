@@ -289,7 +289,7 @@ int s2s_ctx::run(const char *name, dim3 grid, dim3 block, F &&launch) {
 
 int s2s_ctx::gemm(const char *name, const GemmArgs &g, int aload, int epi) {
     unsigned gx, gy;
-    gemm_grid(g, epi, &gx, &gy);
+    gemm_grid(g, aload, epi, &gx, &gy);
     return run(name, dim3(gx, gy, 1), dim3(256, 1, 1),
                [&] { return launch_gemm(g, aload, epi, stream); });
 }
@@ -440,7 +440,7 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
     }
     const int s = arch.scale;
     const int oh = h * s, ow = w * s;
-    return run("conv_last_finish", dim3((ow + 63) / 64, (oh + 3) / 4), dim3(256), [&] {
+    return run("conv_last_finish", conv_last_grid(oh, ow), dim3(256), [&] {
         return launch_conv_last_finish(fplanes[octaves], last_w, last_b, d_out, H, W, feat, oh,
                                        ow, arch.img_range, arch.mean, stream);
     });

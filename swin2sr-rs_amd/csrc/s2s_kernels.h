@@ -46,14 +46,20 @@ struct AttnArgs {
     int shift;
 };
 
+#define GEMM_NVARIANTS 6
 hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st);
-void gemm_grid(const GemmArgs &g, int epi, unsigned *gx, unsigned *gy);
+hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int variant,
+                               hipStream_t st);
+int gemm_pick(const GemmArgs &g, int aload, int epi);
+void gemm_grid(const GemmArgs &g, int aload, int epi, unsigned *gx, unsigned *gy);
+void gemm_variant_grid(const GemmArgs &g, int variant, unsigned *gx, unsigned *gy);
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi);
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out);
 hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
                             hipStream_t st);
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,
                             float *out, int P, int C, hipStream_t st);
+dim3 conv_last_grid(int oh, int ow);
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
                                    float *out, int H, int W, int feat, int oh, int ow,
                                    float img_range, const float *mean, hipStream_t st);

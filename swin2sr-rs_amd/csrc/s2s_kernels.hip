@@ -351,20 +351,55 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 
     const float ls = __expf(fminf(g.logit_scale[h], 4.605170185988092f));
 
-    float qv[2][16], kv[2][16];
+    // Every global read of the wave is issued here, before any arithmetic, so
+    // their latencies overlap: q and k rows (lane half hh takes d = 16hh..+15,
+    // as pairs when head_dim is even), and the 32 v values this lane feeds
+    // the AV product (key 32kt + 8a + 4hh + b, dimension r).
+    float qv[2][16], kv[2][16], vv[2][16];
+    const bool even = (hd & 1) == 0;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
         const float *row = g.qkv + (size_t)pix(32 * t2 + r) * ld + h * hd;
+        if (even) {
+#pragma unroll
+            for (int j = 0; j < 16; j += 2) {
+                const int d = 16 * hh + j;
+                float2 a = make_float2(0.f, 0.f), b = a;
+                if (d < hd) {
+                    a = *reinterpret_cast<const float2 *>(row + d);
+                    b = *reinterpret_cast<const float2 *>(row + g.c + d);
+                }
+                qv[t2][j] = a.x;
+                qv[t2][j + 1] = a.y;
+                kv[t2][j] = b.x;
+                kv[t2][j + 1] = b.y;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int d = 16 * hh + j;
+                qv[t2][j] = d < hd ? row[d] : 0.f;
+                kv[t2][j] = d < hd ? row[g.c + d] : 0.f;
+            }
+        }
+    }
+    {
+        const float *vbase = g.qkv + 2 * g.c + h * hd + r;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+                vv[kt][e] = (r < hd) ? vbase[(size_t)pix(key) * ld] : 0.f;
+            }
+    }
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
         float qs = 0.f, ks = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const int d = 16 * hh + j;
-            const float a = d < hd ? row[d] : 0.f;
-            const float b = d < hd ? row[g.c + d] : 0.f;
-            qv[t2][j] = a;
-            kv[t2][j] = b;
-            qs += a * a;
-            ks += b * b;
+            qs += qv[t2][j] * qv[t2][j];
+            ks += kv[t2][j] * kv[t2][j];
         }
         qs += __shfl_xor(qs, 32, 64);
         ks += __shfl_xor(ks, 32, 64);
@@ -448,26 +483,30 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
     for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[qt][e] = 0.f;
-    const float *vbase = g.qkv + 2 * g.c + h * hd + r;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int e = 0; e < 16; ++e)
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int key = 32 * kt + 8 * a + 4 * hh + b;
-                const float v = (r < hd) ? vbase[(size_t)pix(key) * ld] : 0.f;
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) o[qt] = MFMA32(v, s[kt][qt][4 * a + b], o[qt]);
-            }
+            for (int qt = 0; qt < 2; ++qt) o[qt] = MFMA32(vv[kt][e], s[kt][qt][e], o[qt]);
 
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         float *orow = g.out + (size_t)pix(32 * qt + r) * g.c + h * hd;
+        if (even) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
-            if (d < hd) orow[d] = o[qt][e] * inv[qt];
+            for (int e = 0; e < 16; e += 2) {
+                const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
+                if (d < hd)
+                    *reinterpret_cast<float2 *>(orow + d) =
+                        make_float2(o[qt][e] * inv[qt], o[qt][e + 1] * inv[qt]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
+                if (d < hd) orow[d] = o[qt][e] * inv[qt];
+            }
         }
     }
 }
@@ -551,8 +590,16 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x,
 
 // conv_last (feat -> 3, 3x3, zero pad) fused with the reference's host
 // epilogue cpu::finish (src/cpu.rs:1925-1941): y/img_range + mean, cropped to
-// the unpadded output, written planar [3][oh][ow]. One thread per kept pixel;
-// weights are read as wave-uniform (scalar) loads, layout [tap][ci][3].
+// the unpadded output, written planar [3][oh][ow].
+//
+// HBM-bound (it reads the 64-channel plane of the last octave once): a
+// workgroup owns an 8 x 32 output tile, one pixel per thread, and stages the
+// 10 x 34 input halo through LDS 32 channels at a time (one 128-byte line per
+// pixel per chunk), so every input byte is fetched from HBM about once. The
+// weights, layout [tap][ci][3], are wave-uniform (scalar) loads.
+#define CL_TY 8
+#define CL_TX 32
+#define CL_CC 32
 __global__ __launch_bounds__(256) void k_conv_last_finish(const float *__restrict__ in,
                                                           const float *__restrict__ wt,
                                                           const float *__restrict__ bias,
@@ -560,26 +607,43 @@ __global__ __launch_bounds__(256) void k_conv_last_finish(const float *__restric
                                                           int feat, int oh, int ow,
                                                           float inv_range, float m0, float m1,
                                                           float m2) {
-    const int x = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int y = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (x >= ow || y >= oh) return;
+    constexpr int TH = CL_TY + 2, TW = CL_TX + 2;
+    __shared__ float4 tile[TH * TW * (CL_CC / 4)];
+    const int tid = threadIdx.x;
+    const int tx = tid & (CL_TX - 1), ty = tid / CL_TX;
+    const int x0 = blockIdx.x * CL_TX, y0 = blockIdx.y * CL_TY;
+    const int x = x0 + tx, y = y0 + ty;
     float a0 = bias[0], a1 = bias[1], a2 = bias[2];
-    for (int tap = 0; tap < 9; ++tap) {
-        const int sy = y + tap / 3 - 1, sx = x + tap % 3 - 1;
-        if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
-        const float *src = in + ((size_t)sy * W + sx) * feat;
-        const float *wk = wt + tap * feat * 3;
-        for (int ci = 0; ci < feat; ci += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + ci);
-            const float vv[4] = {v.x, v.y, v.z, v.w};
+    for (int c0 = 0; c0 < feat; c0 += CL_CC) {
+        __syncthreads();
+        for (int i = tid; i < TH * TW * (CL_CC / 4); i += 256) {
+            const int q = i % (CL_CC / 4);
+            const int p = i / (CL_CC / 4);
+            const int sy = y0 - 1 + p / TW, sx = x0 - 1 + p % TW;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (sy >= 0 && sy < H && sx >= 0 && sx < W)
+                v = *reinterpret_cast<const float4 *>(in + ((size_t)sy * W + sx) * feat + c0 + 4 * q);
+            tile[i] = v;
+        }
+        __syncthreads();
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                a0 += wk[(ci + u) * 3 + 0] * vv[u];
-                a1 += wk[(ci + u) * 3 + 1] * vv[u];
-                a2 += wk[(ci + u) * 3 + 2] * vv[u];
+        for (int tap = 0; tap < 9; ++tap) {
+            const float4 *src = &tile[((ty + tap / 3) * TW + tx + tap % 3) * (CL_CC / 4)];
+            const float *wk = wt + (tap * feat + c0) * 3;
+#pragma unroll
+            for (int q = 0; q < CL_CC / 4; ++q) {
+                const float4 v = src[q];
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    a0 += wk[(4 * q + u) * 3 + 0] * vv[u];
+                    a1 += wk[(4 * q + u) * 3 + 1] * vv[u];
+                    a2 += wk[(4 * q + u) * 3 + 2] * vv[u];
+                }
             }
         }
     }
+    if (x >= ow || y >= oh) return;
     const size_t plane = (size_t)oh * ow, o = (size_t)y * ow + x;
     out[o] = a0 * inv_range + m0;
     out[plane + o] = a1 * inv_range + m1;
@@ -646,18 +710,35 @@ static hipError_t run_gemm_t(const GemmArgs &g, hipStream_t st) {
     return hipGetLastError();
 }
 
+// The tile shapes (rows MT x columns NT, wavefront grid WM x WN).
+static const int kVariants[GEMM_NVARIANTS][4] = {
+    {128, 192, 2, 2}, {64, 192, 2, 2}, {128, 64, 4, 1}, {128, 128, 2, 2}, {64, 128, 2, 2},
+    {64, 64, 2, 2}};
+
 template <int MT, int NT, int WM, int WN, int ALOAD>
 static hipError_t run_gemm_e(const GemmArgs &g, int epi, hipStream_t st) {
     switch (epi) {
     case EPI_STORE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_STORE>(g, st);
     case EPI_GELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_GELU>(g, st);
     case EPI_RES: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_RES>(g, st);
-    case EPI_LN: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN>(g, st);
-    case EPI_LN_RES: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN_RES>(g, st);
     case EPI_LRELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
     case EPI_SHUFFLE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_SHUFFLE>(g, st);
+    case EPI_LN:
+    case EPI_LN_RES:
+        // the whole row must be one column tile
+        if constexpr (NT >= 192) {
+            return epi == EPI_LN ? run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN>(g, st)
+                                 : run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN_RES>(g, st);
+        }
+        return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
+}
+
+template <int MT, int NT, int WM, int WN>
+static hipError_t run_gemm_v(const GemmArgs &g, int aload, int epi, hipStream_t st) {
+    return aload == ALOAD_ROWS ? run_gemm_e<MT, NT, WM, WN, ALOAD_ROWS>(g, epi, st)
+                               : run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL>(g, epi, st);
 }
 
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
@@ -670,33 +751,47 @@ const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
     return names[aload == ALOAD_IM2COL][epi];
 }
 
-void gemm_grid(const GemmArgs &g, int epi, unsigned *gx, unsigned *gy) {
-    int MT = 128, NT = 192;
-    if (epi != EPI_LN && epi != EPI_LN_RES) {
-        if (g.N <= 64) NT = 64;
-        else if (epi == EPI_SHUFFLE) NT = 128;
-    }
+// Tile choice by shape, from a sweep of every variant on the forward's own
+// shapes on MI355X. These GEMMs are short in K (180-1620) and latency-bound:
+// the 64x64 tile (one 32x32 MFMA tile per wavefront, ~18 KB of LDS) keeps the
+// most wavefronts resident and wins everywhere except the shuffle octaves
+// (K = 576, 256 columns: 64x128). LayerNorm epilogues need the whole row in
+// one 192-wide column tile; 64 rows keeps that grid from ending in a nearly
+// empty round of workgroups.
+int gemm_pick(const GemmArgs &g, int aload, int epi) {
+    (void)aload;
+    (void)g;
+    if (epi == EPI_LN || epi == EPI_LN_RES) return 1;
+    if (epi == EPI_SHUFFLE) return 4;
+    return 5;
+}
+
+void gemm_variant_grid(const GemmArgs &g, int variant, unsigned *gx, unsigned *gy) {
+    const int MT = kVariants[variant][0], NT = kVariants[variant][1];
     *gx = (unsigned)((g.M + MT - 1) / MT);
     *gy = (unsigned)((g.N + NT - 1) / NT);
 }
 
-hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
-    // Column tile: 192 (6 MFMA tiles) covers the 180-wide rows in one
-    // workgroup (LayerNorm epilogues need that) with 6.7% padding; 64 for the
-    // head's 64-wide conv; 128 for the shuffle octaves (256 = 2 x 128).
-    if (epi == EPI_LN || epi == EPI_LN_RES) {
-        if (g.N > 192) return hipErrorInvalidValue;
-        return aload == ALOAD_ROWS ? run_gemm_e<128, 192, 2, 2, ALOAD_ROWS>(g, epi, st)
-                                   : run_gemm_e<128, 192, 2, 2, ALOAD_IM2COL>(g, epi, st);
+void gemm_grid(const GemmArgs &g, int aload, int epi, unsigned *gx, unsigned *gy) {
+    gemm_variant_grid(g, gemm_pick(g, aload, epi), gx, gy);
+}
+
+hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int variant,
+                               hipStream_t st) {
+    if ((epi == EPI_LN || epi == EPI_LN_RES) && g.N > 192) return hipErrorInvalidValue;
+    switch (variant) {
+    case 0: return run_gemm_v<128, 192, 2, 2>(g, aload, epi, st);
+    case 1: return run_gemm_v<64, 192, 2, 2>(g, aload, epi, st);
+    case 2: return run_gemm_v<128, 64, 4, 1>(g, aload, epi, st);
+    case 3: return run_gemm_v<128, 128, 2, 2>(g, aload, epi, st);
+    case 4: return run_gemm_v<64, 128, 2, 2>(g, aload, epi, st);
+    case 5: return run_gemm_v<64, 64, 2, 2>(g, aload, epi, st);
+    default: return hipErrorInvalidValue;
     }
-    if (g.N <= 64)
-        return aload == ALOAD_ROWS ? run_gemm_e<128, 64, 4, 1, ALOAD_ROWS>(g, epi, st)
-                                   : run_gemm_e<128, 64, 4, 1, ALOAD_IM2COL>(g, epi, st);
-    if (epi == EPI_SHUFFLE)
-        return aload == ALOAD_ROWS ? run_gemm_e<128, 128, 2, 2, ALOAD_ROWS>(g, epi, st)
-                                   : run_gemm_e<128, 128, 2, 2, ALOAD_IM2COL>(g, epi, st);
-    return aload == ALOAD_ROWS ? run_gemm_e<128, 192, 2, 2, ALOAD_ROWS>(g, epi, st)
-                               : run_gemm_e<128, 192, 2, 2, ALOAD_IM2COL>(g, epi, st);
+}
+
+hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
+    return launch_gemm_variant(g, aload, epi, gemm_pick(g, aload, epi), st);
 }
 
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out) {
@@ -721,10 +816,13 @@ hipError_t launch_layernorm(const float *x, const float *w, const float *b, cons
     return hipGetLastError();
 }
 
+dim3 conv_last_grid(int oh, int ow) { return dim3((ow + CL_TX - 1) / CL_TX, (oh + CL_TY - 1) / CL_TY); }
+
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
                                    float *out, int H, int W, int feat, int oh, int ow,
                                    float img_range, const float *mean, hipStream_t st) {
-    dim3 grid((ow + 63) / 64, (oh + 3) / 4);
+    if (feat % CL_CC) return hipErrorInvalidValue;
+    const dim3 grid = conv_last_grid(oh, ow);
     hipLaunchKernelGGL(k_conv_last_finish, grid, dim3(256), 0, st, in, wt, bias, out, H, W, feat,
                        oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
     return hipGetLastError();
