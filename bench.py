@@ -83,24 +83,30 @@ def traffic_from_profiles(kernel):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(M, orc, arch, weights, sample):
-    """The oracle (C restatement of the crate's CPU path) on `sample` x `sample`."""
+def cpu_baseline(M, orc, arch, weights, sample, passes):
+    """The oracle (C restatement of the crate's CPU path, OpenMP over the host
+    cores) on the same workload: median of `passes` whole-image forwards of a
+    `sample` x `sample` input after a 32x32 warm-up."""
     img = M.to_unit(M.input_sinusoids(sample, sample, seed=3))
     x = M.adjust(arch, img)
     warm = M.adjust(arch, M.to_unit(M.input_sinusoids(32, 32, seed=3)))
     orc.forward(arch, weights, 32, 32, warm)
-    t0 = time.perf_counter()
-    orc.forward(arch, weights, sample, sample, x)
-    dt = time.perf_counter() - t0
+    times = []
+    for i in range(passes):
+        t0 = time.perf_counter()
+        orc.forward(arch, weights, sample, sample, x)
+        times.append(time.perf_counter() - t0)
+        log(f"bench: cpu pass {i + 1}/{passes}: {times[-1]:.2f} s")
+    dt = float(np.median(times))
     out_px = (sample * arch.scale) ** 2
     return {
         "value": round(out_px / dt / 1e6, 5),
         "unit": "Mpix/s",
         "cores": int(orc.lib().orc_threads()),
         "kind": "port",
-        "sample": (f"one classical-x4 {sample}x{sample}->{sample * arch.scale}x{sample * arch.scale}"
-                   f" whole-image forward (same weights and input generator), after a 32x32"
-                   f" warm-up; {dt:.2f} s"),
+        "sample": (f"median of {passes} classical-x4 {sample}x{sample}->{sample * arch.scale}x"
+                   f"{sample * arch.scale} whole-image forwards (same weights and input), after a"
+                   f" 32x32 warm-up; {sum(times):.1f} s of CPU work in total"),
     }
 
 
@@ -111,7 +117,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--size", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=128)
+    ap.add_argument("--cpu-sample", type=int, default=256)
+    ap.add_argument("--cpu-passes", type=int, default=3)
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="before the warm-up, one device-to-device copy of this many MiB: the "
+                         "plain copy kernel of known size that scales rocprofv3's FETCH_SIZE / "
+                         "WRITE_SIZE counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this backend runs a whole image on one device and has "
@@ -136,6 +147,15 @@ def main():
     s = arch.scale
     dout = hip.DeviceBuffer(3 * h * s * w * s)
     stream = be.stream()
+
+    if args.copy_probe_mb > 0:
+        n = args.copy_probe_mb * 2**20 // 4
+        a, b = hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+        hip.copy_device(b.ptr, a.ptr, n * 4)
+        hip.synchronize()
+        a.free()
+        b.free()
+        log(f"bench: copy probe of {args.copy_probe_mb} MiB done")
 
     for _ in range(args.warmup):
         be.forward_device(h, w, din.ptr, dout.ptr)
@@ -200,7 +220,8 @@ def main():
     if not args.no_cpu:
         orc = ge._load_oracle()
         log(f"bench: cpu baseline on {orc.lib().orc_threads()} threads ...")
-        result["cpu_baseline"] = cpu_baseline(M, orc, arch, weights, args.cpu_sample)
+        result["cpu_baseline"] = cpu_baseline(M, orc, arch, weights, args.cpu_sample,
+                                              args.cpu_passes)
         log(f"bench: cpu {result['cpu_baseline']}")
     else:
         result["cpu_baseline"] = None

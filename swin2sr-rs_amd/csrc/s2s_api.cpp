@@ -288,10 +288,9 @@ int s2s_ctx::run(const char *name, dim3 grid, dim3 block, F &&launch) {
 }
 
 int s2s_ctx::gemm(const char *name, const GemmArgs &g, int aload, int epi) {
-    unsigned gx, gy;
-    gemm_grid(g, aload, epi, &gx, &gy);
-    return run(name, dim3(gx, gy, 1), dim3(256, 1, 1),
-               [&] { return launch_gemm(g, aload, epi, stream); });
+    dim3 grid, block;
+    gemm_geometry(g, aload, epi, &grid, &block);
+    return run(name, grid, block, [&] { return launch_gemm(g, aload, epi, stream); });
 }
 
 namespace {

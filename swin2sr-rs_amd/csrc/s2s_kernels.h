@@ -36,6 +36,25 @@ struct GemmArgs {
     int M, N, K;
 };
 
+// The weight-stationary token GEMM (k_bsgemm): out = epi(A B^T + bias) with A
+// [M][lda] rows, B [N][ldb] rows. Set by the launcher: P (workgroups per
+// column group) and ngw (columns per group).
+struct BsArgs {
+    const float *A;
+    int lda;
+    const float *B;
+    int ldb;
+    const float *bias;
+    float *out;
+    int ldo;
+    const float *res;
+    int ldr;
+    const float *ln_w, *ln_b;
+    float slope;
+    int M, N, K;
+    int P, ngw;
+};
+
 struct AttnArgs {
     const float *qkv;          // [hp*wp][3c] plane order: q | k | v
     const float *cpbt;         // [heads][64][64]
@@ -54,6 +73,9 @@ int gemm_pick(const GemmArgs &g, int aload, int epi);
 void gemm_grid(const GemmArgs &g, int aload, int epi, unsigned *gx, unsigned *gy);
 void gemm_variant_grid(const GemmArgs &g, int variant, unsigned *gx, unsigned *gy);
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi);
+// The launch geometry launch_gemm will use for these arguments (for the
+// profiler's rows), and the kernel family name it picks.
+void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block);
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out);
 hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
                             hipStream_t st);

@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "s2s_kernels.h"
 
 typedef float f16v __attribute__((ext_vector_type(16)));
@@ -271,6 +273,285 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                 }
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2, the 1x1 convs) with the
+// WEIGHTS STATIONARY IN REGISTERS.
+//
+// Every token GEMM of the network has K in {C, 2C} and a weight of at most
+// 540 x 360 floats, while M is the whole plane (69,696 tokens at 256x256).
+// So the weight slice a wavefront needs is loaded into VGPRs once, and the
+// activations stream past it exactly once:
+//   - a workgroup owns one column group of <= 192 output columns (4 waves x
+//     48 columns = 3 MFMA tiles of 16) and, for K = 2*KPW, a second set of 4
+//     waves holding the other half of K (their partial sums meet in LDS);
+//   - it is persistent: it walks 16-row tasks p, p+P, p+2P, ... of the plane;
+//     each task's A tile (16 rows x K, contiguous in HBM) is loaded once,
+//     coalesced, into LDS (double-buffered: the next task's loads are in flight
+//     while this one multiplies), and read by the 4 column waves;
+//   - v_mfma_f32_16x16x4f32, fp32 in and out. A step s consumes k(s, q) from
+//     lane group q = lane/16: k = 16(s/4) + 4q + s%4 for the full groups of 16
+//     (so a lane's A operands for 4 steps are one ds_read_b128 and its B
+//     operands are 4 consecutive floats of a weight row), and k = 16G + Rq + t
+//     for the R-step tail. The permutation reorders the reduction, not the
+//     result.
+//   - the whole row is inside the workgroup, so LayerNorm (+ residual) is an
+//     epilogue: row sums over the lane's 3 tiles, over the 16 lanes of a lane
+//     group, then over the 4 column waves through LDS.
+// Blocks are numbered ng*P + p with P a multiple of 8, so the column groups
+// that read the same A tile run on the same XCD and share its L2.
+//
+// MFMA 16x16x4 f32 lane layout: lane l supplies A[l%16][k] and B[k][l%16] for
+// its k (above); accumulator register r of lane l holds D[4*(l/16) + r][l%16].
+// ---------------------------------------------------------------------------
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+#define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x4f32((a), (b), (c), 0, 0, 0)
+
+// LDS row stride (floats) of an A tile: a multiple of 4 that is an odd
+// multiple of 4 modulo 32, so the 16 rows read by one ds_read_b128 (8 lanes
+// per 128-byte bank sweep) land in distinct banks.
+__host__ __device__ constexpr int bs_lds_stride(int k) {
+    return (k % 32 == 4 || k % 32 == 12 || k % 32 == 20 || k % 32 == 28) ? k
+           : (k % 8 == 0) ? k + 4 : k + 8;
+}
+
+// Raw buffer access: a load whose byte offset lies past the resource's size
+// returns zero and such a store is dropped, so tile edges (rows past M, columns
+// past the group) need no branches, and every wave issues the same number of
+// memory instructions on every path - which lets the compiler count them
+// exactly in its s_waitcnt instead of draining the queue.
+#define BUF_OOB 0x7ffffff0
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu),
+                                             0x00020000);
+}
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
+}
+
+template <int KPW, int KS, int EPI>
+__global__ __launch_bounds__(256 * KS) void k_bsgemm(BsArgs g) {
+    constexpr int NT = 256 * KS;
+    constexpr int G = KPW / 16;
+    constexpr int R = (KPW % 16) / 4;
+    constexpr int S = KPW / 4;
+    constexpr int KT = KPW * KS;
+    constexpr int SA = bs_lds_stride(KT);
+    constexpr int V4 = 16 * KT / 4;            // float4s per A tile
+    constexpr int NL = (V4 + NT - 1) / NT;     // per thread
+    constexpr bool HAS_RES = EPI == EPI_RES || EPI == EPI_LN_RES;
+    constexpr bool HAS_LN = EPI == EPI_LN || EPI == EPI_LN_RES;
+    static_assert(KPW % 4 == 0, "K must be a multiple of 4");
+
+    __shared__ float As[2][16 * SA];
+    __shared__ float ksum[KS == 2 ? 4 * 3 * 4 * 64 : 1];
+    __shared__ float rstat[4][16][2];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int cg = wave & 3;
+    const int kq = wave >> 2;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int ng = blockIdx.x / g.P;
+    const int p = blockIdx.x - ng * g.P;
+    const int gc0 = ng * g.ngw;
+    const int gc1 = min(gc0 + g.ngw, g.N);
+    const int kbase = kq * KPW;
+
+    const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(g.A, (size_t)g.M * g.lda * 4);
+    const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
+    const __amdgpu_buffer_rsrc_t ro_rs = buf_rsrc(g.out, (size_t)g.M * g.ldo * 4);
+    const __amdgpu_buffer_rsrc_t rr_rs = buf_rsrc(HAS_RES ? g.res : g.out,
+                                                  HAS_RES ? (size_t)g.M * g.ldr * 4 : 0);
+
+    // ---- the weight slice, once (columns outside the group read as zero) ----
+    float bw[3][S];
+    float bias_v[3], lnw[3], lnb[3];
+    bool cok[3];
+    int col[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        col[t] = gc0 + 48 * cg + 16 * t + j;
+        cok[t] = col[t] < gc1;
+        const int boff = cok[t] ? (col[t] * g.ldb + kbase) * 4 : BUF_OOB;
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const float4 v = buf_load4(rb_rs, boff + (16 * gi + 4 * q) * 4);
+            bw[t][4 * gi + 0] = v.x;
+            bw[t][4 * gi + 1] = v.y;
+            bw[t][4 * gi + 2] = v.z;
+            bw[t][4 * gi + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < R; ++i) bw[t][4 * G + i] = buf_load1(rb_rs, boff + (16 * G + R * q + i) * 4);
+        const int cc = cok[t] ? col[t] : gc0;
+        bias_v[t] = (cok[t] && g.bias) ? g.bias[cc] : 0.f;
+        lnw[t] = (HAS_LN && cok[t]) ? g.ln_w[cc] : 0.f;
+        lnb[t] = (HAS_LN && cok[t]) ? g.ln_b[cc] : 0.f;
+    }
+    // Retire the weight loads here, once.
+    __builtin_amdgcn_s_waitcnt(0);
+
+    const int ntask = (g.M + 15) >> 4;
+    float4 ra[NL];
+    // A tile of task `task`: always NL loads per thread (rows past M read 0;
+    // the few lanes past the tile re-read its first float4 and are not stored)
+    auto gload = [&](int task) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            int idx = tid + u * NT;
+            if (NL * NT > V4) idx = idx < V4 ? idx : idx - V4;
+            const int row = idx / (KT / 4);
+            const int c4 = idx - row * (KT / 4);
+            const int m = task * 16 + row;
+            ra[u] = buf_load4(ra_rs, m < g.M ? (m * g.lda + 4 * c4) * 4 : BUF_OOB);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int idx = tid + u * NT;
+            if (idx < V4) {
+                const int row = idx / (KT / 4);
+                const int c4 = idx - row * (KT / 4);
+                *reinterpret_cast<float4 *>(&As[buf][row * SA + 4 * c4]) = ra[u];
+            }
+        }
+    };
+
+    int task = p;
+    int buf = 0;
+    if (task < ntask) {
+        gload(task);
+        lstore(0);
+    }
+    __syncthreads();
+    for (; task < ntask; task += g.P) {
+        const int nxt = task + g.P;
+        const int m0 = task * 16 + 4 * q;
+        // this task's residual first, then the next task's A tile: both are in
+        // flight while this task multiplies
+        float rv[3][4];
+        if (HAS_RES) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+                    rv[t][r] = buf_load1(rr_rs, (m0 + r < g.M && cok[t])
+                                                    ? ((m0 + r) * g.ldr + col[t]) * 4
+                                                    : BUF_OOB);
+        }
+        gload(nxt < ntask ? nxt : task);
+
+        f4v acc[3];
+#pragma unroll
+        for (int t = 0; t < 3; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
+        const float *arow = &As[buf][j * SA + kbase];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const float4 a = *reinterpret_cast<const float4 *>(arow + 16 * gi + 4 * q);
+            const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int t = 0; t < 3; ++t) acc[t] = MFMA16(av[i], bw[t][4 * gi + i], acc[t]);
+        }
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const float a = arow[16 * G + R * q + i];
+#pragma unroll
+            for (int t = 0; t < 3; ++t) acc[t] = MFMA16(a, bw[t][4 * G + i], acc[t]);
+        }
+
+        if (KS == 2) {
+            // the second K half's partial sums meet the first's in LDS
+            if (kq == 1) {
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ksum[((cg * 3 + t) * 4 + r) * 64 + lane] = acc[t][r];
+            }
+            __syncthreads();
+            if (kq == 0) {
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[t][r] += ksum[((cg * 3 + t) * 4 + r) * 64 + lane];
+            }
+        }
+
+        // bias, and the row statistics when a LayerNorm follows
+        float mean[4], rstd[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < 3; ++t) acc[t][r] += bias_v[t];
+        if (HAS_LN) {
+            // single-pass statistics over the whole row, as the reference's
+            // channel LayerNorm computes them (padding columns hold exact zeros)
+            float s1[4], s2[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s1[r] = (acc[0][r] + acc[1][r]) + acc[2][r];
+                s2[r] = (acc[0][r] * acc[0][r] + acc[1][r] * acc[1][r]) + acc[2][r] * acc[2][r];
+#pragma unroll
+                for (int o = 8; o >= 1; o >>= 1) {
+                    s1[r] += __shfl_xor(s1[r], o, 64);
+                    s2[r] += __shfl_xor(s2[r], o, 64);
+                }
+            }
+            if (kq == 0 && j == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    rstat[cg][4 * q + r][0] = s1[r];
+                    rstat[cg][4 * q + r][1] = s2[r];
+                }
+            }
+            __syncthreads();
+            const float invn = 1.0f / (float)(gc1 - gc0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float a1 = (rstat[0][4 * q + r][0] + rstat[1][4 * q + r][0]) +
+                                 (rstat[2][4 * q + r][0] + rstat[3][4 * q + r][0]);
+                const float a2 = (rstat[0][4 * q + r][1] + rstat[1][4 * q + r][1]) +
+                                 (rstat[2][4 * q + r][1] + rstat[3][4 * q + r][1]);
+                mean[r] = a1 * invn;
+                float var = a2 * invn - mean[r] * mean[r];
+                var = var > 0.f ? var : 0.f;
+                rstd[r] = 1.0f / sqrtf(var + 1e-5f);
+            }
+        }
+        if (kq == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + r;
+#pragma unroll
+                for (int t = 0; t < 3; ++t) {
+                    float v = acc[t][r];
+                    if (HAS_LN) v = (v - mean[r]) * rstd[r] * lnw[t] + lnb[t];
+                    if (EPI == EPI_GELU) v = gelu_erf(v);
+                    if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
+                    if (HAS_RES) v += rv[t][r];
+                    buf_store1(ro_rs, (m < g.M && cok[t]) ? (m * g.ldo + col[t]) * 4 : BUF_OOB, v);
+                }
+            }
+        }
+
+        if (nxt < ntask) lstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
     }
 }
 
@@ -790,7 +1071,123 @@ hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int varian
     }
 }
 
+// ---- k_bsgemm dispatch ----------------------------------------------------
+
+static int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            v <= 0) {
+            (void)hipGetLastError();
+            v = 256;
+        }
+        n = v;
+    }
+    return n;
+}
+
+// k_bsgemm takes a row GEMM whose K per wave is one it is built for (the
+// embed widths of the released checkpoints: 180 and 60, with K = 2*KPW split
+// over two wave sets).
+static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks) {
+    if (aload != ALOAD_ROWS || epi == EPI_SHUFFLE) return false;
+    if (g.lda % 4 || g.ldb % 4 || g.M <= 0 || g.N <= 0) return false;
+    if (g.K == 180 || g.K == 60) {
+        *kpw = g.K;
+        *ks = 1;
+    } else if (g.K == 360 || g.K == 120) {
+        *kpw = g.K / 2;
+        *ks = 2;
+    } else {
+        return false;
+    }
+    if ((epi == EPI_LN || epi == EPI_LN_RES) && g.N > 192) return false;
+    return true;
+}
+
+template <int KPW, int KS, int EPI>
+static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *grid_out) {
+    static int per_cu = 0;  // resident workgroups per CU, from the occupancy query
+    if (!per_cu) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_bsgemm<KPW, KS, EPI>, 256 * KS, 0) !=
+                hipSuccess ||
+            nb < 1) {
+            (void)hipGetLastError();
+            nb = 1;
+        }
+        per_cu = nb;
+    }
+    const int ng = (g.N + 191) / 192;
+    const int ngw = (g.N + ng - 1) / ng;
+    const int ntask = (g.M + 15) / 16;
+    int P = per_cu * cu_count() / ng;
+    if (P >= 8) P -= P % 8;
+    P = std::max(1, std::min(P, ntask));
+    const dim3 grid((unsigned)(P * ng));
+    if (grid_out) *grid_out = grid;
+    if (!launch) return hipSuccess;
+    BsArgs a{};
+    a.A = g.A;
+    a.lda = g.lda;
+    a.B = g.B;
+    a.ldb = g.ldb;
+    a.bias = g.bias;
+    a.out = g.out;
+    a.ldo = g.ldo;
+    a.res = g.res;
+    a.ldr = g.ldr;
+    a.ln_w = g.ln_w;
+    a.ln_b = g.ln_b;
+    a.slope = g.slope;
+    a.M = g.M;
+    a.N = g.N;
+    a.K = g.K;
+    a.P = P;
+    a.ngw = ngw;
+    hipLaunchKernelGGL((k_bsgemm<KPW, KS, EPI>), grid, dim3(256 * KS), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int KPW, int KS>
+static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool launch, dim3 *grid) {
+    switch (epi) {
+    case EPI_STORE: return run_bs<KPW, KS, EPI_STORE>(g, st, launch, grid);
+    case EPI_GELU: return run_bs<KPW, KS, EPI_GELU>(g, st, launch, grid);
+    case EPI_RES: return run_bs<KPW, KS, EPI_RES>(g, st, launch, grid);
+    case EPI_LN: return run_bs<KPW, KS, EPI_LN>(g, st, launch, grid);
+    case EPI_LN_RES: return run_bs<KPW, KS, EPI_LN_RES>(g, st, launch, grid);
+    case EPI_LRELU: return run_bs<KPW, KS, EPI_LRELU>(g, st, launch, grid);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+static hipError_t run_bs_any(const GemmArgs &g, int kpw, int ks, int epi, hipStream_t st,
+                             bool launch, dim3 *grid) {
+    if (kpw == 180) return ks == 1 ? run_bs_e<180, 1>(g, epi, st, launch, grid)
+                                   : run_bs_e<180, 2>(g, epi, st, launch, grid);
+    return ks == 1 ? run_bs_e<60, 1>(g, epi, st, launch, grid)
+                   : run_bs_e<60, 2>(g, epi, st, launch, grid);
+}
+
+void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block) {
+    int kpw, ks;
+    if (bs_eligible(g, aload, epi, &kpw, &ks)) {
+        (void)run_bs_any(g, kpw, ks, epi, 0, false, grid);
+        *block = dim3(256 * ks);
+        return;
+    }
+    unsigned gx, gy;
+    gemm_grid(g, aload, epi, &gx, &gy);
+    *grid = dim3(gx, gy);
+    *block = dim3(256);
+}
+
 hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
+    int kpw, ks;
+    if (bs_eligible(g, aload, epi, &kpw, &ks)) return run_bs_any(g, kpw, ks, epi, st, true, nullptr);
     return launch_gemm_variant(g, aload, epi, gemm_pick(g, aload, epi), st);
 }
 

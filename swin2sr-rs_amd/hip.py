@@ -85,6 +85,11 @@ class DeviceBuffer:
             pass
 
 
+def copy_device(dst: int, src: int, nbytes: int):
+    """Device-to-device hipMemcpy of `nbytes` (the runtime's plain copy kernel)."""
+    _chk(rt().hipMemcpy(C.c_void_p(dst), C.c_void_p(src), nbytes, D2D), "hipMemcpy D2D")
+
+
 def synchronize():
     _chk(rt().hipDeviceSynchronize(), "hipDeviceSynchronize")
 

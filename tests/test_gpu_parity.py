@@ -91,7 +91,8 @@ def test_cpb_table(pkg, orc):
 
 
 @pytest.mark.parametrize("rows,cin,cout", [(37, 60, 43), (300, 180, 180), (513, 180, 540),
-                                           (200, 360, 180), (130, 180, 360), (97, 27, 64)])
+                                           (200, 360, 180), (130, 180, 360), (97, 27, 64),
+                                           (150, 120, 60), (20011, 180, 540), (17003, 360, 180)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 5])
 def test_linear(pkg, orc, rows, cin, cout, epi):
     r = rng(rows + cin + cout + epi)
@@ -113,7 +114,8 @@ def test_linear(pkg, orc, rows, cin, cout, epi):
     assert err < 3e-5 * max(1.0, np.abs(want).max()), err
 
 
-@pytest.mark.parametrize("rows,cin,cout", [(37, 60, 60), (300, 180, 180), (129, 360, 180)])
+@pytest.mark.parametrize("rows,cin,cout", [(37, 60, 60), (300, 180, 180), (129, 360, 180),
+                                           (70, 120, 60), (23001, 180, 180), (19005, 360, 180)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_linear_layernorm(pkg, orc, rows, cin, cout, with_res):
     r = rng(rows * 7 + cin + with_res)
