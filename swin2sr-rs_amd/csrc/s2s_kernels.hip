@@ -340,7 +340,7 @@ __device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, fl
 }
 
 template <int KPW, int KS, int EPI>
-__global__ __launch_bounds__(256 * KS) void k_bsgemm(BsArgs g) {
+__global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int NT = 256 * KS;
     constexpr int G = KPW / 16;
     constexpr int R = (KPW % 16) / 4;
@@ -401,9 +401,6 @@ __global__ __launch_bounds__(256 * KS) void k_bsgemm(BsArgs g) {
         lnw[t] = (HAS_LN && cok[t]) ? g.ln_w[cc] : 0.f;
         lnb[t] = (HAS_LN && cok[t]) ? g.ln_b[cc] : 0.f;
     }
-    // Retire the weight loads here, once.
-    __builtin_amdgcn_s_waitcnt(0);
-
     const int ntask = (g.M + 15) >> 4;
     float4 ra[NL];
     // A tile of task `task`: always NL loads per thread (rows past M read 0;
@@ -419,24 +416,26 @@ __global__ __launch_bounds__(256 * KS) void k_bsgemm(BsArgs g) {
             ra[u] = buf_load4(ra_rs, m < g.M ? (m * g.lda + 4 * c4) * 4 : BUF_OOB);
         }
     };
+    // (unconditional: a lane past the tile rewrites the float4 it re-read,
+    // with the value it already holds, so every path retires every load)
     auto lstore = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < NL; ++u) {
-            const int idx = tid + u * NT;
-            if (idx < V4) {
-                const int row = idx / (KT / 4);
-                const int c4 = idx - row * (KT / 4);
-                *reinterpret_cast<float4 *>(&As[buf][row * SA + 4 * c4]) = ra[u];
-            }
+            int idx = tid + u * NT;
+            if (NL * NT > V4) idx = idx < V4 ? idx : idx - V4;
+            const int row = idx / (KT / 4);
+            const int c4 = idx - row * (KT / 4);
+            *reinterpret_cast<float4 *>(&As[buf][row * SA + 4 * c4]) = ra[u];
         }
     };
 
     int task = p;
     int buf = 0;
-    if (task < ntask) {
-        gload(task);
-        lstore(0);
-    }
+    // the first A tile is in flight together with the weight loads; then
+    // everything is retired once, so no later wait has to count these
+    if (task < ntask) gload(task);
+    __builtin_amdgcn_s_waitcnt(0);
+    if (task < ntask) lstore(0);
     __syncthreads();
     for (; task < ntask; task += g.P) {
         const int nxt = task + g.P;
@@ -454,6 +453,8 @@ __global__ __launch_bounds__(256 * KS) void k_bsgemm(BsArgs g) {
                                                     : BUF_OOB);
         }
         gload(nxt < ntask ? nxt : task);
+        // keep these loads at the top: their latency hides under the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
 
         f4v acc[3];
 #pragma unroll
@@ -549,7 +550,7 @@ __global__ __launch_bounds__(256 * KS) void k_bsgemm(BsArgs g) {
             }
         }
 
-        if (nxt < ntask) lstore(buf ^ 1);
+        lstore(buf ^ 1);
         __syncthreads();
         buf ^= 1;
     }
