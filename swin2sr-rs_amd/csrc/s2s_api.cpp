@@ -352,7 +352,7 @@ int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *
     a.head_dim = hd;
     a.c = c;
     a.shift = shift;
-    unsigned ag = (unsigned)((a.nw * a.heads + 3) / 4);
+    const unsigned ag = attention_grid(a);
     if (run("window_attention", dim3(ag), dim3(256),
             [&] { return launch_attention(a, stream, nullptr); }))
         return -1;

@@ -77,6 +77,7 @@ const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi);
 // profiler's rows), and the kernel family name it picks.
 void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block);
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out);
+unsigned attention_grid(const AttnArgs &g);
 hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
                             hipStream_t st);
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,

@@ -794,6 +794,241 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// k_wattn: the same window attention, one workgroup per (window, head pair).
+//
+// The window's q, k and v slices of its two heads (64 tokens x 3 x 2*hd floats)
+// are loaded once with coalesced float4 loads - each token's slice is a
+// contiguous 8*hd-byte run of its qkv row - into LDS, [token][q | k | v] rows of
+// 6*hd + 2 floats (an odd number of float2s, so 16 consecutive rows read by a
+// ds_read_b64 land in distinct bank pairs). Wave w handles head 2*hg + w/2 and
+// query tile w%2 (32 queries):
+//   - its q row and the 64 k rows come out of LDS as MFMA operands (step j of
+//     lane half hh covers d = 4(j/2) + 2hh + j%2, then d = hd-2+hh for the odd
+//     tail pair), scaled in registers by exp(min(ls, ln 100))/|q| and 1/|k|;
+//   - S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x2f32 with the softmax in
+//     registers between them, as in k_attention; the bias table values a lane
+//     needs are loaded once (32 floats);
+//   - O^T goes back into the wave's own q rows of the LDS tile (no other wave
+//     reads them), and after one barrier the workgroup writes the window's
+//     output slices with coalesced float4 stores.
+// Three workgroups fit a CU (46.6 KB of LDS each at hd = 30), so one
+// workgroup's loads overlap the others' MFMAs.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256, 3) void k_wattn(AttnArgs g) {
+    static_assert(HD % 2 == 0 && HD <= 32, "even head_dim <= 32");
+    constexpr int NS = HD / 2;          // MFMA k-steps over d
+    constexpr int G4 = HD / 4;          // float2 pairs of steps
+    constexpr bool TAIL = (HD % 4) != 0;
+    constexpr int W = 2 * HD;           // floats per segment (two heads)
+    constexpr int RS = 6 * HD + 2;      // LDS row stride
+    constexpr int V4MAX = W / 4;        // float4s per segment
+    constexpr int NLD = (64 * 3 * V4MAX + 255) / 256;
+    __shared__ float tile[64 * RS];
+
+    const int HG = (g.heads + 1) >> 1;
+    const int hg = blockIdx.x % HG;
+    const int wi = blockIdx.x / HG;
+    const int nh = min(2, g.heads - 2 * hg);
+    const int v4 = nh * HD / 4;         // float4s per segment in this group
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hl = wave >> 1;
+    const int qt = wave & 1;
+    const int r = lane & 31;
+    const int hh = lane >> 5;
+    const int wh = wi / g.nww;
+    const int ww = wi - wh * g.nww;
+    const int shift = g.shift;
+    const int head = 2 * hg + hl;
+    const bool active = hl < nh;
+    const size_t ld = (size_t)3 * g.c;
+
+    // ---- the window's slices -> LDS (all loads in flight together) ----
+    // Element i of the copy is (token, segment, float4) with compile-time
+    // divisors; a one-head group skips the second head's float4s.
+    {
+        constexpr int PER_TOK = 3 * V4MAX;
+        float4 buf[NLD];
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) {
+            const int i = tid + 256 * u;
+            const int tok = i / PER_TOK;
+            const int rem = i - tok * PER_TOK;
+            const int seg = rem / V4MAX;
+            const int c4 = rem - seg * V4MAX;
+            buf[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (tok < 64 && c4 < v4) {
+                const int pix = win_pixel(wh, ww, tok, shift, g.hp, g.wp);
+                buf[u] = *reinterpret_cast<const float4 *>(g.qkv + (size_t)pix * ld + seg * g.c +
+                                                           2 * hg * HD + 4 * c4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) {
+            const int i = tid + 256 * u;
+            const int tok = i / PER_TOK;
+            const int rem = i - tok * PER_TOK;
+            const int seg = rem / V4MAX;
+            const int c4 = rem - seg * V4MAX;
+            if (tok < 64) {
+                float *dst = tile + tok * RS + seg * W + 4 * c4;
+                *reinterpret_cast<float2 *>(dst) = make_float2(buf[u].x, buf[u].y);
+                *reinterpret_cast<float2 *>(dst + 2) = make_float2(buf[u].z, buf[u].w);
+            }
+        }
+    }
+    // the bias values this lane adds: query 32qt + r, keys 32kt + 8a + 4hh + b
+    float bias[2][16];
+    if (active) {
+        const float *cp = g.cpbt + ((size_t)head * 64 + 32 * qt + r) * 64;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float4 b4 = *reinterpret_cast<const float4 *>(cp + 32 * kt + 8 * a + 4 * hh);
+                bias[kt][4 * a + 0] = b4.x;
+                bias[kt][4 * a + 1] = b4.y;
+                bias[kt][4 * a + 2] = b4.z;
+                bias[kt][4 * a + 3] = b4.w;
+            }
+    }
+    __syncthreads();
+
+    if (active) {
+        const float ls = __expf(fminf(g.logit_scale[head], 4.605170185988092f));
+        // q operands (this lane's query, its half of d), normalised and scaled
+        float qop[NS];
+        {
+            const float *qrow = tile + (32 * qt + r) * RS + hl * HD;
+#pragma unroll
+            for (int s2 = 0; s2 < G4; ++s2) {
+                const float2 v = *reinterpret_cast<const float2 *>(qrow + 4 * s2 + 2 * hh);
+                qop[2 * s2] = v.x;
+                qop[2 * s2 + 1] = v.y;
+            }
+            if (TAIL) qop[NS - 1] = qrow[4 * G4 + hh];
+            float qs = 0.f;
+#pragma unroll
+            for (int j = 0; j < NS; ++j) qs += qop[j] * qop[j];
+            qs += __shfl_xor(qs, 32, 64);
+            const float qsc = ls / fmaxf(sqrtf(qs), 1e-12f);
+#pragma unroll
+            for (int j = 0; j < NS; ++j) qop[j] *= qsc;
+        }
+        float kop[2][NS];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const float *krow = tile + (32 * kt + r) * RS + W + hl * HD;
+#pragma unroll
+            for (int s2 = 0; s2 < G4; ++s2) {
+                const float2 v = *reinterpret_cast<const float2 *>(krow + 4 * s2 + 2 * hh);
+                kop[kt][2 * s2] = v.x;
+                kop[kt][2 * s2 + 1] = v.y;
+            }
+            if (TAIL) kop[kt][NS - 1] = krow[4 * G4 + hh];
+            float ks = 0.f;
+#pragma unroll
+            for (int j = 0; j < NS; ++j) ks += kop[kt][j] * kop[kt][j];
+            ks += __shfl_xor(ks, 32, 64);
+            const float ksc = 1.0f / fmaxf(sqrtf(ks), 1e-12f);
+#pragma unroll
+            for (int j = 0; j < NS; ++j) kop[kt][j] *= ksc;
+        }
+
+        f16v s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[kt][e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) s[kt] = MFMA32(kop[kt][j], qop[j], s[kt]);
+
+        // bias, shift mask, softmax over the query's 64 keys (2 lanes). The
+        // mask bands (win_band) are all 0 except in the last window row and
+        // column of a shifted block, where a token's band is 1 or 2 by whether
+        // its row (column) inside the window is below 8 - shift.
+        const int qtok = 32 * qt + r;
+        const bool ey = shift && (wh * 8 + 8 >= g.hp);
+        const bool ex = shift && (ww * 8 + 8 >= g.wp);
+        const bool qy = (qtok >> 3) < 8 - shift;
+        const bool qx = (qtok & 7) < 8 - shift;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float v = s[kt][e] + bias[kt][e];
+                if (ey || ex) {
+                    const int krow = 4 * kt + (e >> 2);        // key >> 3
+                    const int kcol = 4 * hh + (e & 3);         // key & 7
+                    const bool dy = ey && ((krow < 8 - shift) != qy);
+                    const bool dx = ex && ((kcol < 8 - shift) != qx);
+                    if (dy || dx) v -= 100.f;
+                }
+                s[kt][e] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float sum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = __expf(s[kt][e] - mx);
+                s[kt][e] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 32, 64);
+        const float inv = 1.0f / sum;
+
+        // O^T = V^T P^T: lane r supplies V[key][d = r]
+        f16v o;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = 0.f;
+        const float *vcol = tile + 2 * W + hl * HD + r;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+                const float vv = (r < HD) ? vcol[key * RS] : 0.f;
+                o = MFMA32(vv, s[kt][e], o);
+            }
+        // into this wave's own q rows (no other wave reads them)
+        float *orow = tile + qtok * RS + hl * HD;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
+            if (d < HD) orow[d] = o[e] * inv;
+        }
+    }
+    __syncthreads();
+
+    // ---- the window's output slices, coalesced ----
+    {
+        constexpr int NST = (64 * V4MAX + 255) / 256;
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const int i = tid + 256 * u;
+            const int tok = i / V4MAX;
+            const int c4 = i - tok * V4MAX;
+            if (tok < 64 && c4 < v4) {
+                const float *src = tile + tok * RS + 4 * c4;
+                const float2 a = *reinterpret_cast<const float2 *>(src);
+                const float2 b = *reinterpret_cast<const float2 *>(src + 2);
+                const int pix = win_pixel(wh, ww, tok, shift, g.hp, g.wp);
+                *reinterpret_cast<float4 *>(g.out + (size_t)pix * g.c + 2 * hg * HD + 4 * c4) =
+                    make_float4(a.x, a.y, b.x, b.y);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Streaming kernels.
 // ---------------------------------------------------------------------------
 
@@ -1192,11 +1427,37 @@ hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
     return launch_gemm_variant(g, aload, epi, gemm_pick(g, aload, epi), st);
 }
 
+// k_wattn takes every even head_dim it is built for whose head-pair slices are
+// float4-aligned (all released checkpoints: 30 and 10); k_attention the rest.
+static bool wattn_eligible(const AttnArgs &g) {
+    const int hd = g.head_dim;
+    if (hd != 2 && hd != 10 && hd != 30 && hd != 32) return false;
+    if ((2 * hd) % 4 || g.c % 4) return false;
+    if ((g.heads & 1) && hd % 4) return false;  // a lone last head's slice must be float4s
+    return true;
+}
+
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out) {
+    if (wattn_eligible(g)) {
+        const unsigned grid = (unsigned)(g.nw * ((g.heads + 1) / 2));
+        if (grid_out) *grid_out = grid;
+        switch (g.head_dim) {
+        case 2: hipLaunchKernelGGL(k_wattn<2>, dim3(grid), dim3(256), 0, st, g); break;
+        case 10: hipLaunchKernelGGL(k_wattn<10>, dim3(grid), dim3(256), 0, st, g); break;
+        case 30: hipLaunchKernelGGL(k_wattn<30>, dim3(grid), dim3(256), 0, st, g); break;
+        default: hipLaunchKernelGGL(k_wattn<32>, dim3(grid), dim3(256), 0, st, g); break;
+        }
+        return hipGetLastError();
+    }
     const unsigned grid = (unsigned)((g.nw * g.heads + 3) / 4);
     if (grid_out) *grid_out = grid;
     hipLaunchKernelGGL(k_attention, dim3(grid), dim3(256), 0, st, g);
     return hipGetLastError();
+}
+
+unsigned attention_grid(const AttnArgs &g) {
+    return wattn_eligible(g) ? (unsigned)(g.nw * ((g.heads + 1) / 2))
+                             : (unsigned)((g.nw * g.heads + 3) / 4);
 }
 
 hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
