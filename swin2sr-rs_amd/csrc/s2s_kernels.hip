@@ -339,29 +339,65 @@ __device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, fl
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
 }
 
-template <int KPW, int KS, int EPI>
+// Direct global -> LDS copy (gfx950 buffer_load_dwordx4 ... lds): lane l of the
+// wave writes its 16 bytes at lds + 16*l, so one instruction moves a contiguous
+// 1 KiB chunk without staging it in VGPRs. Out-of-range offsets write zeros.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float *lds, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                             off, 0, 0, 0);
+}
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
+// expcnt and lgkmcnt left at their maxima).
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
+// A workgroup barrier for LDS traffic only: this wave's LDS writes retired
+// (lgkmcnt(0)), then s_barrier, with compiler fences on both sides. Unlike
+// __syncthreads() it does not drain outstanding global stores (its release
+// fence does), so a task's output stores and the next task's copies stay in
+// flight across it. Data copied into LDS by DMA is covered by a WAIT_VMCNT
+// before the barrier.
+__device__ __forceinline__ void lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int KPW, int KS, int RB, int EPI>
 __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int NT = 256 * KS;
+    constexpr int NW = 4 * KS;                 // waves
+    constexpr int TR = 16 * RB;                // rows per task
     constexpr int G = KPW / 16;
     constexpr int R = (KPW % 16) / 4;
     constexpr int S = KPW / 4;
     constexpr int KT = KPW * KS;
-    constexpr int SA = bs_lds_stride(KT);
-    constexpr int V4 = 16 * KT / 4;            // float4s per A tile
-    constexpr int NL = (V4 + NT - 1) / NT;     // per thread
     constexpr bool HAS_RES = EPI == EPI_RES || EPI == EPI_LN_RES;
     constexpr bool HAS_LN = EPI == EPI_LN || EPI == EPI_LN_RES;
+    // A tile: TR rows x KT floats, contiguous in HBM and in LDS; copied in
+    // 1 KiB chunks, NCA per wave
+    constexpr int CA = (TR * KT * 4 + 1023) / 1024;
+    constexpr int NCA = (CA + NW - 1) / NW;
+    constexpr int ATILE = NCA * NW * 256;      // floats reserved per buffer
+    // residual tile: TR rows x N (<= 192) floats
+    constexpr int CR = HAS_RES ? (TR * 192 * 4 + 1023) / 1024 : 0;
+    constexpr int NCR = HAS_RES ? (CR + NW - 1) / NW : 0;
+    constexpr int RTILE = HAS_RES ? NCR * NW * 256 : 1;
+    constexpr int NSTORE = 4 * 3 * RB;         // buffer stores per lane per task
     static_assert(KPW % 4 == 0, "K must be a multiple of 4");
 
-    __shared__ float As[2][16 * SA];
-    __shared__ float ksum[KS == 2 ? 4 * 3 * 4 * 64 : 1];
-    __shared__ float rstat[4][16][2];
+    // two separate arrays, not one [2][..]: the compiler then knows that the
+    // copy into one cannot alias reads of the other and does not wait for it
+    __shared__ __attribute__((aligned(16))) float As0[ATILE];
+    __shared__ __attribute__((aligned(16))) float As1[ATILE];
+    __shared__ __attribute__((aligned(16))) float Rs[RTILE];
+    __shared__ float ksum[KS == 2 ? 4 * RB * 3 * 4 * 64 : 1];
+    __shared__ float rstat[4][TR][2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int cg = wave & 3;
-    const int kq = wave >> 2;
+    const int kq = KS == 1 ? 0 : wave >> 2;
     const int j = lane & 15;
     const int q = lane >> 4;
     const int ng = blockIdx.x / g.P;
@@ -401,158 +437,179 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         lnw[t] = (HAS_LN && cok[t]) ? g.ln_w[cc] : 0.f;
         lnb[t] = (HAS_LN && cok[t]) ? g.ln_b[cc] : 0.f;
     }
-    const int ntask = (g.M + 15) >> 4;
-    float4 ra[NL];
-    // A tile of task `task`: always NL loads per thread (rows past M read 0;
-    // the few lanes past the tile re-read its first float4 and are not stored)
-    auto gload = [&](int task) {
+
+    const int ntask = (g.M + TR - 1) / TR;
+    // chunk c of a task's tile goes to wave c % NW; every wave issues the same
+    // count, chunks past the tile read whatever follows it into LDS padding
+    auto dma_a = [&](int task, float *dst) {
 #pragma unroll
-        for (int u = 0; u < NL; ++u) {
-            int idx = tid + u * NT;
-            if (NL * NT > V4) idx = idx < V4 ? idx : idx - V4;
-            const int row = idx / (KT / 4);
-            const int c4 = idx - row * (KT / 4);
-            const int m = task * 16 + row;
-            ra[u] = buf_load4(ra_rs, m < g.M ? (m * g.lda + 4 * c4) * 4 : BUF_OOB);
+        for (int u = 0; u < NCA; ++u) {
+            const int c = wave + NW * u;
+            dma16(ra_rs, dst + c * 256, (task * TR * g.lda + c * 256 + 4 * lane) * 4);
         }
     };
-    // (unconditional: a lane past the tile rewrites the float4 it re-read,
-    // with the value it already holds, so every path retires every load)
-    auto lstore = [&](int buf) {
+    auto dma_r = [&](int task) {
 #pragma unroll
-        for (int u = 0; u < NL; ++u) {
-            int idx = tid + u * NT;
-            if (NL * NT > V4) idx = idx < V4 ? idx : idx - V4;
-            const int row = idx / (KT / 4);
-            const int c4 = idx - row * (KT / 4);
-            *reinterpret_cast<float4 *>(&As[buf][row * SA + 4 * c4]) = ra[u];
+        for (int u = 0; u < NCR; ++u) {
+            const int c = wave + NW * u;
+            dma16(rr_rs, &Rs[c * 256], (task * TR * g.ldr + c * 256 + 4 * lane) * 4);
         }
     };
 
-    int task = p;
-    int buf = 0;
-    // the first A tile is in flight together with the weight loads; then
-    // everything is retired once, so no later wait has to count these
-    if (task < ntask) gload(task);
-    __builtin_amdgcn_s_waitcnt(0);
-    if (task < ntask) lstore(0);
-    __syncthreads();
-    for (; task < ntask; task += g.P) {
+    // One task: multiply the tile in `cur` while the next task's tile streams
+    // into `nxt_buf`, then the epilogue. Called with the two arrays swapped on
+    // alternate tasks, always with compile-time-known arrays.
+    auto body = [&](int task, const float *cur, float *nxt_buf) __attribute__((always_inline)) {
         const int nxt = task + g.P;
-        const int m0 = task * 16 + 4 * q;
-        // this task's residual first, then the next task's A tile: both are in
-        // flight while this task multiplies
-        float rv[3][4];
-        if (HAS_RES) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int t = 0; t < 3; ++t)
-                    rv[t][r] = buf_load1(rr_rs, (m0 + r < g.M && cok[t])
-                                                    ? ((m0 + r) * g.ldr + col[t]) * 4
-                                                    : BUF_OOB);
-        }
-        gload(nxt < ntask ? nxt : task);
-        // keep these loads at the top: their latency hides under the MFMAs
-        __builtin_amdgcn_sched_barrier(0);
+        dma_a(nxt < ntask ? nxt : task, nxt_buf);
 
-        f4v acc[3];
+        f4v acc[RB][3];
 #pragma unroll
-        for (int t = 0; t < 3; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
-        const float *arow = &As[buf][j * SA + kbase];
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int t = 0; t < 3; ++t) acc[rb][t] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
-            const float4 a = *reinterpret_cast<const float4 *>(arow + 16 * gi + 4 * q);
-            const float av[4] = {a.x, a.y, a.z, a.w};
+            float av[RB][4];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const float4 a = *reinterpret_cast<const float4 *>(
+                    &cur[(rb * 16 + j) * KT + kbase + 16 * gi + 4 * q]);
+                av[rb][0] = a.x;
+                av[rb][1] = a.y;
+                av[rb][2] = a.z;
+                av[rb][3] = a.w;
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int t = 0; t < 3; ++t) acc[t] = MFMA16(av[i], bw[t][4 * gi + i], acc[t]);
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int t = 0; t < 3; ++t)
+                        acc[rb][t] = MFMA16(av[rb][i], bw[t][4 * gi + i], acc[rb][t]);
         }
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-            const float a = arow[16 * G + R * q + i];
 #pragma unroll
-            for (int t = 0; t < 3; ++t) acc[t] = MFMA16(a, bw[t][4 * G + i], acc[t]);
+            for (int rb = 0; rb < RB; ++rb) {
+                const float a = cur[(rb * 16 + j) * KT + kbase + 16 * G + R * q + i];
+#pragma unroll
+                for (int t = 0; t < 3; ++t) acc[rb][t] = MFMA16(a, bw[t][4 * G + i], acc[rb][t]);
+            }
         }
 
         if (KS == 2) {
             // the second K half's partial sums meet the first's in LDS
             if (kq == 1) {
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
+                for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ksum[((cg * 3 + t) * 4 + r) * 64 + lane] = acc[t][r];
+                    for (int t = 0; t < 3; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            ksum[(((cg * RB + rb) * 3 + t) * 4 + r) * 64 + lane] = acc[rb][t][r];
             }
-            __syncthreads();
+            lds_sync();
             if (kq == 0) {
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
+                for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[t][r] += ksum[((cg * 3 + t) * 4 + r) * 64 + lane];
+                    for (int t = 0; t < 3; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[rb][t][r] += ksum[(((cg * RB + rb) * 3 + t) * 4 + r) * 64 + lane];
             }
         }
 
-        // bias, and the row statistics when a LayerNorm follows
-        float mean[4], rstd[4];
+        // the residual tile (copied during the previous task) has landed once
+        // everything but this task's A-tile chunks has
+        if (HAS_RES) WAIT_VMCNT(NCA);
+        float mean[RB][4], rstd[RB][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int t = 0; t < 3; ++t) acc[t][r] += bias_v[t];
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int t = 0; t < 3; ++t) acc[rb][t][r] += bias_v[t];
         if (HAS_LN) {
             // single-pass statistics over the whole row, as the reference's
             // channel LayerNorm computes them (padding columns hold exact zeros)
-            float s1[4], s2[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                s1[r] = (acc[0][r] + acc[1][r]) + acc[2][r];
-                s2[r] = (acc[0][r] * acc[0][r] + acc[1][r] * acc[1][r]) + acc[2][r] * acc[2][r];
-#pragma unroll
-                for (int o = 8; o >= 1; o >>= 1) {
-                    s1[r] += __shfl_xor(s1[r], o, 64);
-                    s2[r] += __shfl_xor(s2[r], o, 64);
-                }
-            }
-            if (kq == 0 && j == 0) {
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    rstat[cg][4 * q + r][0] = s1[r];
-                    rstat[cg][4 * q + r][1] = s2[r];
+                    float s1 = (acc[rb][0][r] + acc[rb][1][r]) + acc[rb][2][r];
+                    float s2 = (acc[rb][0][r] * acc[rb][0][r] + acc[rb][1][r] * acc[rb][1][r]) +
+                               acc[rb][2][r] * acc[rb][2][r];
+#pragma unroll
+                    for (int o = 8; o >= 1; o >>= 1) {
+                        s1 += __shfl_xor(s1, o, 64);
+                        s2 += __shfl_xor(s2, o, 64);
+                    }
+                    if (kq == 0 && j == 0) {
+                        rstat[cg][rb * 16 + 4 * q + r][0] = s1;
+                        rstat[cg][rb * 16 + 4 * q + r][1] = s2;
+                    }
                 }
-            }
-            __syncthreads();
+        }
+        if (HAS_LN || HAS_RES) lds_sync();
+        if (HAS_LN) {
             const float invn = 1.0f / (float)(gc1 - gc0);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float a1 = (rstat[0][4 * q + r][0] + rstat[1][4 * q + r][0]) +
-                                 (rstat[2][4 * q + r][0] + rstat[3][4 * q + r][0]);
-                const float a2 = (rstat[0][4 * q + r][1] + rstat[1][4 * q + r][1]) +
-                                 (rstat[2][4 * q + r][1] + rstat[3][4 * q + r][1]);
-                mean[r] = a1 * invn;
-                float var = a2 * invn - mean[r] * mean[r];
-                var = var > 0.f ? var : 0.f;
-                rstd[r] = 1.0f / sqrtf(var + 1e-5f);
-            }
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = rb * 16 + 4 * q + r;
+                    const float a1 = (rstat[0][row][0] + rstat[1][row][0]) +
+                                     (rstat[2][row][0] + rstat[3][row][0]);
+                    const float a2 = (rstat[0][row][1] + rstat[1][row][1]) +
+                                     (rstat[2][row][1] + rstat[3][row][1]);
+                    mean[rb][r] = a1 * invn;
+                    float var = a2 * invn - mean[rb][r] * mean[rb][r];
+                    var = var > 0.f ? var : 0.f;
+                    rstd[rb][r] = 1.0f / sqrtf(var + 1e-5f);
+                }
         }
-        if (kq == 0) {
+        // every wave issues the same stores (the second K half's go out of
+        // range and are dropped), so the memory counters stay countable
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + r;
+                const int row = rb * 16 + 4 * q + r;
+                const int m = task * TR + row;
 #pragma unroll
                 for (int t = 0; t < 3; ++t) {
-                    float v = acc[t][r];
-                    if (HAS_LN) v = (v - mean[r]) * rstd[r] * lnw[t] + lnb[t];
+                    float v = acc[rb][t][r];
+                    if (HAS_LN) v = (v - mean[rb][r]) * rstd[rb][r] * lnw[t] + lnb[t];
                     if (EPI == EPI_GELU) v = gelu_erf(v);
                     if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
-                    if (HAS_RES) v += rv[t][r];
-                    buf_store1(ro_rs, (m < g.M && cok[t]) ? (m * g.ldo + col[t]) * 4 : BUF_OOB, v);
+                    if (HAS_RES) v += Rs[row * g.ldr + (cok[t] ? col[t] : gc0)];
+                    buf_store1(ro_rs,
+                               (kq == 0 && m < g.M && cok[t]) ? (m * g.ldo + col[t]) * 4 : BUF_OOB, v);
                 }
             }
-        }
+        // all reads of this task's A tile and residual are done past here
+        lds_sync();
+        if (HAS_RES) dma_r(nxt < ntask ? nxt : task);
+        // the next A tile: outstanding are [its chunks][stores][residual chunks]
+        WAIT_VMCNT(NSTORE + NCR);
+        lds_sync();
+    };
 
-        lstore(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
+    int task = p;
+    if (task < ntask) {
+        dma_a(task, As0);
+        if (HAS_RES) dma_r(task);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_sync();
+    while (task < ntask) {
+        body(task, As0, As1);
+        task += g.P;
+        if (task >= ntask) break;
+        body(task, As1, As0);
+        task += g.P;
     }
 }
 
@@ -1330,6 +1387,9 @@ static int cu_count() {
 static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks) {
     if (aload != ALOAD_ROWS || epi == EPI_SHUFFLE) return false;
     if (g.lda % 4 || g.ldb % 4 || g.M <= 0 || g.N <= 0) return false;
+    // the A tile (and the residual tile) are copied as contiguous blocks
+    if (g.lda != g.K) return false;
+    if ((epi == EPI_RES || epi == EPI_LN_RES) && (g.ldr != g.N || g.N > 192)) return false;
     if (g.K == 180 || g.K == 60) {
         *kpw = g.K;
         *ks = 1;
@@ -1343,13 +1403,13 @@ static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks
     return true;
 }
 
-template <int KPW, int KS, int EPI>
+template <int KPW, int KS, int RB, int EPI>
 static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *grid_out) {
     static int per_cu = 0;  // resident workgroups per CU, from the occupancy query
     if (!per_cu) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_bsgemm<KPW, KS, EPI>, 256 * KS, 0) !=
-                hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_bsgemm<KPW, KS, RB, EPI>, 256 * KS,
+                                                         0) != hipSuccess ||
             nb < 1) {
             (void)hipGetLastError();
             nb = 1;
@@ -1358,7 +1418,7 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     }
     const int ng = (g.N + 191) / 192;
     const int ngw = (g.N + ng - 1) / ng;
-    const int ntask = (g.M + 15) / 16;
+    const int ntask = (g.M + 16 * RB - 1) / (16 * RB);
     int P = per_cu * cu_count() / ng;
     if (P >= 8) P -= P % 8;
     P = std::max(1, std::min(P, ntask));
@@ -1383,29 +1443,46 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     a.K = g.K;
     a.P = P;
     a.ngw = ngw;
-    hipLaunchKernelGGL((k_bsgemm<KPW, KS, EPI>), grid, dim3(256 * KS), 0, st, a);
+    hipLaunchKernelGGL((k_bsgemm<KPW, KS, RB, EPI>), grid, dim3(256 * KS), 0, st, a);
     return hipGetLastError();
 }
 
-template <int KPW, int KS>
+template <int KPW, int KS, int RB>
 static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool launch, dim3 *grid) {
     switch (epi) {
-    case EPI_STORE: return run_bs<KPW, KS, EPI_STORE>(g, st, launch, grid);
-    case EPI_GELU: return run_bs<KPW, KS, EPI_GELU>(g, st, launch, grid);
-    case EPI_RES: return run_bs<KPW, KS, EPI_RES>(g, st, launch, grid);
-    case EPI_LN: return run_bs<KPW, KS, EPI_LN>(g, st, launch, grid);
-    case EPI_LN_RES: return run_bs<KPW, KS, EPI_LN_RES>(g, st, launch, grid);
-    case EPI_LRELU: return run_bs<KPW, KS, EPI_LRELU>(g, st, launch, grid);
+    case EPI_STORE: return run_bs<KPW, KS, RB, EPI_STORE>(g, st, launch, grid);
+    case EPI_GELU: return run_bs<KPW, KS, RB, EPI_GELU>(g, st, launch, grid);
+    case EPI_RES: return run_bs<KPW, KS, RB, EPI_RES>(g, st, launch, grid);
+    case EPI_LN: return run_bs<KPW, KS, RB, EPI_LN>(g, st, launch, grid);
+    case EPI_LN_RES: return run_bs<KPW, KS, RB, EPI_LN_RES>(g, st, launch, grid);
+    case EPI_LRELU: return run_bs<KPW, KS, RB, EPI_LRELU>(g, st, launch, grid);
     default: return hipErrorInvalidValue;
     }
 }
 
+// Rows per task: 32 (twice the MFMA work per task for the same per-task
+// overhead) where the task count still divides well over the workgroups
+// (several column groups) and the epilogue leaves room in the register file;
+// 16 otherwise.
+static int bs_rb(const GemmArgs &g, int ks, int epi) {
+    const int ng = (g.N + 191) / 192;
+    const bool ln = epi == EPI_LN || epi == EPI_LN_RES;
+    return (ng >= 2 && !ln) ? 2 : 1;
+}
+
 static hipError_t run_bs_any(const GemmArgs &g, int kpw, int ks, int epi, hipStream_t st,
                              bool launch, dim3 *grid) {
-    if (kpw == 180) return ks == 1 ? run_bs_e<180, 1>(g, epi, st, launch, grid)
-                                   : run_bs_e<180, 2>(g, epi, st, launch, grid);
-    return ks == 1 ? run_bs_e<60, 1>(g, epi, st, launch, grid)
-                   : run_bs_e<60, 2>(g, epi, st, launch, grid);
+    const int rb = bs_rb(g, ks, epi);
+    if (kpw == 180) {
+        if (ks == 1) return rb == 1 ? run_bs_e<180, 1, 1>(g, epi, st, launch, grid)
+                                    : run_bs_e<180, 1, 2>(g, epi, st, launch, grid);
+        return rb == 1 ? run_bs_e<180, 2, 1>(g, epi, st, launch, grid)
+                       : run_bs_e<180, 2, 2>(g, epi, st, launch, grid);
+    }
+    if (ks == 1) return rb == 1 ? run_bs_e<60, 1, 1>(g, epi, st, launch, grid)
+                                : run_bs_e<60, 1, 2>(g, epi, st, launch, grid);
+    return rb == 1 ? run_bs_e<60, 2, 1>(g, epi, st, launch, grid)
+                   : run_bs_e<60, 2, 2>(g, epi, st, launch, grid);
 }
 
 void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block) {
