@@ -27,6 +27,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "s2s_kernels.h"
 
@@ -362,6 +363,20 @@ __device__ __forceinline__ void lds_sync() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Sum over the 16 lanes of a DPP row, every lane receiving the total: four
+// DPP moves on the VALU (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror) instead of LDS-routed lane shuffles.
+#define DPP_ADD(v, ctrl)                                                                       \
+    ((v) + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), \
+                                                              (ctrl), 0xF, 0xF, true)))
+__device__ __forceinline__ float row16_sum(float v) {
+    v = DPP_ADD(v, 0xB1);
+    v = DPP_ADD(v, 0x4E);
+    v = DPP_ADD(v, 0x141);
+    v = DPP_ADD(v, 0x140);
+    return v;
+}
+
 template <int KPW, int KS, int RB, int EPI>
 __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int NT = 256 * KS;
@@ -384,14 +399,18 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int RTILE = HAS_RES ? NCR * NW * 256 : 1;
     constexpr int NSTORE = 4 * 3 * RB;         // buffer stores per lane per task
     static_assert(KPW % 4 == 0, "K must be a multiple of 4");
+    (void)NT;
 
-    // two separate arrays, not one [2][..]: the compiler then knows that the
-    // copy into one cannot alias reads of the other and does not wait for it
+    // Separate arrays, not [2][..]: the compiler then knows a copy into one
+    // cannot alias reads of the other and does not wait for it.
     __shared__ __attribute__((aligned(16))) float As0[ATILE];
     __shared__ __attribute__((aligned(16))) float As1[ATILE];
-    __shared__ __attribute__((aligned(16))) float Rs[RTILE];
+    __shared__ __attribute__((aligned(16))) float Rs0[RTILE];
+    __shared__ __attribute__((aligned(16))) float Rs1[RTILE];
     __shared__ float ksum[KS == 2 ? 4 * RB * 3 * 4 * 64 : 1];
-    __shared__ float rstat[4][TR][2];
+    __shared__ float rst0[4][TR][2];
+    __shared__ float rst1[4][TR][2];
+    __shared__ float prm[3][192];              // bias, LN weight, LN bias of the group's columns
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -403,7 +422,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const int ng = blockIdx.x / g.P;
     const int p = blockIdx.x - ng * g.P;
     const int gc0 = ng * g.ngw;
-    const int gc1 = min(gc0 + g.ngw, g.N);
+    const int gw = min(gc0 + g.ngw, g.N) - gc0;  // columns in this group
     const int kbase = kq * KPW;
 
     const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(g.A, (size_t)g.M * g.lda * 4);
@@ -414,14 +433,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 
     // ---- the weight slice, once (columns outside the group read as zero) ----
     float bw[3][S];
-    float bias_v[3], lnw[3], lnb[3];
-    bool cok[3];
-    int col[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
-        col[t] = gc0 + 48 * cg + 16 * t + j;
-        cok[t] = col[t] < gc1;
-        const int boff = cok[t] ? (col[t] * g.ldb + kbase) * 4 : BUF_OOB;
+        const int cl = 48 * cg + 16 * t + j;
+        const int boff = cl < gw ? ((gc0 + cl) * g.ldb + kbase) * 4 : BUF_OOB;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             const float4 v = buf_load4(rb_rs, boff + (16 * gi + 4 * q) * 4);
@@ -432,15 +447,15 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         }
 #pragma unroll
         for (int i = 0; i < R; ++i) bw[t][4 * G + i] = buf_load1(rb_rs, boff + (16 * G + R * q + i) * 4);
-        const int cc = cok[t] ? col[t] : gc0;
-        bias_v[t] = (cok[t] && g.bias) ? g.bias[cc] : 0.f;
-        lnw[t] = (HAS_LN && cok[t]) ? g.ln_w[cc] : 0.f;
-        lnb[t] = (HAS_LN && cok[t]) ? g.ln_b[cc] : 0.f;
+    }
+    if (tid < 192) {
+        const bool ok = tid < gw;
+        prm[0][tid] = (ok && g.bias) ? g.bias[gc0 + tid] : 0.f;
+        prm[1][tid] = (HAS_LN && ok) ? g.ln_w[gc0 + tid] : 0.f;
+        prm[2][tid] = (HAS_LN && ok) ? g.ln_b[gc0 + tid] : 0.f;
     }
 
     const int ntask = (g.M + TR - 1) / TR;
-    // chunk c of a task's tile goes to wave c % NW; every wave issues the same
-    // count, chunks past the tile read whatever follows it into LDS padding
     auto dma_a = [&](int task, float *dst) {
 #pragma unroll
         for (int u = 0; u < NCA; ++u) {
@@ -448,18 +463,64 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             dma16(ra_rs, dst + c * 256, (task * TR * g.lda + c * 256 + 4 * lane) * 4);
         }
     };
-    auto dma_r = [&](int task) {
+    auto dma_r = [&](int task, float *dst) {
 #pragma unroll
         for (int u = 0; u < NCR; ++u) {
             const int c = wave + NW * u;
-            dma16(rr_rs, &Rs[c * 256], (task * TR * g.ldr + c * 256 + 4 * lane) * 4);
+            dma16(rr_rs, dst + c * 256, (task * TR * g.ldr + c * 256 + 4 * lane) * 4);
         }
     };
 
-    // One task: multiply the tile in `cur` while the next task's tile streams
-    // into `nxt_buf`, then the epilogue. Called with the two arrays swapped on
-    // alternate tasks, always with compile-time-known arrays.
-    auto body = [&](int task, const float *cur, float *nxt_buf) __attribute__((always_inline)) {
+    // The epilogue of a task (normalise, activation, residual, store) runs
+    // one task late, under the next task's MFMAs: `pacc` holds the previous
+    // task's bias-added sums, its row statistics sit in `prst`, its residual
+    // tile in `pres`.
+    f4v pacc[RB][3];
+    auto finish = [&](int task, const float (*prst)[TR][2], const float *pres)
+        __attribute__((always_inline)) {
+        const float invn = 1.0f / (float)gw;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = rb * 16 + 4 * q + r;
+                const int m = task * TR + row;
+                float mean = 0.f, rstd = 1.f;
+                if (HAS_LN) {
+                    const float a1 = (prst[0][row][0] + prst[1][row][0]) +
+                                     (prst[2][row][0] + prst[3][row][0]);
+                    const float a2 = (prst[0][row][1] + prst[1][row][1]) +
+                                     (prst[2][row][1] + prst[3][row][1]);
+                    mean = a1 * invn;
+                    float var = a2 * invn - mean * mean;
+                    var = var > 0.f ? var : 0.f;
+                    rstd = 1.0f / sqrtf(var + 1e-5f);
+                }
+#pragma unroll
+                for (int t = 0; t < 3; ++t) {
+                    const int cl = 48 * cg + 16 * t + j;
+                    const bool cok = cl < gw;
+                    float v = pacc[rb][t][r];
+                    if (HAS_LN) v = (v - mean) * rstd * prm[1][cl] + prm[2][cl];
+                    if (EPI == EPI_GELU) v = gelu_erf(v);
+                    if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
+                    if (HAS_RES) v += pres[row * g.ldr + (cok ? cl : 0)];
+                    // every wave issues the same stores (the second K half's go
+                    // out of range and are dropped): the counters stay countable
+                    buf_store1(ro_rs,
+                               (kq == 0 && m < g.M && cok) ? (m * g.ldo + gc0 + cl) * 4 : BUF_OOB, v);
+                }
+            }
+    };
+
+    // One task: the next A tile streams into `nxt_buf` while this one
+    // multiplies from `cur` and the previous task is finished; then this
+    // task's row statistics go to `wrst` and, past the barrier, the residual
+    // tile of the task after next starts streaming into `rnext`.
+    auto body = [&](auto have_prev, int task, const float *cur, float *nxt_buf, int prev_task,
+                    const float (*prst)[TR][2], const float *pres, float (*wrst)[TR][2],
+                    float *rnext) __attribute__((always_inline)) {
+        constexpr bool HP = decltype(have_prev)::value;
         const int nxt = task + g.P;
         dma_a(nxt < ntask ? nxt : task, nxt_buf);
 
@@ -487,6 +548,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
                     for (int t = 0; t < 3; ++t)
                         acc[rb][t] = MFMA16(av[rb][i], bw[t][4 * gi + i], acc[rb][t]);
+            // the previous task's epilogue, issued while these MFMAs run
+            if constexpr (HP) {
+                if (gi == 0) finish(prev_task, prst, pres);
+            }
         }
 #pragma unroll
         for (int i = 0; i < R; ++i) {
@@ -521,95 +586,80 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             }
         }
 
-        // the residual tile (copied during the previous task) has landed once
-        // everything but this task's A-tile chunks has
-        if (HAS_RES) WAIT_VMCNT(NCA);
-        float mean[RB][4], rstd[RB][4];
+        // bias, and the row statistics when a LayerNorm follows (single-pass,
+        // as the reference's channel LayerNorm computes them; padding columns
+        // hold exact zeros)
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+        for (int t = 0; t < 3; ++t) {
+            const float bv = prm[0][48 * cg + 16 * t + j];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int t = 0; t < 3; ++t) acc[rb][t][r] += bias_v[t];
+                for (int r = 0; r < 4; ++r) acc[rb][t][r] += bv;
+        }
         if (HAS_LN) {
-            // single-pass statistics over the whole row, as the reference's
-            // channel LayerNorm computes them (padding columns hold exact zeros)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float s1 = (acc[rb][0][r] + acc[rb][1][r]) + acc[rb][2][r];
-                    float s2 = (acc[rb][0][r] * acc[rb][0][r] + acc[rb][1][r] * acc[rb][1][r]) +
-                               acc[rb][2][r] * acc[rb][2][r];
-#pragma unroll
-                    for (int o = 8; o >= 1; o >>= 1) {
-                        s1 += __shfl_xor(s1, o, 64);
-                        s2 += __shfl_xor(s2, o, 64);
-                    }
+                    const float s1 = row16_sum((acc[rb][0][r] + acc[rb][1][r]) + acc[rb][2][r]);
+                    const float s2 = row16_sum(
+                        (acc[rb][0][r] * acc[rb][0][r] + acc[rb][1][r] * acc[rb][1][r]) +
+                        acc[rb][2][r] * acc[rb][2][r]);
                     if (kq == 0 && j == 0) {
-                        rstat[cg][rb * 16 + 4 * q + r][0] = s1;
-                        rstat[cg][rb * 16 + 4 * q + r][1] = s2;
+                        wrst[cg][rb * 16 + 4 * q + r][0] = s1;
+                        wrst[cg][rb * 16 + 4 * q + r][1] = s2;
                     }
                 }
         }
-        if (HAS_LN || HAS_RES) lds_sync();
-        if (HAS_LN) {
-            const float invn = 1.0f / (float)(gc1 - gc0);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = rb * 16 + 4 * q + r;
-                    const float a1 = (rstat[0][row][0] + rstat[1][row][0]) +
-                                     (rstat[2][row][0] + rstat[3][row][0]);
-                    const float a2 = (rstat[0][row][1] + rstat[1][row][1]) +
-                                     (rstat[2][row][1] + rstat[3][row][1]);
-                    mean[rb][r] = a1 * invn;
-                    float var = a2 * invn - mean[rb][r] * mean[rb][r];
-                    var = var > 0.f ? var : 0.f;
-                    rstd[rb][r] = 1.0f / sqrtf(var + 1e-5f);
-                }
-        }
-        // every wave issues the same stores (the second K half's go out of
-        // range and are dropped), so the memory counters stay countable
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = rb * 16 + 4 * q + r;
-                const int m = task * TR + row;
-#pragma unroll
-                for (int t = 0; t < 3; ++t) {
-                    float v = acc[rb][t][r];
-                    if (HAS_LN) v = (v - mean[rb][r]) * rstd[rb][r] * lnw[t] + lnb[t];
-                    if (EPI == EPI_GELU) v = gelu_erf(v);
-                    if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
-                    if (HAS_RES) v += Rs[row * g.ldr + (cok[t] ? col[t] : gc0)];
-                    buf_store1(ro_rs,
-                               (kq == 0 && m < g.M && cok[t]) ? (m * g.ldo + col[t]) * 4 : BUF_OOB, v);
-                }
-            }
-        // all reads of this task's A tile and residual are done past here
+            for (int t = 0; t < 3; ++t) pacc[rb][t] = acc[rb][t];
+
+        // everything this task needs next (the next A tile, and the residual
+        // tile copied during the previous task) has landed; the previous
+        // task's reads of `pres` are done past this barrier
+        // (outstanding, oldest first: this task's residual, the next A tile,
+        // the previous task's stores)
+        if constexpr (HP) {
+            WAIT_VMCNT(NSTORE);
+        } else {
+            WAIT_VMCNT(0);
+        }
         lds_sync();
-        if (HAS_RES) dma_r(nxt < ntask ? nxt : task);
-        // the next A tile: outstanding are [its chunks][stores][residual chunks]
-        WAIT_VMCNT(NSTORE + NCR);
-        lds_sync();
+        if (HAS_RES) dma_r(nxt < ntask ? nxt : task, rnext);
     };
 
     int task = p;
     if (task < ntask) {
         dma_a(task, As0);
-        if (HAS_RES) dma_r(task);
+        if (HAS_RES) dma_r(task, Rs0);
     }
     __builtin_amdgcn_s_waitcnt(0);
     lds_sync();
-    while (task < ntask) {
-        body(task, As0, As1);
+    if (task < ntask) {
+        // task k multiplies from As[k%2], writes its statistics to rst[k%2] and
+        // finds its residual in Rs[k%2]; it is finished during task k+1
+        using std::false_type;
+        using std::true_type;
+        body(false_type{}, task, As0, As1, 0, rst1, Rs1, rst0, Rs1);
+        int prev = task;
+        bool last_even = true;
         task += g.P;
-        if (task >= ntask) break;
-        body(task, As1, As0);
-        task += g.P;
+        while (task < ntask) {
+            body(true_type{}, task, As1, As0, prev, rst0, Rs0, rst1, Rs0);
+            prev = task;
+            last_even = false;
+            task += g.P;
+            if (task >= ntask) break;
+            body(true_type{}, task, As0, As1, prev, rst1, Rs1, rst0, Rs1);
+            prev = task;
+            last_even = true;
+            task += g.P;
+        }
+        if (last_even) finish(prev, rst0, Rs0);
+        else finish(prev, rst1, Rs1);
     }
 }
 
@@ -1452,12 +1502,19 @@ static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool laun
     switch (epi) {
     case EPI_STORE: return run_bs<KPW, KS, RB, EPI_STORE>(g, st, launch, grid);
     case EPI_GELU: return run_bs<KPW, KS, RB, EPI_GELU>(g, st, launch, grid);
-    case EPI_RES: return run_bs<KPW, KS, RB, EPI_RES>(g, st, launch, grid);
-    case EPI_LN: return run_bs<KPW, KS, RB, EPI_LN>(g, st, launch, grid);
-    case EPI_LN_RES: return run_bs<KPW, KS, RB, EPI_LN_RES>(g, st, launch, grid);
     case EPI_LRELU: return run_bs<KPW, KS, RB, EPI_LRELU>(g, st, launch, grid);
-    default: return hipErrorInvalidValue;
+    default: break;
     }
+    // residual and LayerNorm epilogues run with 16-row tasks only (bs_rb)
+    if constexpr (RB == 1) {
+        switch (epi) {
+        case EPI_RES: return run_bs<KPW, KS, RB, EPI_RES>(g, st, launch, grid);
+        case EPI_LN: return run_bs<KPW, KS, RB, EPI_LN>(g, st, launch, grid);
+        case EPI_LN_RES: return run_bs<KPW, KS, RB, EPI_LN_RES>(g, st, launch, grid);
+        default: break;
+        }
+    }
+    return hipErrorInvalidValue;
 }
 
 // Rows per task: 32 (twice the MFMA work per task for the same per-task
@@ -1466,8 +1523,9 @@ static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool laun
 // 16 otherwise.
 static int bs_rb(const GemmArgs &g, int ks, int epi) {
     const int ng = (g.N + 191) / 192;
-    const bool ln = epi == EPI_LN || epi == EPI_LN_RES;
-    return (ng >= 2 && !ln) ? 2 : 1;
+    const bool simple = epi == EPI_STORE || epi == EPI_GELU || epi == EPI_LRELU;
+    (void)ks;
+    return (ng >= 2 && simple) ? 2 : 1;
 }
 
 static hipError_t run_bs_any(const GemmArgs &g, int kpw, int ks, int epi, hipStream_t st,
