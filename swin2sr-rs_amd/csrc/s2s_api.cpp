@@ -104,6 +104,14 @@ struct s2s_ctx {
     float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C]
     std::vector<float *> up_w, up_b;           // octave convs, shuffle-permuted [4F][9*F]
     float *last_w = nullptr, *last_b = nullptr;  // conv_last [9][F][3]
+    // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [3][9*F], conv_after_aux [F][9*4]
+    float *bc_w = nullptr, *bc_b = nullptr, *ax_w = nullptr, *ax_b = nullptr;
+    float *caa_w = nullptr, *caa_b = nullptr;
+    // pixelshuffledirect: upsample.0 [3*s*s][9*C]
+    float *psd_w = nullptr, *psd_b = nullptr;
+    // nearest+conv: conv_up1, conv_up2, conv_hr [F][9*F]
+    float *nu1_w = nullptr, *nu1_b = nullptr, *nu2_w = nullptr, *nu2_b = nullptr;
+    float *hr_w = nullptr, *hr_b = nullptr;
 
     // buffers planned for one padded plane (hp, wp)
     int bhp = 0, bwp = 0;
@@ -114,7 +122,10 @@ struct s2s_ctx {
     int ih = 0, iw = 0;
     std::vector<void *> head_allocs;
     float *in_dev = nullptr, *in4 = nullptr, *out_dev = nullptr;
-    std::vector<float *> fplanes;  // F0 .. F_octaves
+    std::vector<float *> fplanes;  // the head's feature planes
+    // pixelshuffle_aux: aux conv output [P][4], its planar image [3][P], the
+    // bicubic input [(hp*s)*(wp*s)][4] and its conv [(hp*s)*(wp*s)][F]
+    float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr, *bicf = nullptr;
 
     bool prof = false;
     std::vector<Pending> pending;
@@ -136,6 +147,7 @@ struct s2s_ctx {
     int block_fwd(const BlockW &b, int hp, int wp, int shift, const float *x_in, float *x_out);
     int stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out);
     int forward_device(int h, int w, const float *d_in, float *d_out);
+    int head(int h, int w, float *d_out);
 };
 
 namespace {
@@ -221,12 +233,29 @@ int s2s_ctx::plan_image(int h, int w) {
     int rc = alloc(head_allocs, (size_t)3 * h * w, &in_dev, "input") ||
              alloc(head_allocs, P * 4, &in4, "padded input") ||
              alloc(head_allocs, (size_t)3 * h * s * w * s, &out_dev, "output");
-    size_t px = P;
-    for (int o_ = 0; rc == 0 && o_ <= octaves; ++o_) {
+    // the head's feature planes: one per octave for the pixel-shuffle heads,
+    // P, 4P, 16P, 16P for nearest+conv, none for pixelshuffledirect
+    std::vector<size_t> planes;
+    if (arch.upsampler == S2S_PIXELSHUFFLE || arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
+        size_t px = P;
+        for (int o_ = 0; o_ <= octaves; ++o_, px *= 4) planes.push_back(px);
+    } else if (arch.upsampler == S2S_NEAREST_CONV) {
+        planes = {P, 4 * P, 16 * P, 16 * P};
+    }
+    for (size_t i = 0; rc == 0 && i < planes.size(); ++i) {
         float *f = nullptr;
-        rc = alloc(head_allocs, px * feat, &f, "head plane");
+        rc = alloc(head_allocs, planes[i] * feat, &f, "head plane");
         fplanes.push_back(f);
-        px *= 4;
+    }
+    if (rc == 0 && arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
+        const size_t Q = P * s * s;
+        rc = alloc(head_allocs, P * 4, &aux4, "aux conv") ||
+             alloc(head_allocs, P * 3, &auxp, "aux image") ||
+             alloc(head_allocs, Q * 4, &bic4, "bicubic input") ||
+             alloc(head_allocs, Q * feat, &bicf, "bicubic conv");
+        // channel 3 of aux4 is never written and must read zero
+        if (rc == 0 && hipMemset(aux4, 0, P * 4 * sizeof(float)) != hipSuccess)
+            rc = fail("hipMemset(aux conv) failed");
     }
     if (rc) {
         free_list(head_allocs);
@@ -401,9 +430,6 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
                     " window. The reference pads to the NEXT window multiple by concatenating "
                     "the image with its own mirror, which for an image shorter than a window "
                     "falls through to a different padding rule this engine does not implement.");
-    if (arch.upsampler != S2S_PIXELSHUFFLE)
-        return fail("this device backend implements the pixelshuffle head; upsampler " +
-                    std::to_string(arch.upsampler) + " is not built yet");
     if (plan_image(h, w)) return -1;
     const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
     const int P = hp * wp;
@@ -425,24 +451,91 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
     g.res = body;
     g.ldr = c;
     if (gemm("conv_after_body_res", g, ALOAD_IM2COL, EPI_RES)) return -1;
-    g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
-    g.slope = 0.01f;
-    if (gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
-    int H = hp, W = wp;
-    for (int oc = 0; oc < octaves; ++oc) {
-        g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
-        g.feat = feat;
-        const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
-        if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
-        H *= 2;
-        W *= 2;
-    }
-    const int s = arch.scale;
+    return head(h, w, d_out);
+}
+
+// The reconstruction heads (reference src/gpu.rs:591-733 / src/cpu.rs:1701-1880)
+// from `cur`, the body's output, into the planar, denormalised, cropped output.
+int s2s_ctx::head(int h, int w, float *d_out) {
+    const int win = arch.window, s = arch.scale;
+    const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
+    const int P = hp * wp;
     const int oh = h * s, ow = w * s;
-    return run("conv_last_finish", conv_last_grid(oh, ow), dim3(256), [&] {
-        return launch_conv_last_finish(fplanes[octaves], last_w, last_b, d_out, H, W, feat, oh,
-                                       ow, arch.img_range, arch.mean, stream);
-    });
+    GemmArgs g{};
+    auto last = [&](const float *f, int H, int W) {
+        return run("conv_last_finish", conv_last_grid(oh, ow), dim3(256), [&] {
+            return launch_conv_last_finish(f, last_w, last_b, d_out, H, W, feat, oh, ow,
+                                           arch.img_range, arch.mean, stream);
+        });
+    };
+    switch (arch.upsampler) {
+    case S2S_PIXELSHUFFLE:
+    case S2S_PIXELSHUFFLE_AUX: {
+        const bool aux = arch.upsampler == S2S_PIXELSHUFFLE_AUX;
+        g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
+        g.slope = 0.01f;
+        if (gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+        if (aux) {
+            // the bicubic branch from the padded input, its conv; the aux image
+            // and its conv back to features (reference network_swin2sr.py:948-958)
+            const int qh = hp * s, qw = wp * s, Q = qh * qw;
+            if (run("bicubic", dim3((Q + 255) / 256), dim3(256),
+                    [&] { return launch_bicubic4(in4, bic4, hp, wp, qh, qw, stream); }))
+                return -1;
+            g = conv_gemm(bic4, qh, qw, 4, bc_w, bc_b, bicf, feat, feat);
+            if (gemm("conv_bicubic", g, ALOAD_IM2COL, EPI_STORE)) return -1;
+            g = conv_gemm(fplanes[0], hp, wp, feat, ax_w, ax_b, aux4, 4, 3);
+            if (gemm("conv_aux", g, ALOAD_IM2COL, EPI_STORE)) return -1;
+            g = conv_gemm(aux4, hp, wp, 4, caa_w, caa_b, fplanes[0], feat, feat);
+            g.slope = 0.01f;
+            if (gemm("conv_after_aux", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+            if (run("aux_finish", dim3((P + 255) / 256), dim3(256), [&] {
+                    return launch_aux_finish(aux4, auxp, P, arch.img_range, arch.mean, stream);
+                }))
+                return -1;
+        }
+        int H = hp, W = wp;
+        for (int oc = 0; oc < octaves; ++oc) {
+            g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
+            g.feat = feat;
+            if (aux && oc == octaves - 1) g.res = bicf;  // + the bicubic branch
+            const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
+            if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
+            H *= 2;
+            W *= 2;
+        }
+        return last(fplanes[octaves], H, W);
+    }
+    case S2S_PIXELSHUFFLE_DIRECT: {
+        // one conv to 3*s^2 channels, stored through pixel_shuffle(s) straight
+        // into the denormalised, cropped output
+        g = conv_gemm(cur, hp, wp, c, psd_w, psd_b, d_out, 0, 3 * s * s);
+        g.scale = s;
+        g.oh = oh;
+        g.ow = ow;
+        g.img_range = arch.img_range;
+        for (int i = 0; i < 3; ++i) g.mean[i] = arch.mean[i];
+        return gemm("conv_shuffle_finish", g, ALOAD_IM2COL, EPI_SHUFFLE_FINISH);
+    }
+    case S2S_NEAREST_CONV: {
+        g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
+        g.slope = 0.01f;
+        if (gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+        // two nearest-2x steps, each read by the next conv's operand loader
+        g = conv_gemm(fplanes[0], 2 * hp, 2 * wp, feat, nu1_w, nu1_b, fplanes[1], feat, feat);
+        g.slope = 0.2f;
+        if (gemm("conv_up1", g, ALOAD_IM2COL_UP2, EPI_LRELU)) return -1;
+        g = conv_gemm(fplanes[1], 4 * hp, 4 * wp, feat, nu2_w, nu2_b, fplanes[2], feat, feat);
+        g.slope = 0.2f;
+        if (gemm("conv_up2", g, ALOAD_IM2COL_UP2, EPI_LRELU)) return -1;
+        g = conv_gemm(fplanes[2], 4 * hp, 4 * wp, feat, hr_w, hr_b, fplanes[3], feat, feat);
+        g.slope = 0.2f;
+        if (gemm("conv_hr", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+        return last(fplanes[3], 4 * hp, 4 * wp);
+    }
+    default:
+        return fail("unknown upsampler " + std::to_string(arch.upsampler));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -676,15 +769,32 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
         }
     }
 
-    if (!rc && (A.upsampler == S2S_PIXELSHUFFLE || A.upsampler == S2S_PIXELSHUFFLE_AUX)) {
+    // ---- the reconstruction head (reference src/gpu.rs:801-872, network_swin2sr.py:790-860)
+    auto head_feat = [&]() -> int {
         const s2s_tensor *cb = ts.find("conv_before_upsample.0.weight");
-        if (!cb || cb->ndim != 4 || cb->shape[0] <= 0 || cb->shape[0] % 4 != 0)
-            rc = fail("weight `conv_before_upsample.0.weight` is missing or not [feat][C][3][3] "
-                      "with feat a multiple of 4");
-        if (!rc) rc = ts.get("conv_before_upsample.0.weight", {cb->shape[0], C, 3, 3}, &cb);
+        if (!cb || cb->ndim != 4 || cb->shape[0] <= 0 || cb->shape[0] % 32 != 0)
+            return fail("weight `conv_before_upsample.0.weight` is missing or not [feat][C][3][3] "
+                        "with feat a multiple of 32");
+        if (ts.get("conv_before_upsample.0.weight", {cb->shape[0], C, 3, 3}, &cb)) return -1;
+        ctx->feat = (int)cb->shape[0];
+        return 0;
+    };
+    auto conv_last = [&](int F) -> int {
+        const s2s_tensor *lw;
+        if (ts.get("conv_last.weight", {3, F, 3, 3}, &lw)) return -1;
+        std::vector<float> t((size_t)9 * F * 3);
+        for (int co = 0; co < 3; ++co)
+            for (int ci = 0; ci < F; ++ci)
+                for (int tap = 0; tap < 9; ++tap)
+                    t[((size_t)tap * F + ci) * 3 + co] = lw->data[((size_t)co * F + ci) * 9 + tap];
+        return ctx->upload(t, &ctx->last_w) || up("conv_last.bias", {3}, &ctx->last_b);
+    };
+    if (!rc && (A.upsampler == S2S_PIXELSHUFFLE || A.upsampler == S2S_PIXELSHUFFLE_AUX)) {
+        if (A.scale < 2 || (A.scale & (A.scale - 1)))
+            rc = fail("the pixel-shuffle head needs a power-of-two scale, got " + std::to_string(A.scale));
+        rc = rc || head_feat();
         if (!rc) {
-            const int F = (int)cb->shape[0];
-            ctx->feat = F;
+            const int F = ctx->feat;
             int oct = 0;
             while ((1 << oct) < A.scale) ++oct;
             ctx->octaves = oct;
@@ -704,17 +814,36 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 ctx->up_w.push_back(dw);
                 ctx->up_b.push_back(db);
             }
-            const s2s_tensor *lw;
-            rc = rc || ts.get("conv_last.weight", {3, F, 3, 3}, &lw);
-            if (!rc) {
-                std::vector<float> t((size_t)9 * F * 3);
-                for (int co = 0; co < 3; ++co)
-                    for (int ci = 0; ci < F; ++ci)
-                        for (int tap = 0; tap < 9; ++tap)
-                            t[((size_t)tap * F + ci) * 3 + co] = lw->data[((size_t)co * F + ci) * 9 + tap];
-                rc = ctx->upload(t, &ctx->last_w);
+            rc = rc || conv_last(F);
+            if (A.upsampler == S2S_PIXELSHUFFLE_AUX) {
+                rc = rc || upconv("conv_bicubic.weight", F, 3, &ctx->bc_w, nullptr);
+                rc = rc || up("conv_bicubic.bias", {F}, &ctx->bc_b);
+                rc = rc || upconv("conv_aux.weight", 3, F, &ctx->ax_w, nullptr);
+                rc = rc || up("conv_aux.bias", {3}, &ctx->ax_b);
+                rc = rc || upconv("conv_after_aux.0.weight", F, 3, &ctx->caa_w, nullptr);
+                rc = rc || up("conv_after_aux.0.bias", {F}, &ctx->caa_b);
             }
-            rc = rc || up("conv_last.bias", {3}, &ctx->last_b);
+        }
+    } else if (!rc && A.upsampler == S2S_PIXELSHUFFLE_DIRECT) {
+        const int n = 3 * A.scale * A.scale;
+        rc = rc || upconv("upsample.0.weight", n, C, &ctx->psd_w, nullptr);
+        rc = rc || up("upsample.0.bias", {n}, &ctx->psd_b);
+    } else if (!rc && A.upsampler == S2S_NEAREST_CONV) {
+        if (A.scale != 4)
+            rc = fail("the nearest+conv head upsamples by exactly 4 (two nearest-2x steps), got scale " +
+                      std::to_string(A.scale));
+        rc = rc || head_feat();
+        if (!rc) {
+            const int F = ctx->feat;
+            rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
+            rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
+            rc = rc || upconv("conv_up1.weight", F, F, &ctx->nu1_w, nullptr);
+            rc = rc || up("conv_up1.bias", {F}, &ctx->nu1_b);
+            rc = rc || upconv("conv_up2.weight", F, F, &ctx->nu2_w, nullptr);
+            rc = rc || up("conv_up2.bias", {F}, &ctx->nu2_b);
+            rc = rc || upconv("conv_hr.weight", F, F, &ctx->hr_w, nullptr);
+            rc = rc || up("conv_hr.bias", {F}, &ctx->hr_b);
+            rc = rc || conv_last(F);
         }
     }
     if (rc) {
@@ -749,8 +878,17 @@ int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out
     if (ctx->forward_device(h, w, ctx->in_dev, ctx->out_dev)) return -1;
     HIPCHK("hipMemcpyAsync(output)", hipMemcpyAsync(out, ctx->out_dev, nout * 4,
                                                     hipMemcpyDeviceToHost, ctx->stream));
-    HIPCHK("hipStreamSynchronize", hipStreamSynchronize(ctx->stream));
     ctx->aux_host.clear();
+    if (ctx->arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
+        // the compressed head's second image, at the padded geometry
+        // (reference src/gpu.rs:752-758)
+        const int win = ctx->arch.window;
+        const size_t P = (size_t)(h / win + 1) * win * ((w / win + 1) * win);
+        ctx->aux_host.resize(3 * P);
+        HIPCHK("hipMemcpyAsync(aux)", hipMemcpyAsync(ctx->aux_host.data(), ctx->auxp, 3 * P * 4,
+                                                     hipMemcpyDeviceToHost, ctx->stream));
+    }
+    HIPCHK("hipStreamSynchronize", hipStreamSynchronize(ctx->stream));
     return 0;
 }
 

@@ -5,7 +5,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-enum { ALOAD_ROWS = 0, ALOAD_IM2COL = 1 };
+enum {
+    ALOAD_ROWS = 0,       // A[m*lda + k]
+    ALOAD_IM2COL = 1,     // 3x3 im2col of the channel-last H x W plane A[H*W][cin]
+    ALOAD_IM2COL_UP2 = 2  // 3x3 im2col of the nearest-2x upsampling of A[(H/2)*(W/2)][cin]
+};
 enum {
     EPI_STORE = 0,   // out = acc + bias
     EPI_GELU = 1,    // out = gelu_erf(acc + bias)
@@ -13,7 +17,10 @@ enum {
     EPI_LN = 3,      // out = LayerNorm(acc + bias)             (N <= 192)
     EPI_LN_RES = 4,  // out = res + LayerNorm(acc + bias)       (N <= 192)
     EPI_LRELU = 5,   // out = leaky_relu(acc + bias, slope)
-    EPI_SHUFFLE = 6  // pixel_shuffle(2) store into a 2H x 2W channel-last plane
+    EPI_SHUFFLE = 6,  // pixel_shuffle(2) store into a 2H x 2W channel-last plane (+ res
+                      // in that layout when res is set)
+    EPI_SHUFFLE_FINISH = 7  // pixel_shuffle(scale) of a 3*scale^2-channel conv, denormalised
+                            // and cropped into the planar [3][oh][ow] output
 };
 
 struct GemmArgs {
@@ -33,6 +40,9 @@ struct GemmArgs {
     const float *ln_w, *ln_b;
     float slope;
     int feat;  // EPI_SHUFFLE: output channels (N = 4*feat)
+    // EPI_SHUFFLE_FINISH: scale, output crop, img_range and the RGB mean
+    int scale, oh, ow;
+    float img_range, mean[3];
     int M, N, K;
 };
 
@@ -86,6 +96,13 @@ dim3 conv_last_grid(int oh, int ow);
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
                                    float *out, int H, int W, int feat, int oh, int ow,
                                    float img_range, const float *mean, hipStream_t st);
+// torch's bicubic resize (a = -0.75, align_corners = False, edge clamp) of a
+// channel-last [h*w][4] plane to [oh*ow][4] (channel 3 stays 0).
+hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,
+                           hipStream_t st);
+// [P][4] -> planar [3][P], v / img_range + mean (the compressed head's aux image).
+hipError_t launch_aux_finish(const float *in, float *out, int P, float img_range,
+                             const float *mean, hipStream_t st);
 hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *tab, float *cpbt,
                       int win, int heads, hipStream_t st);
 hipError_t launch_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *reg,

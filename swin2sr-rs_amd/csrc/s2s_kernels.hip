@@ -68,6 +68,18 @@ __device__ __forceinline__ float4 load_a4(const GemmArgs &g, int m, int k) {
     if (m >= g.M || k >= g.K) return z;
     if (ALOAD == ALOAD_ROWS) {
         return *reinterpret_cast<const float4 *>(g.A + (size_t)m * g.lda + k);
+    } else if (ALOAD == ALOAD_IM2COL_UP2) {
+        // the conv runs on the H x W nearest-2x upsampling of an (H/2) x (W/2)
+        // plane; the upsampled plane is never materialised
+        const int tap = k / g.cin;
+        const int ci = k - tap * g.cin;
+        const int y = m / g.W;
+        const int x = m - y * g.W;
+        const int sy = y + tap / 3 - 1;
+        const int sx = x + tap % 3 - 1;
+        if (sy < 0 || sy >= g.H || sx < 0 || sx >= g.W) return z;
+        return *reinterpret_cast<const float4 *>(
+            g.A + ((size_t)(sy >> 1) * (g.W >> 1) + (sx >> 1)) * g.cin + ci);
     } else {
         const int tap = k / g.cin;
         const int ci = k - tap * g.cin;
@@ -268,7 +280,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                     const int y = m / g.W;
                     const int x = m - y * g.W;
                     const size_t op = (size_t)(2 * y + (q >> 1)) * (2 * g.W) + (2 * x + (q & 1));
+                    if (g.res) v += g.res[op * g.feat + ch];
                     g.out[op * g.feat + ch] = v;
+                } else if (EPI == EPI_SHUFFLE_FINISH) {
+                    // n is torch's channel c*s^2 + dy*s + dx of the conv; the
+                    // pixel_shuffle(s) output pixel (s*y+dy, s*x+dx), channel c,
+                    // denormalised and cropped like the reference's finish
+                    const int s2 = g.scale * g.scale;
+                    const int c = n / s2;
+                    const int r = n - c * s2;
+                    const int dy = r / g.scale, dx = r - dy * g.scale;
+                    const int y = m / g.W;
+                    const int x = m - y * g.W;
+                    const int oy = g.scale * y + dy, ox = g.scale * x + dx;
+                    if (oy < g.oh && ox < g.ow)
+                        g.out[((size_t)c * g.oh + oy) * g.ow + ox] = v / g.img_range + g.mean[c];
                 } else {
                     g.out[(size_t)m * g.ldo + n] = v;
                 }
@@ -1274,6 +1300,71 @@ __global__ __launch_bounds__(256) void k_conv_last_finish(const float *__restric
     out[2 * plane + o] = a2 * inv_range + m2;
 }
 
+// torch's bicubic resize, as the reference's cpu::bicubic_resize computes it
+// (src/cpu.rs:875-935: a = -0.75, align_corners = False, taps clamped to the
+// edge, the four horizontal products summed pairwise, then the vertical
+// accumulation in tap order), on a channel-last [h*w][4] plane.
+__device__ __forceinline__ float cubic_w(float t) {
+    const float A = -0.75f;
+    t = fabsf(t);
+    if (t <= 1.0f) return ((A + 2.0f) * t - (A + 3.0f)) * t * t + 1.0f;
+    if (t < 2.0f) return (((t - 5.0f) * t + 8.0f) * t - 4.0f) * A;
+    return 0.0f;
+}
+
+__device__ __forceinline__ void cubic_taps(int i, int n_in, int n_out, int idx[4], float wt[4]) {
+    const float src = ((float)i + 0.5f) * ((float)n_in / (float)n_out) - 0.5f;
+    const float base = floorf(src);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        int id = (int)base - 1 + m;
+        id = id < 0 ? 0 : (id > n_in - 1 ? n_in - 1 : id);
+        idx[m] = id;
+        wt[m] = cubic_w(src - (base + (float)m - 1.0f));
+    }
+}
+
+__global__ void k_bicubic4(const float *__restrict__ in, float *__restrict__ out, int h, int w,
+                           int oh, int ow) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= oh * ow) return;
+    const int y = i / ow, x = i - (i / ow) * ow;
+    int iy[4], ix[4];
+    float wy[4], wx[4];
+    cubic_taps(y, h, oh, iy, wy);
+    cubic_taps(x, w, ow, ix, wx);
+    float acc[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float *r = in + (size_t)iy[m] * w * 4;
+        const float4 p0 = *reinterpret_cast<const float4 *>(r + ix[0] * 4);
+        const float4 p1 = *reinterpret_cast<const float4 *>(r + ix[1] * 4);
+        const float4 p2 = *reinterpret_cast<const float4 *>(r + ix[2] * 4);
+        const float4 p3 = *reinterpret_cast<const float4 *>(r + ix[3] * 4);
+        const float v0[3] = {p0.x, p0.y, p0.z}, v1[3] = {p1.x, p1.y, p1.z};
+        const float v2[3] = {p2.x, p2.y, p2.z}, v3[3] = {p3.x, p3.y, p3.z};
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float a0 = wx[0] * v0[c], a1 = wx[1] * v1[c];
+            const float a2 = wx[2] * v2[c], a3 = wx[3] * v3[c];
+            acc[c] += wy[m] * ((a0 + a1) + (a2 + a3));
+        }
+    }
+    *reinterpret_cast<float4 *>(out + (size_t)i * 4) = make_float4(acc[0], acc[1], acc[2], 0.f);
+}
+
+// reference cpu::finish_aux (src/cpu.rs:1925-1941): the aux image, denormalised,
+// planar at the padded geometry.
+__global__ void k_aux_finish(const float *__restrict__ in, float *__restrict__ out, int P,
+                             float img_range, float m0, float m1, float m2) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= P) return;
+    const float4 v = *reinterpret_cast<const float4 *>(in + (size_t)i * 4);
+    out[i] = v.x / img_range + m0;
+    out[(size_t)P + i] = v.y / img_range + m1;
+    out[2 * (size_t)P + i] = v.z / img_range + m2;
+}
+
 // The continuous position bias table (reference tools/convert.py:141-167 and
 // network_swin2sr.py:101-136), built on the device from the cpb_mlp weights:
 // one workgroup per relative offset (dy, dx) in [-(win-1), win-1]^2, the
@@ -1341,38 +1432,53 @@ static const int kVariants[GEMM_NVARIANTS][4] = {
 
 template <int MT, int NT, int WM, int WN, int ALOAD>
 static hipError_t run_gemm_e(const GemmArgs &g, int epi, hipStream_t st) {
-    switch (epi) {
-    case EPI_STORE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_STORE>(g, st);
-    case EPI_GELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_GELU>(g, st);
-    case EPI_RES: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_RES>(g, st);
-    case EPI_LRELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
-    case EPI_SHUFFLE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_SHUFFLE>(g, st);
-    case EPI_LN:
-    case EPI_LN_RES:
-        // the whole row must be one column tile
-        if constexpr (NT >= 192) {
-            return epi == EPI_LN ? run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN>(g, st)
-                                 : run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN_RES>(g, st);
-        }
+    if constexpr (ALOAD == ALOAD_IM2COL_UP2) {
+        // the real-world head's conv_up1 / conv_up2 (+ LeakyReLU 0.2)
+        if (epi == EPI_LRELU) return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
         return hipErrorInvalidValue;
-    default: return hipErrorInvalidValue;
+    } else {
+        switch (epi) {
+        case EPI_STORE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_STORE>(g, st);
+        case EPI_GELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_GELU>(g, st);
+        case EPI_RES: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_RES>(g, st);
+        case EPI_LRELU: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
+        case EPI_SHUFFLE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_SHUFFLE>(g, st);
+        case EPI_SHUFFLE_FINISH:
+            return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_SHUFFLE_FINISH>(g, st);
+        case EPI_LN:
+        case EPI_LN_RES:
+            // the whole row must be one column tile
+            if constexpr (NT >= 192) {
+                return epi == EPI_LN ? run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN>(g, st)
+                                     : run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LN_RES>(g, st);
+            }
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+        }
     }
 }
 
 template <int MT, int NT, int WM, int WN>
 static hipError_t run_gemm_v(const GemmArgs &g, int aload, int epi, hipStream_t st) {
-    return aload == ALOAD_ROWS ? run_gemm_e<MT, NT, WM, WN, ALOAD_ROWS>(g, epi, st)
-                               : run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL>(g, epi, st);
+    switch (aload) {
+    case ALOAD_ROWS: return run_gemm_e<MT, NT, WM, WN, ALOAD_ROWS>(g, epi, st);
+    case ALOAD_IM2COL: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL>(g, epi, st);
+    case ALOAD_IM2COL_UP2: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL_UP2>(g, epi, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
     (void)g;
-    static const char *names[2][7] = {
+    static const char *names[3][8] = {
         {"gemm_rows_store", "gemm_rows_gelu", "gemm_rows_res", "gemm_rows_ln", "gemm_rows_ln_res",
-         "gemm_rows_lrelu", "gemm_rows_shuffle"},
+         "gemm_rows_lrelu", "gemm_rows_shuffle", "gemm_rows_shuffle_finish"},
         {"conv3x3_store", "conv3x3_gelu", "conv3x3_res", "conv3x3_ln", "conv3x3_ln_res",
-         "conv3x3_lrelu", "conv3x3_shuffle"}};
-    return names[aload == ALOAD_IM2COL][epi];
+         "conv3x3_lrelu", "conv3x3_shuffle", "conv3x3_shuffle_finish"},
+        {"conv3x3_up2_store", "conv3x3_up2_gelu", "conv3x3_up2_res", "conv3x3_up2_ln",
+         "conv3x3_up2_ln_res", "conv3x3_up2_lrelu", "conv3x3_up2_shuffle",
+         "conv3x3_up2_shuffle_finish"}};
+    return names[aload][epi];
 }
 
 // Tile choice by shape, from a sweep of every variant on the forward's own
@@ -1404,10 +1510,7 @@ hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int varian
                                hipStream_t st) {
     if ((epi == EPI_LN || epi == EPI_LN_RES) && g.N > 192) return hipErrorInvalidValue;
     switch (variant) {
-    case 0: return run_gemm_v<128, 192, 2, 2>(g, aload, epi, st);
     case 1: return run_gemm_v<64, 192, 2, 2>(g, aload, epi, st);
-    case 2: return run_gemm_v<128, 64, 4, 1>(g, aload, epi, st);
-    case 3: return run_gemm_v<128, 128, 2, 2>(g, aload, epi, st);
     case 4: return run_gemm_v<64, 128, 2, 2>(g, aload, epi, st);
     case 5: return run_gemm_v<64, 64, 2, 2>(g, aload, epi, st);
     default: return hipErrorInvalidValue;
@@ -1632,6 +1735,20 @@ hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *
     const int total = heads * n * n;
     hipLaunchKernelGGL(k_cpb_gather, dim3((total + 255) / 256), dim3(256), 0, st, tab, cpbt, win,
                        heads);
+    return hipGetLastError();
+}
+
+hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,
+                           hipStream_t st) {
+    const int n = oh * ow;
+    hipLaunchKernelGGL(k_bicubic4, dim3((n + 255) / 256), dim3(256), 0, st, in, out, h, w, oh, ow);
+    return hipGetLastError();
+}
+
+hipError_t launch_aux_finish(const float *in, float *out, int P, float img_range,
+                             const float *mean, hipStream_t st) {
+    hipLaunchKernelGGL(k_aux_finish, dim3((P + 255) / 256), dim3(256), 0, st, in, out, P,
+                       img_range, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
 

@@ -298,3 +298,77 @@ def test_profiler_counts_launches(pkg):
         assert be.profile_query("qkv") == (0.0, 0)
     finally:
         be.close()
+
+
+# ---- the published network's own outputs (tests/golden/make_golden.py) ---------
+
+def _golden_cases():
+    import json
+    from pathlib import Path
+    man = Path(__file__).resolve().parent / "golden" / "net_manifest.json"
+    return json.loads(man.read_text()) if man.exists() else []
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c["name"])
+def test_forward_against_published_network(pkg, orc, case):
+    """Every head on the device against the reference's PyTorch network (golden
+    vectors) and against the oracle: <= 1e-4 max-abs, <= 1 8-bit level."""
+    from pathlib import Path
+    G = Path(__file__).resolve().parent / "golden"
+    M = pkg.model
+    arch = M.Arch(**case["arch"])
+    wts = M.make_weights(arch, seed=case["seed"], perturb=True)
+    img = np.load(G / f"net_{case['name']}_in.npy")
+    want = np.load(G / f"net_{case['name']}_out.npy")
+    h, w = case["h"], case["w"]
+    x = M.adjust(arch, M.to_unit(img))
+    be = pkg.abi.HipBackend(arch, wts)
+    try:
+        got = be.forward(h, w, x)
+        aux = be.aux()
+    finally:
+        be.close()
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() < 1e-4
+    d8 = np.abs(M.to_rgb8(got).astype(int) - M.to_rgb8(want).astype(int)).max()
+    assert d8 <= 1
+    orc_out, orc_aux = orc.forward(arch, wts, h, w, x)
+    assert np.abs(got - orc_out).max() < 1e-4
+    if case["aux"]:
+        want_aux = np.load(G / f"net_{case['name']}_aux.npy")
+        assert aux is not None and aux.size == want_aux.size
+        aux = aux.reshape(want_aux.shape)
+        assert np.abs(aux - want_aux).max() < 1e-4
+        assert np.abs(aux - orc_aux).max() < 1e-4
+    else:
+        assert aux is None
+
+
+@pytest.mark.parametrize("upsampler,scale,h,w", [
+    ("pixelshuffledirect", 2, 64, 64),      # config 0's geometry (128x128 out)
+    ("pixelshuffledirect", 3, 37, 29),
+    ("nearest+conv", 4, 40, 56),
+    ("pixelshuffle_aux", 4, 37, 45),
+])
+def test_other_heads_against_oracle(pkg, orc, upsampler, scale, h, w):
+    """The non-classical heads at the released widths (C = 60 lightweight, 180
+    otherwise; feat 64) and planes wider than one 64-lane wavefront."""
+    M = pkg.model
+    if upsampler == "pixelshuffledirect":
+        arch = M.Arch(upsampler=upsampler, scale=scale, embed=60, depths=[2, 2])
+    else:
+        arch = M.Arch(upsampler=upsampler, scale=scale, embed=180, depths=[2])
+    wts = M.make_weights(arch, seed=scale + h, perturb=True)
+    x = M.adjust(arch, M.to_unit(M.input_uniform(h, w, seed=1)))
+    be = pkg.abi.HipBackend(arch, wts)
+    try:
+        got = be.forward(h, w, x)
+        aux = be.aux()
+    finally:
+        be.close()
+    want, want_aux = orc.forward(arch, wts, h, w, x)
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() < 1e-4
+    assert np.abs(M.to_rgb8(got).astype(int) - M.to_rgb8(want).astype(int)).max() <= 1
+    if want_aux is not None:
+        assert np.abs(aux.reshape(want_aux.shape) - want_aux).max() < 1e-4

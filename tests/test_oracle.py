@@ -251,3 +251,30 @@ def test_oracle_threads_do_not_change_results(orc, pkg):
         orc.lib().orc_set_threads(n0)
     b, _ = orc.forward(arch, wts, 24, 16, x)
     assert np.array_equal(a, b)
+
+
+# ---- the published network's own outputs ---------------------------------------
+
+def _golden_cases():
+    import json
+    man = GOLDEN / "net_manifest.json"
+    return json.loads(man.read_text()) if man.exists() else []
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c["name"])
+def test_forward_against_published_network(orc, pkg, case):
+    """Golden vectors written by tests/golden/make_golden.py from the reference's
+    PyTorch Swin2SR (tools/network_swin2sr.py) on the same synthetic weights:
+    pins the graph's composition and every head, at 1e-4 (the north_star bar)."""
+    M = pkg.model
+    arch = M.Arch(**case["arch"])
+    wts = M.make_weights(arch, seed=case["seed"], perturb=True)
+    img = np.load(GOLDEN / f"net_{case['name']}_in.npy")
+    want = np.load(GOLDEN / f"net_{case['name']}_out.npy")
+    got, aux = orc.forward(arch, wts, case["h"], case["w"], M.adjust(arch, M.to_unit(img)))
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() < 1e-4
+    if case["aux"]:
+        want_aux = np.load(GOLDEN / f"net_{case['name']}_aux.npy")
+        assert aux.shape == want_aux.shape
+        assert np.abs(aux - want_aux).max() < 1e-4
