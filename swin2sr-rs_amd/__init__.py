@@ -5,10 +5,12 @@ Layout of this package:
   Makefile         builds libswin2sr_hip.so with hipcc --offload-arch=gfx950
   abi.py           ctypes binding of the ABI and the `Backend` mirror (HipBackend)
   model.py         architectures, synthetic checkpoints (crate tensor names) and inputs
+  tiling.py        the crate's tile loop and memory policy over the Backend interface
 
 The directory name is not an identifier, so callers load it with
 `load_package()` from the repository root (see __graft_entry__.py).
 """
 from . import model  # noqa: F401
 from . import hip  # noqa: F401
+from . import tiling  # noqa: F401
 from .abi import HipBackend, S2SError, device_info, load_library  # noqa: F401

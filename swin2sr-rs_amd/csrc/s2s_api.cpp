@@ -124,7 +124,7 @@ struct s2s_ctx {
     float *in_dev = nullptr, *in4 = nullptr, *out_dev = nullptr;
     std::vector<float *> fplanes;  // the head's feature planes
     // pixelshuffle_aux: aux conv output [P][4], its planar image [3][P], the
-    // bicubic input [(hp*s)*(wp*s)][4] and its conv [(hp*s)*(wp*s)][F]
+    // bicubic input [(hp*s)*(wp*s)][4] and its conv (= the last head plane)
     float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr, *bicf = nullptr;
 
     bool prof = false;
@@ -251,8 +251,11 @@ int s2s_ctx::plan_image(int h, int w) {
         const size_t Q = P * s * s;
         rc = alloc(head_allocs, P * 4, &aux4, "aux conv") ||
              alloc(head_allocs, P * 3, &auxp, "aux image") ||
-             alloc(head_allocs, Q * 4, &bic4, "bicubic input") ||
-             alloc(head_allocs, Q * feat, &bicf, "bicubic conv");
+             alloc(head_allocs, Q * 4, &bic4, "bicubic input");
+        // the bicubic branch's conv lands in the last octave's plane, which the
+        // last shuffle then updates in place (each element read, added, written
+        // by one thread)
+        bicf = fplanes[octaves];
         // channel 3 of aux4 is never written and must read zero
         if (rc == 0 && hipMemset(aux4, 0, P * 4 * sizeof(float)) != hipSuccess)
             rc = fail("hipMemset(aux conv) failed");

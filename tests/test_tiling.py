@@ -1,0 +1,165 @@
+"""The crate's tiling and memory policy (reference src/backend.rs:88-383,
+tests/tiling.rs) over the Backend interface.
+
+CPU tests drive `run_tiled` with the oracle as the backend (the crate's own
+tiling tests run it on the CPU backend); GPU tests hold the HIP backend's tiled
+output against the oracle's, tile for tile, including config 4's geometry
+(256-pixel tiles with 64 pixels of context).
+"""
+import numpy as np
+import pytest
+
+
+class OracleBackend:
+    """The oracle behind the `Backend` shape (test code only)."""
+
+    def __init__(self, orc, arch, weights):
+        self.orc, self.arch, self.weights = orc, arch, weights
+
+    def forward(self, h, w, x):
+        out, _ = self.orc.forward(self.arch, self.weights, h, w, x)
+        return out
+
+
+def tiny(pkg, **kw):
+    base = dict(upsampler="pixelshuffledirect", scale=2, embed=12, heads=2, depths=[1, 1])
+    base.update(kw)
+    return pkg.model.Arch(**base)
+
+
+def test_crop_side_is_the_reference_rule(pkg):
+    T = pkg.tiling
+    # (n // win + 1) * win, never ceil: a 256 image runs on 264
+    assert T.crop_side(256, 256, 0, 0, 8) == 264
+    assert T.crop_side(648, 640, 0, 0, 8) == 656
+    # a 256 tile with 64 of context on a 1024 image: 384 -> 392
+    assert T.crop_side(1024, 1024, 256, 64, 8) == 392
+    # the crop is clamped to the image
+    assert T.crop_side(100, 300, 256, 64, 8) == 304
+    # the context rounds UP to a window and is never zero
+    assert T.crop_side(1024, 1024, 256, 1, 8) == T.crop_side(1024, 1024, 256, 8, 8)
+    assert T.crop_side(1024, 1024, 256, 9, 8) == T.crop_side(1024, 1024, 256, 16, 8)
+
+
+def test_per_pixel_floats_stays_within_the_crates_device_model(pkg):
+    """The crate budgets with its own device inventory (src/backend.rs:300-383);
+    this backend must not allocate more per padded pixel than that model says."""
+    M = pkg.model
+    T = pkg.tiling
+
+    def crate_model(a):
+        c, mlp, r2, f = a.embed, a.embed * a.mlp_ratio, a.scale ** 2, a.feat
+        acts = 5 * c + 3 * c + 3 * c + mlp
+        if a.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
+            prev, peak = f, 0
+            for o in range(a.octaves):
+                shuf = 4 * f * 4 ** o
+                peak, prev = max(peak, prev + shuf), shuf
+            head = max(peak, prev + 3 * r2)
+        elif a.upsampler == "nearest+conv":
+            head = max(max(4 * f * 4 ** s + f * 4 ** (s + 1) for s in range(2)), 4 * f + 3 * r2)
+        else:
+            head = 2 * 3 * r2
+        return acts + head + 3 + 3 * r2
+
+    for a in (M.classical(4), M.classical(2), M.lightweight(2), M.realworld(), M.compressed()):
+        assert T.per_pixel_floats(a) <= crate_model(a), a.upsampler
+
+
+def test_auto_tile(pkg):
+    T = pkg.tiling
+    a = pkg.model.classical(4)
+    per = T.per_pixel_floats(a)
+    # a budget the whole image fits: one pass
+    assert T.auto_tile(a, per * 264 * 264 * 4, 256, 256, 32) == 0
+    # a budget a 256 tile with 32 of context fits but the image does not
+    side = T.crop_side(1024, 1024, 256, 32, 8)
+    t = T.auto_tile(a, per * side * side * 4, 1024, 1024, 32)
+    assert t == 256 and t % 8 == 0
+    # the launch ceiling tiles even an unlimited budget
+    big = T.auto_tile(a, 1 << 62, 2000, 2000, 32)
+    assert big != 0 and T.crop_side(2000, 2000, big, 32, 8) ** 2 <= T.GPU_MAX_PLANE_PIXELS
+
+
+def test_tile_covering_the_image_is_one_exact_pass(pkg, orc):
+    M = pkg.model
+    a = tiny(pkg)
+    be = OracleBackend(orc, a, M.make_weights(a, seed=3, perturb=True))
+    img = M.to_unit(M.input_uniform(20, 28, seed=2))
+    whole = pkg.tiling.run_tiled(a, be, img, 0, 0)
+    got = pkg.tiling.run_tiled(a, be, img, 64, 8)
+    assert np.array_equal(got, whole)
+
+
+@pytest.mark.parametrize("tile,pad", [(8, 0), (8, 8), (16, 0), (16, 16), (24, 8)])
+def test_tiled_output_covers_the_image(pkg, orc, tile, pad):
+    """reference tests/tiling.rs:79-109: a flat input leaves no pixel unwritten
+    and the mosaic stays close to one pass."""
+    M = pkg.model
+    a = tiny(pkg)
+    be = OracleBackend(orc, a, M.make_weights(a, seed=4, perturb=True))
+    img = np.full((3, 32, 32), 0.55, np.float32)
+    whole = pkg.tiling.run_tiled(a, be, img, 0, 0)
+    got = pkg.tiling.run_tiled(a, be, img, tile, pad)
+    assert np.count_nonzero(got == 0.0) == 0
+    assert np.abs(got - whole).max() <= 1e-2
+
+
+def test_the_pad_rounds_up_to_a_whole_window(pkg, orc):
+    M = pkg.model
+    a = tiny(pkg)
+    be = OracleBackend(orc, a, M.make_weights(a, seed=5, perturb=True))
+    img = M.to_unit(M.input_uniform(40, 40, seed=6))
+    one = pkg.tiling.run_tiled(a, be, img, 8, 8)
+    for asked in (0, 1, 7, 8):
+        assert np.array_equal(pkg.tiling.run_tiled(a, be, img, 8, asked), one)
+    # one more pixel of context asks for a second window
+    two = pkg.tiling.run_tiled(a, be, img, 8, 9)
+    assert np.array_equal(two, pkg.tiling.run_tiled(a, be, img, 8, 16))
+    assert not np.array_equal(two, one)
+
+
+# ---- the HIP backend through the tile loop ---------------------------------------
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tile,pad", [(16, 8), (24, 16), (0, 0)])
+def test_tiled_device_matches_tiled_oracle(pkg, orc, tile, pad):
+    M = pkg.model
+    a = M.Arch(upsampler="pixelshuffle", scale=4, embed=24, heads=2, depths=[1, 1])
+    wts = M.make_weights(a, seed=7, perturb=True)
+    img = M.to_unit(M.input_sinusoids(40, 52, seed=8))
+    want = pkg.tiling.run_tiled(a, OracleBackend(orc, a, wts), img, tile, pad)
+    be = pkg.abi.HipBackend(a, wts)
+    try:
+        got = pkg.tiling.run_tiled(a, be, img, tile, pad)
+    finally:
+        be.close()
+    assert np.abs(got - want).max() < 1e-4
+
+
+@pytest.mark.gpu
+def test_config4_tile_geometry(pkg, orc):
+    """Config 4's tiling (1024x1024, 256-pixel tiles, 64 of context, the
+    compressed head) on a two-block model of the released width: every tile's
+    crop runs on a 392x392 plane; a corner and an interior tile are each held
+    against the oracle on the same crop, and the assembled image is finite and
+    fully written."""
+    M = pkg.model
+    a = M.Arch(upsampler="pixelshuffle_aux", scale=4, embed=180, heads=6, depths=[1, 1])
+    wts = M.make_weights(a, seed=5, perturb=True)
+    img = M.to_unit(M.input_sinusoids(1024, 1024, seed=5))
+    be = pkg.abi.HipBackend(a, wts)
+    try:
+        out = pkg.tiling.run_tiled(a, be, img, 256, 64)
+        for (y0, y1, x0, x1) in [(0, 320, 0, 320), (192, 576, 448, 832)]:
+            sub = np.ascontiguousarray(img[:, y0:y1, x0:x1])
+            x = M.adjust(a, sub)
+            got = be.forward(y1 - y0, x1 - x0, x)
+            got_aux = be.aux()
+            want, want_aux = orc.forward(a, wts, y1 - y0, x1 - x0, x)
+            assert np.abs(got - want).max() < 1e-4
+            assert np.abs(got_aux.reshape(want_aux.shape) - want_aux).max() < 1e-4
+    finally:
+        be.close()
+    assert out.shape == (3, 4096, 4096)
+    assert np.isfinite(out).all() and np.count_nonzero(out == 0.0) == 0
