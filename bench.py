@@ -40,12 +40,14 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_work(arch, h, w):
+def kernel_work(arch, h, w, hp=None, wp=None):
     """Algorithmic work per launch of each named kernel: (bound, flops, bytes).
     FLOPs count 2 per multiply-add over the real (unpadded) GEMM extents on the
-    padded plane; bytes are the minimum unique fp32 reads + writes."""
+    padded plane; bytes are the minimum unique fp32 reads + writes. (hp, wp)
+    default to the padded plane of an h x w image."""
     win, C, s, F = arch.window, arch.embed, arch.scale, arch.feat
-    hp, wp = (h // win + 1) * win, (w // win + 1) * win
+    if hp is None:
+        hp, wp = (h // win + 1) * win, (w // win + 1) * win
     P = hp * wp
     Hd = arch.mlp_ratio * C
     f = 4
@@ -110,6 +112,84 @@ def cpu_baseline(M, orc, arch, weights, sample, passes):
     }
 
 
+def kernel_table(be, work, steps):
+    """Per-kernel (launches, avg ms, share, rate) from the library's event
+    profiler, logged; returns the rows and the dominant kernel's roofline."""
+    rows = {}
+    for k in work:
+        ms, n = be.profile_query(k)
+        if n:
+            rows[k] = (ms, n)
+    total_dev = sum(ms for ms, _ in rows.values())
+    table = {}
+    for k, (ms, n) in sorted(rows.items(), key=lambda kv: -kv[1][0]):
+        bound, fl, by = work[k]
+        avg = ms / n
+        rate = (fl / (avg / 1e3) / 1e12) if bound == "mfma" else (by / (avg / 1e3) / 1e9)
+        unit = "TFLOP/s" if bound == "mfma" else "GB/s"
+        hbm = by / (avg / 1e3) / 1e9
+        log(f"  {k:24s} {n:5d} launches {avg:9.4f} ms avg {100 * ms / total_dev:5.1f}% "
+            f"{rate:9.2f} {unit}  ({hbm:7.1f} GB/s algorithmic)")
+        table[k] = {"launches": n, "avg_ms": round(avg, 4), "rate": round(rate, 2), "unit": unit,
+                    "frac": round(rate / (MFMA_FP32_PEAK / 1e12 if bound == "mfma" else HBM_PEAK / 1e9), 4),
+                    "algorithmic_GBps": round(hbm, 1)}
+    dom = max(rows, key=lambda k: rows[k][0])
+    bound, fl, by = work[dom]
+    avg_s = rows[dom][0] / rows[dom][1] / 1e3
+    if bound == "mfma":
+        achieved, peak, unit = fl / avg_s / 1e12, MFMA_FP32_PEAK / 1e12, "TFLOP/s"
+    else:
+        achieved, peak, unit = by / avg_s / 1e9, HBM_PEAK / 1e9, "GB/s"
+    roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(dom),
+                "kernel": dom, "avg_ms": round(avg_s * 1e3, 4),
+                "work_per_launch": fl if bound == "mfma" else by,
+                "device_ms_per_step": round(total_dev / steps, 3)}
+    return table, roofline
+
+
+def bench_rstb(args, pkg):
+    """Config 1: one RSTB (6 Swin V2 layers, shifts 0/4, then conv3x3 + 1x1 +
+    residual) on an UNPADDED 256x256x180 plane of N(0,1) activations (seed 2),
+    1024 windows; weights by the config-0 rules (seed 0). One JSON line with the
+    per-kernel rates."""
+    M, hip = pkg.model, pkg.hip
+    arch = M.Arch(upsampler="pixelshuffle", scale=2, embed=180, heads=6, depths=[6])
+    weights = M.make_weights(arch, seed=0)
+    hp = wp = 256
+    rng = np.random.Generator(np.random.PCG64(2))
+    x = rng.standard_normal((hp * wp, arch.embed), dtype=np.float32)
+    be = pkg.HipBackend(arch, weights)
+    din = hip.DeviceBuffer.from_array(x)
+    dout = hip.DeviceBuffer(din.n)
+    for _ in range(args.warmup):
+        be.rstb_device(0, hp, wp, din.ptr, dout.ptr)
+    hip.synchronize()
+    be.profile(True)
+    be.profile_reset()
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        be.rstb_device(0, hp, wp, din.ptr, dout.ptr)
+    hip.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    assert np.isfinite(dout.download()).all()
+    log(f"bench: rstb {args.steps} calls, {ms:.3f} ms per RSTB")
+    work = kernel_work(arch, hp, wp, hp=hp, wp=wp)
+    table, roofline = kernel_table(be, work, args.steps)
+    be.profile(False)
+    be.close()
+    print(json.dumps({
+        "metric": "single-RSTB ms, 256x256x180 fp32 (6 Swin V2 layers + conv3x3 + 1x1 + residual)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (N(0,1) activations seed 2, random-init weights seed 0)",
+        "config": {"workload": "config 1: single RSTB on an unpadded 256x256x180 plane",
+                   "windows": (hp // 8) * (wp // 8), "parallelism": "1 GPU"},
+        "roofline": roofline, "kernels": table}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,6 +199,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=256)
     ap.add_argument("--cpu-passes", type=int, default=3)
+    ap.add_argument("--workload", choices=["classical-x4", "rstb"], default="classical-x4",
+                    help="classical-x4: the BASELINE metric (default); rstb: config 1's "
+                         "single-RSTB micro-bench")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="before the warm-up, one device-to-device copy of this many MiB: the "
                          "plain copy kernel of known size that scales rocprofv3's FETCH_SIZE / "
@@ -131,6 +214,9 @@ def main():
         sys.exit(2)
 
     pkg = ge.load_package()
+    if args.workload == "rstb":
+        bench_rstb(args, pkg)
+        return
     M, hip = pkg.model, pkg.hip
     arch = M.classical(4)
     h = w = args.size
@@ -178,31 +264,19 @@ def main():
     log(f"bench: {args.steps} steps, {ms_per_step:.3f} ms/step, {value:.3f} output Mpix/s")
 
     work = kernel_work(arch, h, w)
-    rows = {}
-    for k in work:
-        ms, n = be.profile_query(k)
-        if n:
-            rows[k] = (ms, n)
-    total_dev = sum(ms for ms, _ in rows.values())
-    for k, (ms, n) in sorted(rows.items(), key=lambda kv: -kv[1][0]):
-        bound, fl, by = work[k]
-        avg = ms / n
-        rate = (fl / (avg / 1e3) / 1e12) if bound == "mfma" else (by / (avg / 1e3) / 1e9)
-        unit = "TFLOP/s" if bound == "mfma" else "GB/s"
-        log(f"  {k:24s} {n:5d} launches {avg:9.4f} ms avg {100 * ms / total_dev:5.1f}% "
-            f"{rate:9.2f} {unit}")
-    dom = max(rows, key=lambda k: rows[k][0])
-    bound, fl, by = work[dom]
-    avg_s = rows[dom][0] / rows[dom][1] / 1e3
-    if bound == "mfma":
-        achieved, peak, unit = fl / avg_s / 1e12, MFMA_FP32_PEAK / 1e12, "TFLOP/s"
-    else:
-        achieved, peak, unit = by / avg_s / 1e9, HBM_PEAK / 1e9, "GB/s"
-    roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(dom),
-                "kernel": dom, "avg_ms": round(avg_s * 1e3, 4),
-                "work_per_launch": fl if bound == "mfma" else by,
-                "device_ms_per_step": round(total_dev / args.steps, 3)}
+    table, roofline = kernel_table(be, work, args.steps)
+    be.profile(False)
+
+    # the crate's own boundary hands over host slices: s2s_forward uploads the
+    # input, runs, downloads the output (PCIe included); reported, never `value`
+    xh = np.ascontiguousarray(x)
+    be.forward(h, w, xh)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        be.forward(h, w, xh)
+    host_ms = (time.perf_counter() - t0) * 1e3 / 3
+    log(f"bench: host-buffer path (s2s_forward, PCIe included): {host_ms:.3f} ms, "
+        f"{(h * s) * (w * s) / 1e3 / host_ms:.3f} output Mpix/s")
 
     result = {
         "metric": METRIC, "value": round(value, 4), "unit": "Mpix/s", "n_gpus": 1,
@@ -214,8 +288,9 @@ def main():
                    "window": arch.window, "padded_plane": [(h // 8 + 1) * 8, (w // 8 + 1) * 8],
                    "parallelism": "1 GPU"},
         "roofline": roofline,
+        "kernels": table,
+        "host_path_mpix_s": round((h * s) * (w * s) / 1e3 / host_ms, 3),
     }
-    be.profile(False)
     be.close()
     if not args.no_cpu:
         orc = ge._load_oracle()
