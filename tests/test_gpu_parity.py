@@ -114,6 +114,29 @@ def test_linear(pkg, orc, rows, cin, cout, epi):
     assert err < 3e-5 * max(1.0, np.abs(want).max()), err
 
 
+@pytest.mark.parametrize("c", [180, 60, 27])
+def test_gelu_epilogue_against_exact_erf(pkg, c):
+    """The device GELU (an erfc-based polynomial form, both GEMM kernels'
+    epilogues: K = 180 and 60 take the weight-stationary kernel, 27 the tiled
+    one) against the float64 erf GELU over [-12, 12] and at 0 / -0 / tiny
+    arguments; an identity weight makes the GEMM pass each value through
+    exactly. Bar: 1e-6 absolute, the rounding of a float32 erff form."""
+    from scipy.special import erf
+    r = rng(c)
+    n = 8192
+    vals = np.concatenate([np.linspace(-12, 12, n * c // 2, dtype=np.float32),
+                           r.standard_normal(n * c // 2 - 6).astype(np.float32) * 2,
+                           np.float32([0.0, -0.0, 1e-30, -1e-30, 1e-7, -1e-7])])
+    x = vals.reshape(n, c)
+    eye = np.eye(c, dtype=np.float32)
+    got = pkg.abi.test_linear(x, eye, np.zeros(c, np.float32), epilogue=1)
+    xd = x.astype(np.float64)
+    want = 0.5 * xd * (1.0 + erf(xd / np.sqrt(2.0)))
+    err = np.abs(got - want).max()
+    assert err < 1e-6, err
+    assert np.all(got[x >= 0] >= 0) and np.all(got[x < 0] <= 0)
+
+
 @pytest.mark.parametrize("rows,cin,cout", [(37, 60, 60), (300, 180, 180), (129, 360, 180),
                                            (70, 120, 60), (23001, 180, 180), (19005, 360, 180)])
 @pytest.mark.parametrize("with_res", [False, True])
