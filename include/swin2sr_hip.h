@@ -154,6 +154,12 @@ int s2s_profile_report(s2s_ctx *ctx, float wall_ms);
  * launch count (after synchronising). Unknown names give 0 and 0. */
 int s2s_profile_query(s2s_ctx *ctx, const char *kernel, double *total_ms, int *launches);
 
+/* Restricts the profiler's event pairs to launches of one kernel name (NULL or
+ * "" = every launch, the default), so a timed run can carry the events of the
+ * kernel it reports without bracketing the others. No counterpart in the
+ * reference (its profiler always brackets every launch); a measurement aid. */
+int s2s_profile_only(s2s_ctx *ctx, const char *kernel);
+
 /* ---- the single-RSTB path (config 1 micro-bench) -------------------------- */
 
 /* One residual Swin transformer block group (stage `stage` of the checkpoint:

@@ -61,6 +61,7 @@ EXPORTS = {
     "s2s_profile_reset": (C.c_int, [C.c_void_p]),
     "s2s_profile_report": (C.c_int, [C.c_void_p, C.c_float]),
     "s2s_profile_query": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
+    "s2s_profile_only": (C.c_int, [C.c_void_p, C.c_char_p]),
     "s2s_rstb_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "s2s_test_window_map": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int32),
                                       C.POINTER(C.c_uint8)]),
@@ -207,6 +208,11 @@ class HipBackend:
 
     def profile_report(self, wall_ms: float = 0.0):
         check(self._lib.s2s_profile_report(self._ctx, wall_ms), "s2s_profile_report")
+
+    def profile_only(self, kernel: Optional[str]):
+        """Bracket only launches named `kernel` with events (None = all)."""
+        check(self._lib.s2s_profile_only(self._ctx, kernel.encode() if kernel else None),
+              "s2s_profile_only")
 
     def profile_query(self, kernel: str) -> Tuple[float, int]:
         ms = C.c_double()

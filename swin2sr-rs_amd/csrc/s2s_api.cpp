@@ -128,6 +128,7 @@ struct s2s_ctx {
     float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr, *bicf = nullptr;
 
     bool prof = false;
+    std::string prof_only;  // bracket only launches of this name ("" = all)
     std::vector<Pending> pending;
     std::vector<hipEvent_t> free_events;
     std::map<ProfKey, ProfRow> rows;
@@ -302,7 +303,8 @@ int s2s_ctx::drain() {
 template <typename F>
 int s2s_ctx::run(const char *name, dim3 grid, dim3 block, F &&launch) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (prof) {
+    const bool timed = prof && (prof_only.empty() || prof_only == name);
+    if (timed) {
         e0 = event();
         e1 = event();
         if (!e0 || !e1) return fail("hipEventCreate failed");
@@ -310,7 +312,7 @@ int s2s_ctx::run(const char *name, dim3 grid, dim3 block, F &&launch) {
     }
     hipError_t e = launch();
     if (e != hipSuccess) return fail(hip_msg(name, e));
-    if (prof) {
+    if (timed) {
         HIPCHK("hipEventRecord", hipEventRecord(e1, stream));
         pending.push_back(Pending{ProfKey{name, {grid.x, grid.y, grid.z}, {block.x, block.y, block.z}},
                                   e0, e1});
@@ -975,6 +977,12 @@ int s2s_profile_report(s2s_ctx *ctx, float wall_ms) {
                 r.second.calls, r.second.ms, r.second.ms / r.second.calls,
                 wall_ms > 0 ? 100.0 * r.second.ms / wall_ms : 0.0);
     }
+    return 0;
+}
+
+int s2s_profile_only(s2s_ctx *ctx, const char *kernel) {
+    if (!ctx) return fail("null context");
+    ctx->prof_only = kernel ? kernel : "";
     return 0;
 }
 

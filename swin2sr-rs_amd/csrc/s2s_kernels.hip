@@ -987,9 +987,15 @@ __global__ __launch_bounds__(256, 3) void k_wattn(AttnArgs g) {
     constexpr int NLD = (64 * 3 * V4MAX + 255) / 256;
     __shared__ float tile[64 * RS];
 
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch). The head groups of
+    // one window share the 128-byte lines their slices straddle, so they are
+    // numbered onto the same XCD (one L2): b = 8 * (HG * (wi / 8) + hg) + wi % 8.
     const int HG = (g.heads + 1) >> 1;
-    const int hg = blockIdx.x % HG;
-    const int wi = blockIdx.x / HG;
+    const int xcd = blockIdx.x & 7;
+    const int slot = blockIdx.x >> 3;
+    const int hg = slot % HG;
+    const int wi = (slot / HG) * 8 + xcd;
+    if (wi >= g.nw) return;  // the grid is padded to whole groups of 8 windows
     const int nh = min(2, g.heads - 2 * hg);
     const int v4 = nh * HD / 4;         // float4s per segment in this group
     const int tid = threadIdx.x;
@@ -1705,7 +1711,7 @@ static bool wattn_eligible(const AttnArgs &g) {
 
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out) {
     if (wattn_eligible(g)) {
-        const unsigned grid = (unsigned)(g.nw * ((g.heads + 1) / 2));
+        const unsigned grid = (unsigned)(((g.nw + 7) / 8) * 8 * ((g.heads + 1) / 2));
         if (grid_out) *grid_out = grid;
         switch (g.head_dim) {
         case 2: hipLaunchKernelGGL(k_wattn<2>, dim3(grid), dim3(256), 0, st, g); break;
@@ -1722,7 +1728,7 @@ hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_ou
 }
 
 unsigned attention_grid(const AttnArgs &g) {
-    return wattn_eligible(g) ? (unsigned)(g.nw * ((g.heads + 1) / 2))
+    return wattn_eligible(g) ? (unsigned)(((g.nw + 7) / 8) * 8 * ((g.heads + 1) / 2))
                              : (unsigned)((g.nw * g.heads + 3) / 4);
 }
 
