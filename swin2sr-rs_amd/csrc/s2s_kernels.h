@@ -73,6 +73,7 @@ struct AttnArgs {
     int hp, wp, nww, nw;
     int heads, head_dim, c;
     int shift;
+    int nws;                   // k_wattn: window lanes per XCD (set by launch_attention)
 };
 
 #define GEMM_NVARIANTS 6

@@ -363,6 +363,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 // ---------------------------------------------------------------------------
 
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x4f32((a), (b), (c), 0, 0, 0)
 
 // LDS row stride (floats) of an A tile: a multiple of 4 that is an odd
@@ -392,6 +393,18 @@ __device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
 }
 __device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, 0);
+}
+// The same with a wave-uniform part of the offset in the instruction's SGPR
+// offset (only for accesses known to be in range: the bounds check is not
+// meant to be relied on for that part).
+__device__ __forceinline__ float4 buf_load4s(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, int soff, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, voff, soff, 0);
 }
 
 // Direct global -> LDS copy (gfx950 buffer_load_dwordx4 ... lds): lane l of the
@@ -955,28 +968,45 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// k_wattn: the same window attention, one workgroup per (window, head pair).
+// k_wattn: the same window attention, persistent workgroups that each own one
+// head pair and walk a list of windows.
 //
-// The window's q, k and v slices of its two heads (64 tokens x 3 x 2*hd floats)
-// are loaded once with coalesced float4 loads - each token's slice is a
-// contiguous 8*hd-byte run of its qkv row - into LDS, [token][q | k | v] rows of
-// 6*hd + 2 floats (an odd number of float2s, so 16 consecutive rows read by a
-// ds_read_b64 land in distinct bank pairs). Wave w handles head 2*hg + w/2 and
-// query tile w%2 (32 queries):
+// A unit of work is (window, head pair). The window's q, k and v slices of its
+// two heads (64 tokens x 3 x 2*hd floats) are loaded with coalesced float4
+// loads - each token's slice is a contiguous 8*hd-byte run of its qkv row -
+// into LDS, [token][q | k | v] rows of 6*hd + 2 floats (an odd number of
+// float2s, so 16 consecutive rows read by a ds_read_b64 land in distinct bank
+// pairs). The loads of the NEXT window are issued into registers before the
+// current window is computed, so they are in flight under its MFMAs and
+// softmax (a non-persistent workgroup would load, then compute, then store,
+// and the workgroups of a CU fall into step with each other). Wave w handles
+// head 2*hg + w/2 and query tile w%2 (32 queries):
 //   - its q row and the 64 k rows come out of LDS as MFMA operands (step j of
 //     lane half hh covers d = 4(j/2) + 2hh + j%2, then d = hd-2+hh for the odd
 //     tail pair), scaled in registers by exp(min(ls, ln 100))/|q| and 1/|k|;
 //   - S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x2f32 with the softmax in
 //     registers between them, as in k_attention; the bias table values a lane
-//     needs are loaded once (32 floats);
+//     needs (32 floats) depend on the head only, so they are loaded once;
 //   - O^T goes back into the wave's own q rows of the LDS tile (no other wave
-//     reads them), and after one barrier the workgroup writes the window's
-//     output slices with coalesced float4 stores.
-// Three workgroups fit a CU (46.6 KB of LDS each at hd = 30), so one
-// workgroup's loads overlap the others' MFMAs.
+//     reads them), and after a barrier the workgroup writes the window's output
+//     slices with coalesced float4 stores.
+// Two workgroups share a CU at hd = 30 (46.6 KB of LDS each). Barriers are
+// LDS-only (lds_sync): the output stores and the next window's loads stay in
+// flight across them.
+//
+// Work assignment: workgroup b runs on XCD b % 8 (round-robin dispatch); its
+// slot s = b / 8 on that XCD fixes the head pair hg = s % HG and a window lane
+// ws = s / HG, and it takes windows xcd + 8 * (ws + nws * k), k = 0, 1, ...
+// where nws is the number of window lanes per XCD. All head pairs of a window
+// then run at the same time on the same XCD and share the 128-byte lines their
+// slices straddle in that XCD's L2.
 // ---------------------------------------------------------------------------
+// Resident workgroups per CU: 3 by LDS (46.6 KB each at hd = 30) and by
+// registers; at hd = 32 the registers leave room for 2 without spilling.
+__host__ __device__ constexpr int wattn_per_cu(int hd) { return hd > 30 ? 2 : 3; }
+
 template <int HD>
-__global__ __launch_bounds__(256, 3) void k_wattn(AttnArgs g) {
+__global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     static_assert(HD % 2 == 0 && HD <= 32, "even head_dim <= 32");
     constexpr int NS = HD / 2;          // MFMA k-steps over d
     constexpr int G4 = HD / 4;          // float2 pairs of steps
@@ -984,214 +1014,240 @@ __global__ __launch_bounds__(256, 3) void k_wattn(AttnArgs g) {
     constexpr int W = 2 * HD;           // floats per segment (two heads)
     constexpr int RS = 6 * HD + 2;      // LDS row stride
     constexpr int V4MAX = W / 4;        // float4s per segment
-    constexpr int NLD = (64 * 3 * V4MAX + 255) / 256;
+    constexpr int PER_TOK = 3 * V4MAX;  // float4s of one token's slices
+    static_assert(PER_TOK <= 64 && V4MAX <= 16, "a token's slices fit one wave");
     __shared__ float tile[64 * RS];
 
-    // Workgroup b runs on XCD b % 8 (round-robin dispatch). The head groups of
-    // one window share the 128-byte lines their slices straddle, so they are
-    // numbered onto the same XCD (one L2): b = 8 * (HG * (wi / 8) + hg) + wi % 8.
     const int HG = (g.heads + 1) >> 1;
     const int xcd = blockIdx.x & 7;
     const int slot = blockIdx.x >> 3;
     const int hg = slot % HG;
-    const int wi = (slot / HG) * 8 + xcd;
-    if (wi >= g.nw) return;  // the grid is padded to whole groups of 8 windows
+    const int ws = slot / HG;
+    const int wstep = 8 * g.nws;        // window stride of one workgroup
     const int nh = min(2, g.heads - 2 * hg);
     const int v4 = nh * HD / 4;         // float4s per segment in this group
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hl = wave >> 1;
     const int qt = wave & 1;
     const int r = lane & 31;
     const int hh = lane >> 5;
-    const int wh = wi / g.nww;
-    const int ww = wi - wh * g.nww;
     const int shift = g.shift;
     const int head = 2 * hg + hl;
     const bool active = hl < nh;
-    const size_t ld = (size_t)3 * g.c;
+    const int C = g.c;
+    const int ld = 3 * C;
+    const int qtok = 32 * qt + r;
 
-    // ---- the window's slices -> LDS (all loads in flight together) ----
-    // Element i of the copy is (token, segment, float4) with compile-time
-    // divisors; a one-head group skips the second head's float4s.
+    // Copy-in: wave w moves tokens 4u + w (u = 0..15), one token per
+    // instruction, lane l taking float4 l of the token's q | k | v slices.
+    // Token (row u/2, column 4(u%2) + w of the window) is the same for the
+    // whole wave, so its pixel offset is scalar work and goes in the
+    // instruction's SGPR offset; the lane's column offset is fixed. Lanes past
+    // the slices (and float4s past a one-head group's) repeat an earlier
+    // float4: same address, same value, no branch.
+    const int li = lane % PER_TOK;
+    const int lseg = li / V4MAX;
+    const int lc4 = min(li - lseg * V4MAX, v4 - 1);
+    const int colq = (lseg * C + 2 * hg * HD + 4 * lc4) * 4;       // bytes in a qkv row
+    float *const ldsq = tile + wave * RS + lseg * W + 4 * lc4;      // + 4u * RS
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qkv, (size_t)g.hp * g.wp * ld * 4);
+    auto load_window = [&](int wi, float4 (&buf)[16]) __attribute__((always_inline)) {
+        const int wv = wi < g.nw ? wi : 0;  // past the end: any in-range window
+        const int wh = wv / g.nww;
+        const int ww = wv - wh * g.nww;
+        int x0 = 8 * ww + wave + shift;
+        if (x0 >= g.wp) x0 -= g.wp;
+        int x1 = 8 * ww + 4 + wave + shift;
+        if (x1 >= g.wp) x1 -= g.wp;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            int y = 8 * wh + (u >> 1) + shift;
+            if (y >= g.hp) y -= g.hp;
+            const int pix = y * g.wp + ((u & 1) ? x1 : x0);
+            buf[u] = buf_load4s(rq, colq, pix * ld * 4);
+        }
+    };
+
+    // Copy-out: 4 tokens per instruction, 16 lanes each (lane 16t + c takes
+    // float4 c of token 16u + 4w + t); the row is scalar, the column per lane.
+    const int otq = lane >> 4;
+    const int oc4 = min(lane & 15, v4 - 1);
+    const int otj = 4 * (wave & 1) + otq;                           // column in the window
+    const float *const ldso = tile + (4 * wave + otq) * RS + 4 * oc4;  // + 16u * RS
+    const int colo = (2 * hg * HD + 4 * oc4) * 4;
+    const __amdgpu_buffer_rsrc_t ro = buf_rsrc(g.out, (size_t)g.hp * g.wp * C * 4);
+
+    // the clamped logit scale (per head, the same for every window) and the
+    // bias values this lane adds: query 32qt + r, keys 32kt + 8a + 4hh + b
+    const float ls = active ? __expf(fminf(g.logit_scale[head], 4.605170185988092f)) : 0.f;
+    const float *cp = g.cpbt + ((size_t)(active ? head : 0) * 64 + qtok) * 64 + 4 * hh;
+
+    constexpr int NST = 4;              // output stores per thread
+    int wi = xcd + 8 * ws;
+    float4 buf[16];
+    load_window(wi, buf);
+    // as many dropped stores as a window's output has: the loop is then entered
+    // with the same queue (loads, then stores) as it loops back with, and the
+    // compiler's waits for the slices need not drain the previous stores
     {
-        constexpr int PER_TOK = 3 * V4MAX;
-        float4 buf[NLD];
+        const __amdgpu_buffer_rsrc_t rnull = buf_rsrc(g.out, 0);  // every offset out of range
 #pragma unroll
-        for (int u = 0; u < NLD; ++u) {
-            const int i = tid + 256 * u;
-            const int tok = i / PER_TOK;
-            const int rem = i - tok * PER_TOK;
-            const int seg = rem / V4MAX;
-            const int c4 = rem - seg * V4MAX;
-            buf[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (tok < 64 && c4 < v4) {
-                const int pix = win_pixel(wh, ww, tok, shift, g.hp, g.wp);
-                buf[u] = *reinterpret_cast<const float4 *>(g.qkv + (size_t)pix * ld + seg * g.c +
-                                                           2 * hg * HD + 4 * c4);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < NLD; ++u) {
-            const int i = tid + 256 * u;
-            const int tok = i / PER_TOK;
-            const int rem = i - tok * PER_TOK;
-            const int seg = rem / V4MAX;
-            const int c4 = rem - seg * V4MAX;
-            if (tok < 64) {
-                float *dst = tile + tok * RS + seg * W + 4 * c4;
-                *reinterpret_cast<float2 *>(dst) = make_float2(buf[u].x, buf[u].y);
-                *reinterpret_cast<float2 *>(dst + 2) = make_float2(buf[u].z, buf[u].w);
-            }
-        }
+        for (int u = 0; u < NST; ++u) buf_store4(rnull, 16 * u, make_float4(0.f, 0.f, 0.f, 0.f));
     }
-    // the bias values this lane adds: query 32qt + r, keys 32kt + 8a + 4hh + b
-    float bias[2][16];
-    if (active) {
-        const float *cp = g.cpbt + ((size_t)head * 64 + 32 * qt + r) * 64;
+    while (wi < g.nw) {
+        // ---- this window's slices -> LDS (the previous window's output
+        // stores have read the tile: barrier at the end of the loop) ----
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const float4 b4 = *reinterpret_cast<const float4 *>(cp + 32 * kt + 8 * a + 4 * hh);
-                bias[kt][4 * a + 0] = b4.x;
-                bias[kt][4 * a + 1] = b4.y;
-                bias[kt][4 * a + 2] = b4.z;
-                bias[kt][4 * a + 3] = b4.w;
-            }
-    }
-    __syncthreads();
-
-    if (active) {
-        const float ls = __expf(fminf(g.logit_scale[head], 4.605170185988092f));
-        // q operands (this lane's query, its half of d), normalised and scaled
-        float qop[NS];
-        {
-            const float *qrow = tile + (32 * qt + r) * RS + hl * HD;
-#pragma unroll
-            for (int s2 = 0; s2 < G4; ++s2) {
-                const float2 v = *reinterpret_cast<const float2 *>(qrow + 4 * s2 + 2 * hh);
-                qop[2 * s2] = v.x;
-                qop[2 * s2 + 1] = v.y;
-            }
-            if (TAIL) qop[NS - 1] = qrow[4 * G4 + hh];
-            float qs = 0.f;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) qs += qop[j] * qop[j];
-            qs += __shfl_xor(qs, 32, 64);
-            const float qsc = ls / fmaxf(sqrtf(qs), 1e-12f);
-#pragma unroll
-            for (int j = 0; j < NS; ++j) qop[j] *= qsc;
+        for (int u = 0; u < 16; ++u) {
+            float *dst = ldsq + 4 * u * RS;
+            *reinterpret_cast<float2 *>(dst) = make_float2(buf[u].x, buf[u].y);
+            *reinterpret_cast<float2 *>(dst + 2) = make_float2(buf[u].z, buf[u].w);
         }
-        float kop[2][NS];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const float *krow = tile + (32 * kt + r) * RS + W + hl * HD;
-#pragma unroll
-            for (int s2 = 0; s2 < G4; ++s2) {
-                const float2 v = *reinterpret_cast<const float2 *>(krow + 4 * s2 + 2 * hh);
-                kop[kt][2 * s2] = v.x;
-                kop[kt][2 * s2 + 1] = v.y;
-            }
-            if (TAIL) kop[kt][NS - 1] = krow[4 * G4 + hh];
-            float ks = 0.f;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) ks += kop[kt][j] * kop[kt][j];
-            ks += __shfl_xor(ks, 32, 64);
-            const float ksc = 1.0f / fmaxf(sqrtf(ks), 1e-12f);
-#pragma unroll
-            for (int j = 0; j < NS; ++j) kop[kt][j] *= ksc;
-        }
-
+        lds_sync();
+        // S^T starts from the bias (an L2-resident table): its loads are issued
+        // before the next window's, so waiting for them leaves those in flight
         f16v s[2];
+        if (active) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[kt][e] = 0.f;
-#pragma unroll
-        for (int j = 0; j < NS; ++j)
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) s[kt] = MFMA32(kop[kt][j], qop[j], s[kt]);
-
-        // bias, shift mask, softmax over the query's 64 keys (2 lanes). The
-        // mask bands (win_band) are all 0 except in the last window row and
-        // column of a shifted block, where a token's band is 1 or 2 by whether
-        // its row (column) inside the window is below 8 - shift.
-        const int qtok = 32 * qt + r;
-        const bool ey = shift && (wh * 8 + 8 >= g.hp);
-        const bool ex = shift && (ww * 8 + 8 >= g.wp);
-        const bool qy = (qtok >> 3) < 8 - shift;
-        const bool qx = (qtok & 7) < 8 - shift;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                float v = s[kt][e] + bias[kt][e];
-                if (ey || ex) {
-                    const int krow = 4 * kt + (e >> 2);        // key >> 3
-                    const int kcol = 4 * hh + (e & 3);         // key & 7
-                    const bool dy = ey && ((krow < 8 - shift) != qy);
-                    const bool dx = ex && ((kcol < 8 - shift) != qx);
-                    if (dy || dx) v -= 100.f;
+                for (int a = 0; a < 4; ++a) {
+                    const float4 b4 = *reinterpret_cast<const float4 *>(cp + 32 * kt + 8 * a);
+                    s[kt][4 * a + 0] = b4.x;
+                    s[kt][4 * a + 1] = b4.y;
+                    s[kt][4 * a + 2] = b4.z;
+                    s[kt][4 * a + 3] = b4.w;
                 }
-                s[kt][e] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        float sum = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float p = __expf(s[kt][e] - mx);
-                s[kt][e] = p;
-                sum += p;
-            }
-        sum += __shfl_xor(sum, 32, 64);
-        const float inv = 1.0f / sum;
-
-        // O^T = V^T P^T: lane r supplies V[key][d = r]
-        f16v o;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[e] = 0.f;
-        const float *vcol = tile + 2 * W + hl * HD + r;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int key = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
-                const float vv = (r < HD) ? vcol[key * RS] : 0.f;
-                o = MFMA32(vv, s[kt][e], o);
-            }
-        // into this wave's own q rows (no other wave reads them)
-        float *orow = tile + qtok * RS + hl * HD;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
-            if (d < HD) orow[d] = o[e] * inv;
         }
-    }
-    __syncthreads();
+        const int wn = wi + wstep;
+        load_window(wn, buf);  // in flight under this window's math
+        const int wh = wi / g.nww;
+        const int ww = wi - wh * g.nww;
 
-    // ---- the window's output slices, coalesced ----
-    {
-        constexpr int NST = (64 * V4MAX + 255) / 256;
+        if (active) {
+            // q operands (this lane's query, its half of d), normalised and scaled
+            float qop[NS];
+            {
+                const float *qrow = tile + qtok * RS + hl * HD;
 #pragma unroll
-        for (int u = 0; u < NST; ++u) {
-            const int i = tid + 256 * u;
-            const int tok = i / V4MAX;
-            const int c4 = i - tok * V4MAX;
-            if (tok < 64 && c4 < v4) {
-                const float *src = tile + tok * RS + 4 * c4;
+                for (int s2 = 0; s2 < G4; ++s2) {
+                    const float2 v = *reinterpret_cast<const float2 *>(qrow + 4 * s2 + 2 * hh);
+                    qop[2 * s2] = v.x;
+                    qop[2 * s2 + 1] = v.y;
+                }
+                if (TAIL) qop[NS - 1] = qrow[4 * G4 + hh];
+                float qs = 0.f;
+#pragma unroll
+                for (int j = 0; j < NS; ++j) qs += qop[j] * qop[j];
+                qs += __shfl_xor(qs, 32, 64);
+                const float qsc = ls / fmaxf(sqrtf(qs), 1e-12f);
+#pragma unroll
+                for (int j = 0; j < NS; ++j) qop[j] *= qsc;
+            }
+            float kop[2][NS];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const float *krow = tile + (32 * kt + r) * RS + W + hl * HD;
+#pragma unroll
+                for (int s2 = 0; s2 < G4; ++s2) {
+                    const float2 v = *reinterpret_cast<const float2 *>(krow + 4 * s2 + 2 * hh);
+                    kop[kt][2 * s2] = v.x;
+                    kop[kt][2 * s2 + 1] = v.y;
+                }
+                if (TAIL) kop[kt][NS - 1] = krow[4 * G4 + hh];
+                float ks = 0.f;
+#pragma unroll
+                for (int j = 0; j < NS; ++j) ks += kop[kt][j] * kop[kt][j];
+                ks += __shfl_xor(ks, 32, 64);
+                const float ksc = 1.0f / fmaxf(sqrtf(ks), 1e-12f);
+#pragma unroll
+                for (int j = 0; j < NS; ++j) kop[kt][j] *= ksc;
+            }
+
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt) s[kt] = MFMA32(kop[kt][j], qop[j], s[kt]);
+
+            // bias, shift mask, softmax over the query's 64 keys (2 lanes). The
+            // mask bands (win_band) are all 0 except in the last window row and
+            // column of a shifted block, where a token's band is 1 or 2 by
+            // whether its row (column) inside the window is below 8 - shift.
+            const bool ey = shift && (wh * 8 + 8 >= g.hp);
+            const bool ex = shift && (ww * 8 + 8 >= g.wp);
+            const bool qy = (qtok >> 3) < 8 - shift;
+            const bool qx = (qtok & 7) < 8 - shift;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    float v = s[kt][e];
+                    if (ey || ex) {
+                        const int krow = 4 * kt + (e >> 2);        // key >> 3
+                        const int kcol = 4 * hh + (e & 3);         // key & 7
+                        const bool dy = ey && ((krow < 8 - shift) != qy);
+                        const bool dx = ex && ((kcol < 8 - shift) != qx);
+                        if (dy || dx) v -= 100.f;
+                    }
+                    s[kt][e] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            float sum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float p = __expf(s[kt][e] - mx);
+                    s[kt][e] = p;
+                    sum += p;
+                }
+            sum += __shfl_xor(sum, 32, 64);
+            const float inv = 1.0f / sum;
+
+            // O^T = V^T P^T: lane r supplies V[key][d = r]
+            f16v o;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[e] = 0.f;
+            const float *vcol = tile + 2 * W + hl * HD + r;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+                    const float vv = (r < HD) ? vcol[key * RS] : 0.f;
+                    o = MFMA32(vv, s[kt][e], o);
+                }
+            // into this wave's own q rows (no other wave reads them)
+            float *orow = tile + qtok * RS + hl * HD;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
+                if (d < HD) orow[d] = o[e] * inv;
+            }
+        }
+        lds_sync();
+
+        // ---- the window's output slices, coalesced ----
+        {
+            int x = 8 * ww + otj + shift;
+            if (x >= g.wp) x -= g.wp;
+            const int xo = x * C * 4 + colo;
+#pragma unroll
+            for (int u = 0; u < NST; ++u) {
+                const float *src = ldso + 16 * u * RS;
                 const float2 a = *reinterpret_cast<const float2 *>(src);
                 const float2 b = *reinterpret_cast<const float2 *>(src + 2);
-                const int pix = win_pixel(wh, ww, tok, shift, g.hp, g.wp);
-                *reinterpret_cast<float4 *>(g.out + (size_t)pix * g.c + 2 * hg * HD + 4 * c4) =
-                    make_float4(a.x, a.y, b.x, b.y);
+                int y = 8 * wh + 2 * u + (wave >> 1) + shift;
+                if (y >= g.hp) y -= g.hp;
+                buf_store4s(ro, xo, y * g.wp * C * 4, make_float4(a.x, a.y, b.x, b.y));
             }
         }
+        lds_sync();
+        wi = wn;
     }
 }
 
@@ -1709,9 +1765,20 @@ static bool wattn_eligible(const AttnArgs &g) {
     return true;
 }
 
-hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out) {
-    if (wattn_eligible(g)) {
-        const unsigned grid = (unsigned)(((g.nw + 7) / 8) * 8 * ((g.heads + 1) / 2));
+// k_wattn's persistent grid: 8 XCDs x HG head pairs x nws window lanes, about
+// as many workgroups as the CUs hold at once, never more lanes than an XCD has
+// windows.
+static int wattn_lanes(const AttnArgs &g) {
+    const int HG = (g.heads + 1) / 2;
+    const int per_xcd = (g.nw + 7) / 8;
+    return std::max(1, std::min(per_xcd, wattn_per_cu(g.head_dim) * cu_count() / (8 * HG)));
+}
+
+hipError_t launch_attention(const AttnArgs &g0, hipStream_t st, unsigned *grid_out) {
+    if (wattn_eligible(g0)) {
+        AttnArgs g = g0;
+        g.nws = wattn_lanes(g);
+        const unsigned grid = (unsigned)(8 * ((g.heads + 1) / 2) * g.nws);
         if (grid_out) *grid_out = grid;
         switch (g.head_dim) {
         case 2: hipLaunchKernelGGL(k_wattn<2>, dim3(grid), dim3(256), 0, st, g); break;
@@ -1721,6 +1788,7 @@ hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_ou
         }
         return hipGetLastError();
     }
+    const AttnArgs &g = g0;
     const unsigned grid = (unsigned)((g.nw * g.heads + 3) / 4);
     if (grid_out) *grid_out = grid;
     hipLaunchKernelGGL(k_attention, dim3(grid), dim3(256), 0, st, g);
@@ -1728,7 +1796,7 @@ hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_ou
 }
 
 unsigned attention_grid(const AttnArgs &g) {
-    return wattn_eligible(g) ? (unsigned)(((g.nw + 7) / 8) * 8 * ((g.heads + 1) / 2))
+    return wattn_eligible(g) ? (unsigned)(8 * ((g.heads + 1) / 2) * wattn_lanes(g))
                              : (unsigned)((g.nw * g.heads + 3) / 4);
 }
 
