@@ -35,6 +35,42 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 #define MFMA32(a, b, c) __builtin_amdgcn_mfma_f32_32x32x2f32((a), (b), (c), 0, 0, 0)
 
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// Raw buffer access: a load whose byte offset lies past the resource's size
+// returns zero and such a store is dropped, so tile edges (rows past M, columns
+// past the group) need no branches, and every wave issues the same number of
+// memory instructions on every path - which lets the compiler count them
+// exactly in its s_waitcnt instead of draining the queue.
+#define BUF_OOB 0x7ffffff0
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu),
+                                             0x00020000);
+}
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, 0);
+}
+// The same with a wave-uniform part of the offset in the instruction's SGPR
+// offset (only for accesses known to be in range: the bounds check is not
+// meant to be relied on for that part).
+__device__ __forceinline__ float4 buf_load4s(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, int soff, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, voff, soff, 0);
+}
+
+
 // The erf GELU, 0.5 v (1 + erf(v/sqrt2)) = v * Phi(v), evaluated through the
 // complementary error function so that one branch-free formula covers every v:
 // with t = |v|/sqrt2, erfc(t) = exp(-t^2) * erfcx(t), and the scaled function
@@ -90,41 +126,6 @@ __device__ __forceinline__ float gelu_erf(float v) {
 #define KC 32
 #define LDS_S 36
 
-template <int ALOAD>
-__device__ __forceinline__ float4 load_a4(const GemmArgs &g, int m, int k) {
-    float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m >= g.M || k >= g.K) return z;
-    if (ALOAD == ALOAD_ROWS) {
-        return *reinterpret_cast<const float4 *>(g.A + (size_t)m * g.lda + k);
-    } else if (ALOAD == ALOAD_IM2COL_UP2) {
-        // the conv runs on the H x W nearest-2x upsampling of an (H/2) x (W/2)
-        // plane; the upsampled plane is never materialised
-        const int tap = k / g.cin;
-        const int ci = k - tap * g.cin;
-        const int y = m / g.W;
-        const int x = m - y * g.W;
-        const int sy = y + tap / 3 - 1;
-        const int sx = x + tap % 3 - 1;
-        if (sy < 0 || sy >= g.H || sx < 0 || sx >= g.W) return z;
-        return *reinterpret_cast<const float4 *>(
-            g.A + ((size_t)(sy >> 1) * (g.W >> 1) + (sx >> 1)) * g.cin + ci);
-    } else {
-        const int tap = k / g.cin;
-        const int ci = k - tap * g.cin;
-        const int y = m / g.W;
-        const int x = m - y * g.W;
-        const int sy = y + tap / 3 - 1;
-        const int sx = x + tap % 3 - 1;
-        if (sy < 0 || sy >= g.H || sx < 0 || sx >= g.W) return z;
-        return *reinterpret_cast<const float4 *>(g.A + ((size_t)sy * g.W + sx) * g.cin + ci);
-    }
-}
-
-__device__ __forceinline__ float4 load_b4(const GemmArgs &g, int n, int k) {
-    if (n >= g.N || k >= g.K) return make_float4(0.f, 0.f, 0.f, 0.f);
-    return *reinterpret_cast<const float4 *>(g.B + (size_t)n * g.ldb + k);
-}
-
 template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     static_assert(WM * WN == 4, "four wavefronts");
@@ -159,17 +160,70 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     float4 ra[AV], rb[BV];
     const int nk = (g.K + KC - 1) / KC;
 
-    auto load_chunk = [&](int k0) {
+    // Loader state. Thread t copies float4 (t & 7) of a K chunk for rows
+    // m0 + (t >> 3) + 32i of A and n0 + (t >> 3) + 32i of B, the same k in every
+    // chunk-relative slot, so everything that depends on the row (its pixel
+    // y, x) is computed once, and the k-dependent part (tap, ci and the tap's
+    // pixel shift) once per chunk for all of the thread's rows. Raw buffer
+    // loads: an element outside A or B (rows past M or N, k past K, a tap
+    // outside the plane) reads zero from an out-of-range offset, without a
+    // branch.
+    const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(
+        g.A, ALOAD == ALOAD_ROWS ? (size_t)g.M * g.lda * 4
+                                 : (size_t)g.H * g.W * g.cin * 4 / (ALOAD == ALOAD_IM2COL_UP2 ? 4 : 1));
+    const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
+    const int kq = (tid & 7) * 4;
+    int am[AV], ay[AV], ax[AV], bo[BV];
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+        am[i] = m0 + (tid >> 3) + 32 * i;
+        ay[i] = ALOAD == ALOAD_ROWS ? 0 : am[i] / g.W;
+        ax[i] = ALOAD == ALOAD_ROWS ? 0 : am[i] - ay[i] * g.W;
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+        const int n = n0 + (tid >> 3) + 32 * i;
+        bo[i] = n < g.N ? (n * g.ldb + kq) * 4 : -1;
+    }
+    // (tap, ci) of k = k0 + kq for the chunk at k0, and the tap's shift
+    int tap = 0, ci = kq, dy = -1, dx = -1;
+    auto norm_k = [&]() __attribute__((always_inline)) {
+        if (ALOAD == ALOAD_ROWS) return;
+        while (ci >= g.cin) {
+            ci -= g.cin;
+            ++tap;
+            if (++dx > 1) {
+                dx = -1;
+                ++dy;
+            }
+        }
+    };
+    norm_k();
+
+    auto load_chunk = [&](int k0) __attribute__((always_inline)) {
+        const bool kok = k0 + kq < g.K;
+        const int shift_px = dy * g.W + dx;
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
-            const int idx = tid + i * 256;
-            ra[i] = load_a4<ALOAD>(g, m0 + (idx >> 3), k0 + (idx & 7) * 4);
+            int off;
+            if (ALOAD == ALOAD_ROWS) {
+                off = (am[i] < g.M && kok) ? (am[i] * g.lda + k0 + kq) * 4 : BUF_OOB;
+            } else {
+                const int sy = ay[i] + dy, sx = ax[i] + dx;
+                const bool ok = am[i] < g.M && kok && (unsigned)sy < (unsigned)g.H &&
+                                (unsigned)sx < (unsigned)g.W;
+                const int px = ALOAD == ALOAD_IM2COL_UP2 ? (sy >> 1) * (g.W >> 1) + (sx >> 1)
+                                                         : am[i] + shift_px;
+                off = ok ? (px * g.cin + ci) * 4 : BUF_OOB;
+            }
+            ra[i] = buf_load4(ra_rs, off);
         }
 #pragma unroll
-        for (int i = 0; i < BV; ++i) {
-            const int idx = tid + i * 256;
-            rb[i] = load_b4(g, n0 + (idx >> 3), k0 + (idx & 7) * 4);
-        }
+        for (int i = 0; i < BV; ++i)
+            rb[i] = buf_load4(rb_rs, (bo[i] >= 0 && kok) ? bo[i] + k0 * 4 : BUF_OOB);
+        // on to the next chunk's k
+        ci += KC;
+        norm_k();
     };
 
     load_chunk(0);
@@ -363,7 +417,6 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 // ---------------------------------------------------------------------------
 
 typedef float f4v __attribute__((ext_vector_type(4)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x4f32((a), (b), (c), 0, 0, 0)
 
 // LDS row stride (floats) of an A tile: a multiple of 4 that is an odd
@@ -372,39 +425,6 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 __host__ __device__ constexpr int bs_lds_stride(int k) {
     return (k % 32 == 4 || k % 32 == 12 || k % 32 == 20 || k % 32 == 28) ? k
            : (k % 8 == 0) ? k + 4 : k + 8;
-}
-
-// Raw buffer access: a load whose byte offset lies past the resource's size
-// returns zero and such a store is dropped, so tile edges (rows past M, columns
-// past the group) need no branches, and every wave issues the same number of
-// memory instructions on every path - which lets the compiler count them
-// exactly in its s_waitcnt instead of draining the queue.
-#define BUF_OOB 0x7ffffff0
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
-                                             (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu),
-                                             0x00020000);
-}
-__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-__device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-__device__ __forceinline__ void buf_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
-}
-__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, float4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, 0);
-}
-// The same with a wave-uniform part of the offset in the instruction's SGPR
-// offset (only for accesses known to be in range: the bounds check is not
-// meant to be relied on for that part).
-__device__ __forceinline__ float4 buf_load4s(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-__device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, int soff, float4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, voff, soff, 0);
 }
 
 // Direct global -> LDS copy (gfx950 buffer_load_dwordx4 ... lds): lane l of the
@@ -1084,10 +1104,29 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     const float ls = active ? __expf(fminf(g.logit_scale[head], 4.605170185988092f)) : 0.f;
     const float *cp = g.cpbt + ((size_t)(active ? head : 0) * 64 + qtok) * 64 + 4 * hh;
 
+    // S^T starts from the bias (an L2-resident table, the same for every
+    // window): the values for the next window are loaded as soon as AV has
+    // consumed the accumulators, so they are in flight across the output
+    // stores and the copy-in, and they are older than the next prefetch.
+    f16v s[2];
+    auto load_bias = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float4 b4 = *reinterpret_cast<const float4 *>(cp + 32 * kt + 8 * a);
+                s[kt][4 * a + 0] = b4.x;
+                s[kt][4 * a + 1] = b4.y;
+                s[kt][4 * a + 2] = b4.z;
+                s[kt][4 * a + 3] = b4.w;
+            }
+    };
+
     constexpr int NST = 4;              // output stores per thread
     int wi = xcd + 8 * ws;
     float4 buf[16];
     load_window(wi, buf);
+    load_bias();
     // as many dropped stores as a window's output has: the loop is then entered
     // with the same queue (loads, then stores) as it loops back with, and the
     // compiler's waits for the slices need not drain the previous stores
@@ -1106,21 +1145,6 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             *reinterpret_cast<float2 *>(dst + 2) = make_float2(buf[u].z, buf[u].w);
         }
         lds_sync();
-        // S^T starts from the bias (an L2-resident table): its loads are issued
-        // before the next window's, so waiting for them leaves those in flight
-        f16v s[2];
-        if (active) {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    const float4 b4 = *reinterpret_cast<const float4 *>(cp + 32 * kt + 8 * a);
-                    s[kt][4 * a + 0] = b4.x;
-                    s[kt][4 * a + 1] = b4.y;
-                    s[kt][4 * a + 2] = b4.z;
-                    s[kt][4 * a + 3] = b4.w;
-                }
-        }
         const int wn = wi + wstep;
         load_window(wn, buf);  // in flight under this window's math
         const int wh = wi / g.nww;
@@ -1208,19 +1232,24 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             sum += __shfl_xor(sum, 32, 64);
             const float inv = 1.0f / sum;
 
-            // O^T = V^T P^T: lane r supplies V[key][d = r]
+            // O^T = V^T P^T: lane r supplies V[key][d = r]. Rows d >= HD of
+            // O^T are never stored, so lanes r >= HD may feed any value: they
+            // read column HD-1. A key tile's 16 values are read before its
+            // MFMAs, so the LDS latency is paid once per tile.
             f16v o;
 #pragma unroll
             for (int e = 0; e < 16; ++e) o[e] = 0.f;
-            const float *vcol = tile + 2 * W + hl * HD + r;
+            const float *vcol = tile + 2 * W + hl * HD + min(r, HD - 1);
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < 2; ++kt) {
+                float vv[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int key = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
-                    const float vv = (r < HD) ? vcol[key * RS] : 0.f;
-                    o = MFMA32(vv, s[kt][e], o);
-                }
+                for (int e = 0; e < 16; ++e)
+                    vv[e] = vcol[(32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3)) * RS];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o = MFMA32(vv[e], s[kt][e], o);
+            }
+            load_bias();  // the accumulators are free again: the next window's bias
             // into this wave's own q rows (no other wave reads them)
             float *orow = tile + qtok * RS + hl * HD;
 #pragma unroll
