@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int CR = HAS_RES ? (TR * 192 * 4 + 1023) / 1024 : 0;
     constexpr int NCR = HAS_RES ? (CR + NW - 1) / NW : 0;
     constexpr int RTILE = HAS_RES ? NCR * NW * 256 : 1;
-    constexpr int NSTORE = 4 * 3 * RB;         // buffer stores per lane per task
+    constexpr int NSTORE = (KS == 2 ? 2 : 4) * 3 * RB;  // buffer stores per lane per task
     static_assert(KPW % 4 == 0, "K must be a multiple of 4");
     (void)NT;
 
@@ -494,7 +494,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     __shared__ __attribute__((aligned(16))) float As1[ATILE];
     __shared__ __attribute__((aligned(16))) float Rs0[RTILE];
     __shared__ __attribute__((aligned(16))) float Rs1[RTILE];
-    __shared__ float ksum[KS == 2 ? 4 * RB * 3 * 4 * 64 : 1];
+    // K halves swap the accumulator registers the other half finishes:
+    // [sender half][column wave][rb][tile][register pair][lane]
+    __shared__ float ksum[KS == 2 ? 2 * 4 * RB * 3 * 2 * 64 : 1];
     __shared__ float rst0[4][TR][2];
     __shared__ float rst1[4][TR][2];
     __shared__ float prm[3][192];              // bias, LN weight, LN bias of the group's columns
@@ -515,6 +517,19 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(g.A, (size_t)g.M * g.lda * 4);
     const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
     const __amdgpu_buffer_rsrc_t ro_rs = buf_rsrc(g.out, (size_t)g.M * g.ldo * 4);
+    // The epilogue: with K split over two wave sets, each finishes half of the
+    // accumulator registers (rows 4q + R0 .. 4q + R0 + NR - 1 of a 16-row tile).
+    constexpr int NR = KS == 2 ? 2 : 4;
+    const int R0 = KS == 2 ? 2 * kq : 0;
+    // output byte offsets: a column part per tile (out of range past the
+    // group) plus a row part; their sum stays below 2^32, so an out-of-range
+    // part keeps the whole offset out of range
+    unsigned colo[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const int cl = 48 * cg + 16 * t + j;
+        colo[t] = cl < gw ? (unsigned)(gc0 + cl) * 4u : (unsigned)BUF_OOB;
+    }
     const __amdgpu_buffer_rsrc_t rr_rs = buf_rsrc(HAS_RES ? g.res : g.out,
                                                   HAS_RES ? (size_t)g.M * g.ldr * 4 : 0);
 
@@ -569,33 +584,34 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int rr = 0; rr < NR; ++rr) {
+                const int r = R0 + rr;
                 const int row = rb * 16 + 4 * q + r;
                 const int m = task * TR + row;
-                float mean = 0.f, rstd = 1.f;
+                const unsigned rowo = m < g.M ? (unsigned)m * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
+                float rstd = 1.f, mr = 0.f;
                 if (HAS_LN) {
                     const float a1 = (prst[0][row][0] + prst[1][row][0]) +
                                      (prst[2][row][0] + prst[3][row][0]);
                     const float a2 = (prst[0][row][1] + prst[1][row][1]) +
                                      (prst[2][row][1] + prst[3][row][1]);
-                    mean = a1 * invn;
+                    const float mean = a1 * invn;
                     float var = a2 * invn - mean * mean;
                     var = var > 0.f ? var : 0.f;
-                    rstd = 1.0f / sqrtf(var + 1e-5f);
+                    rstd = __builtin_amdgcn_rsqf(var + 1e-5f);
+                    mr = mean * rstd;
                 }
 #pragma unroll
                 for (int t = 0; t < 3; ++t) {
                     const int cl = 48 * cg + 16 * t + j;
-                    const bool cok = cl < gw;
                     float v = pacc[rb][t][r];
-                    if (HAS_LN) v = (v - mean) * rstd * prm[1][cl] + prm[2][cl];
+                    if (HAS_LN) v = fmaf(fmaf(v, rstd, -mr), prm[1][cl], prm[2][cl]);
                     if (EPI == EPI_GELU) v = gelu_erf(v);
                     if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
-                    if (HAS_RES) v += pres[row * g.ldr + (cok ? cl : 0)];
-                    // every wave issues the same stores (the second K half's go
-                    // out of range and are dropped): the counters stay countable
-                    buf_store1(ro_rs,
-                               (kq == 0 && m < g.M && cok) ? (m * g.ldo + gc0 + cl) * 4 : BUF_OOB, v);
+                    // columns past the group read inside the tile's allocation
+                    // and are dropped at the store
+                    if (HAS_RES) v += pres[row * g.ldr + cl];
+                    buf_store1(ro_rs, (int)(rowo + colo[t]), v);
                 }
             }
     };
@@ -651,26 +667,25 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         }
 
         if (KS == 2) {
-            // the second K half's partial sums meet the first's in LDS
-            if (kq == 1) {
+            // the two K halves' partial sums meet in LDS: each half sends the
+            // register pair the other half finishes and adds the pair it gets
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int t = 0; t < 3; ++t)
+                for (int t = 0; t < 3; ++t)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            ksum[(((cg * RB + rb) * 3 + t) * 4 + r) * 64 + lane] = acc[rb][t][r];
-            }
+                    for (int rr = 0; rr < 2; ++rr)
+                        ksum[((((kq * 4 + cg) * RB + rb) * 3 + t) * 2 + rr) * 64 + lane] =
+                            acc[rb][t][2 * (1 - kq) + rr];
             lds_sync();
-            if (kq == 0) {
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int t = 0; t < 3; ++t)
+                for (int t = 0; t < 3; ++t)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[rb][t][r] += ksum[(((cg * RB + rb) * 3 + t) * 4 + r) * 64 + lane];
-            }
+                    for (int rr = 0; rr < 2; ++rr)
+                        acc[rb][t][R0 + rr] +=
+                            ksum[(((((1 - kq) * 4 + cg) * RB + rb) * 3 + t) * 2 + rr) * 64 + lane];
         }
 
         // bias, and the row statistics when a LayerNorm follows (single-pass,
@@ -682,18 +697,19 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[rb][t][r] += bv;
+                for (int rr = 0; rr < NR; ++rr) acc[rb][t][R0 + rr] += bv;
         }
         if (HAS_LN) {
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
+                for (int rr = 0; rr < NR; ++rr) {
+                    const int r = R0 + rr;
                     const float s1 = row16_sum((acc[rb][0][r] + acc[rb][1][r]) + acc[rb][2][r]);
                     const float s2 = row16_sum(
                         (acc[rb][0][r] * acc[rb][0][r] + acc[rb][1][r] * acc[rb][1][r]) +
                         acc[rb][2][r] * acc[rb][2][r]);
-                    if (kq == 0 && j == 0) {
+                    if (j == 0) {
                         wrst[cg][rb * 16 + 4 * q + r][0] = s1;
                         wrst[cg][rb * 16 + 4 * q + r][1] = s2;
                     }
