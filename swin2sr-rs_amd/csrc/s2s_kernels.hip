@@ -1182,7 +1182,10 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 #pragma unroll
                 for (int j = 0; j < NS; ++j) qs += qop[j] * qop[j];
                 qs += __shfl_xor(qs, 32, 64);
-                const float qsc = ls / fmaxf(sqrtf(qs), 1e-12f);
+                // ls / max(|q|, 1e-12) = ls * rsq(max(|q|^2, 1e-24)), one
+                // hardware reciprocal square root (1 ulp) instead of the
+                // correctly rounded sqrt and division sequences
+                const float qsc = ls * __builtin_amdgcn_rsqf(fmaxf(qs, 1e-24f));
 #pragma unroll
                 for (int j = 0; j < NS; ++j) qop[j] *= qsc;
             }
@@ -1201,7 +1204,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 #pragma unroll
                 for (int j = 0; j < NS; ++j) ks += kop[kt][j] * kop[kt][j];
                 ks += __shfl_xor(ks, 32, 64);
-                const float ksc = 1.0f / fmaxf(sqrtf(ks), 1e-12f);
+                const float ksc = __builtin_amdgcn_rsqf(fmaxf(ks, 1e-24f));
 #pragma unroll
                 for (int j = 0; j < NS; ++j) kop[kt][j] *= ksc;
             }
@@ -1266,12 +1269,15 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                 for (int e = 0; e < 16; ++e) o = MFMA32(vv[e], s[kt][e], o);
             }
             load_bias();  // the accumulators are free again: the next window's bias
-            // into this wave's own q rows (no other wave reads them)
+            // into this wave's own q rows (the other head's waves read other
+            // columns of them), as float2s: register pairs (e, e+1) hold d, d+1
+            // with d even, and HD is even, so d < HD covers the pair
             float *orow = tile + qtok * RS + hl * HD;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
+            for (int e = 0; e < 16; e += 2) {
                 const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
-                if (d < HD) orow[d] = o[e] * inv;
+                if (d < HD)
+                    *reinterpret_cast<float2 *>(orow + d) = make_float2(o[e] * inv, o[e + 1] * inv);
             }
         }
         lds_sync();
