@@ -338,6 +338,50 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         return;
     }
 
+    if constexpr (EPI == EPI_SHUFFLE) {
+        // pixel_shuffle(2) store: n is the permuted output channel
+        // (2dy+dx)*feat + ch, m a pixel (y, x) of the H x W plane; the value
+        // lands at pixel (2y + dy, 2x + dx) of the 2H x 2W channel-last plane.
+        // Per column: the sub-pixel offset and channel; per row: the pixel
+        // (one division per row tile, the rest by carrying x past W).
+        int qoff[WTN], chn[WTN];
+        float bvs[WTN];
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = n0 + (wn * WTN + j) * 32 + lr;
+            const int q = n / g.feat;
+            chn[j] = n < g.N ? n - q * g.feat : -1;
+            qoff[j] = (q >> 1) * (2 * g.W) + (q & 1);
+            bvs[j] = (n < g.N && g.bias) ? g.bias[n] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+            const int mb = m0 + (wm * WTM + i) * 32 + 4 * lh;
+            const int yb = mb / g.W;
+            const int xb = mb - yb * g.W;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                int x = xb + off, y = yb;
+                while (x >= g.W) {
+                    x -= g.W;
+                    ++y;
+                }
+                if (mb + off >= g.M) continue;
+                const int pbase = (2 * y) * (2 * g.W) + 2 * x;
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) {
+                    if (chn[j] < 0) continue;
+                    const size_t o = (size_t)(pbase + qoff[j]) * g.feat + chn[j];
+                    float v = acc[i][j][r] + bvs[j];
+                    if (g.res) v += g.res[o];
+                    g.out[o] = v;
+                }
+            }
+        }
+        return;
+    }
+
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
         const int n = n0 + (wn * WTN + j) * 32 + lr;
@@ -353,18 +397,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                 if (EPI == EPI_GELU) v = gelu_erf(v);
                 if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
                 if (EPI == EPI_RES) v += g.res[(size_t)m * g.ldr + n];
-                if (EPI == EPI_SHUFFLE) {
-                    // n is the permuted output channel (2dy+dx)*feat + ch; m a
-                    // pixel of the H x W plane; the store lands in the 2H x 2W
-                    // channel-last plane (pixel_shuffle(2)).
-                    const int q = n / g.feat;
-                    const int ch = n - q * g.feat;
-                    const int y = m / g.W;
-                    const int x = m - y * g.W;
-                    const size_t op = (size_t)(2 * y + (q >> 1)) * (2 * g.W) + (2 * x + (q & 1));
-                    if (g.res) v += g.res[op * g.feat + ch];
-                    g.out[op * g.feat + ch] = v;
-                } else if (EPI == EPI_SHUFFLE_FINISH) {
+                if (EPI == EPI_SHUFFLE_FINISH) {
                     // n is torch's channel c*s^2 + dy*s + dx of the conv; the
                     // pixel_shuffle(s) output pixel (s*y+dy, s*x+dx), channel c,
                     // denormalised and cropped like the reference's finish
