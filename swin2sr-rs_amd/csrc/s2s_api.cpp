@@ -184,7 +184,19 @@ int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
     return 0;
 }
 
+// The kernels address a buffer with 32-bit byte offsets (raw buffer loads and
+// stores whose bounds check is the out-of-range mechanism), so no single
+// buffer may reach 2 GiB. A plane that would need one is refused like an
+// allocation failure: the message says "out of memory", which is what the
+// crate's tile-halving retry keys on (src/main.rs:655-662), and a smaller tile
+// then fits.
+static constexpr size_t kMaxBufferBytes = 0x7fffffffu;
+
 int s2s_ctx::alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what) {
+    if (floats > kMaxBufferBytes / sizeof(float))
+        return fail(std::string("hipMalloc(") + what + ", " + std::to_string(floats * sizeof(float)) +
+                    " bytes) refused: above the 2 GiB per-buffer limit of the kernels' 32-bit "
+                    "offsets (out of memory for one pass; tile the image)");
     float *p = nullptr;
     hipError_t e = hipMalloc(&p, std::max<size_t>(floats, 1) * sizeof(float));
     if (e != hipSuccess) {

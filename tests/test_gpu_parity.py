@@ -257,6 +257,24 @@ def test_forward_rejects_tiny_image(pkg):
         be.close()
 
 
+def test_forward_refuses_buffers_past_2gib(pkg):
+    """A plane whose head buffer would pass the kernels' 32-bit byte offsets
+    (1008^2 padded pixels x 16 x 64 channels x 4 B = 4.2 GB at x4) is refused
+    with an "out of memory" message - the condition the crate's tile-halving
+    retry keys on - and the context still runs a small image afterwards."""
+    M = pkg.model
+    arch = M.Arch(upsampler="pixelshuffle", scale=4, embed=24, heads=2, depths=[1])
+    be = pkg.abi.HipBackend(arch, M.make_weights(arch, seed=1))
+    try:
+        with pytest.raises(pkg.abi.S2SError, match="out of memory"):
+            be.forward(1000, 1000, np.zeros((3, 1000, 1000), np.float32))
+        x = M.adjust(arch, M.to_unit(M.input_sinusoids(16, 16, seed=2)))
+        y = be.forward(16, 16, x)
+        assert y.shape == (3, 64, 64) and np.isfinite(y).all()
+    finally:
+        be.close()
+
+
 def test_rstb_device(pkg, orc):
     """One RSTB (config 1's op sequence) on an explicit unpadded plane."""
     hip = pkg.hip
