@@ -1416,62 +1416,128 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x,
 // epilogue cpu::finish (src/cpu.rs:1925-1941): y/img_range + mean, cropped to
 // the unpadded output, written planar [3][oh][ow].
 //
-// HBM-bound (it reads the 64-channel plane of the last octave once): a
-// workgroup owns an 8 x 32 output tile, one pixel per thread, and stages the
-// 10 x 34 input halo through LDS 32 channels at a time (one 128-byte line per
-// pixel per chunk), so every input byte is fetched from HBM about once. The
-// weights, layout [tap][ci][3], are wave-uniform (scalar) loads.
-#define CL_TY 8
-#define CL_TX 32
-#define CL_CC 32
-__global__ __launch_bounds__(256) void k_conv_last_finish(const float *__restrict__ in,
-                                                          const float *__restrict__ wt,
-                                                          const float *__restrict__ bias,
-                                                          float *__restrict__ out, int H, int W,
-                                                          int feat, int oh, int ow,
-                                                          float inv_range, float m0, float m1,
-                                                          float m2) {
-    constexpr int TH = CL_TY + 2, TW = CL_TX + 2;
-    __shared__ float4 tile[TH * TW * (CL_CC / 4)];
+// It reads the 64-channel plane of the last octave once (HBM) and does 27 FMAs
+// per input value on the VALU (N = 3 would waste 13/16 of an MFMA tile). A
+// workgroup owns a 16 x 64 output tile: lane = column, wave w = rows 4w..4w+3,
+// 12 accumulators per lane. The 18 x 66 input halo moves through LDS 8
+// channels at a time, double-buffered: the next chunk's loads are in flight
+// while this one is multiplied. The chunk's weights (layout [tap][ci][3])
+// travel with it into LDS and are read as broadcast float4s, 12 at a time (one
+// tap, 4 channels), for the wave's 4 output rows.
+#define CL_ROWS 16
+#define CL_COLS 64
+#define CL_CC 8
+__global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__restrict__ in,
+                                                             const float *__restrict__ wt,
+                                                             const float *__restrict__ bias,
+                                                             float *__restrict__ out, int H, int W,
+                                                             int feat, int oh, int ow,
+                                                             float inv_range, float m0, float m1,
+                                                             float m2) {
+    constexpr int TH = CL_ROWS + 2, TW = CL_COLS + 2;
+    constexpr int Q = CL_CC / 4;                 // float4s per pixel per chunk
+    constexpr int NV = TH * TW * Q;
+    constexpr int NLD = (NV + 255) / 256;
+    constexpr int NW4 = 9 * CL_CC * 3 / 4;       // the chunk's weights, float4s
+    __shared__ float4 tile[2][NV];
+    __shared__ float4 wsh[2][NW4];
     const int tid = threadIdx.x;
-    const int tx = tid & (CL_TX - 1), ty = tid / CL_TX;
-    const int x0 = blockIdx.x * CL_TX, y0 = blockIdx.y * CL_TY;
-    const int x = x0 + tx, y = y0 + ty;
-    float a0 = bias[0], a1 = bias[1], a2 = bias[2];
-    for (int c0 = 0; c0 < feat; c0 += CL_CC) {
-        __syncthreads();
-        for (int i = tid; i < TH * TW * (CL_CC / 4); i += 256) {
-            const int q = i % (CL_CC / 4);
-            const int p = i / (CL_CC / 4);
-            const int sy = y0 - 1 + p / TW, sx = x0 - 1 + p % TW;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (sy >= 0 && sy < H && sx >= 0 && sx < W)
-                v = *reinterpret_cast<const float4 *>(in + ((size_t)sy * W + sx) * feat + c0 + 4 * q);
-            tile[i] = v;
-        }
-        __syncthreads();
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int x0 = blockIdx.x * CL_COLS, y0 = blockIdx.y * CL_ROWS;
+    const int nch = feat / CL_CC;
+    const __amdgpu_buffer_rsrc_t rin = buf_rsrc(in, (size_t)H * W * feat * 4);
+
+    // this thread's halo elements: (pixel p, float4 q) = divmod(tid + 256u, Q),
+    // out-of-plane taps (the zero padding) and elements past the halo read zero
+    int eoff[NLD];
 #pragma unroll
-        for (int tap = 0; tap < 9; ++tap) {
-            const float4 *src = &tile[((ty + tap / 3) * TW + tx + tap % 3) * (CL_CC / 4)];
-            const float *wk = wt + (tap * feat + c0) * 3;
-#pragma unroll
-            for (int q = 0; q < CL_CC / 4; ++q) {
-                const float4 v = src[q];
-                const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    a0 += wk[(4 * q + u) * 3 + 0] * vv[u];
-                    a1 += wk[(4 * q + u) * 3 + 1] * vv[u];
-                    a2 += wk[(4 * q + u) * 3 + 2] * vv[u];
-                }
-            }
-        }
+    for (int u = 0; u < NLD; ++u) {
+        const int i = tid + 256 * u;
+        const int p = i / Q, q = i - p * Q;
+        const int sy = y0 - 1 + p / TW, sx = x0 - 1 + p % TW;
+        const bool ok = i < NV && sy >= 0 && sy < H && sx >= 0 && sx < W;
+        eoff[u] = ok ? ((sy * W + sx) * feat + 4 * q) * 4 : BUF_OOB;
     }
-    if (x >= ow || y >= oh) return;
-    const size_t plane = (size_t)oh * ow, o = (size_t)y * ow + x;
-    out[o] = a0 * inv_range + m0;
-    out[plane + o] = a1 * inv_range + m1;
-    out[2 * plane + o] = a2 * inv_range + m2;
+    // the chunk's weights [tap][ci 0..7][3] as float4s: thread t < NW4 takes
+    // float4 t (tap t / 6, then 6 float4s of 8 channels x 3)
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wt, (size_t)9 * feat * 3 * 4);
+    const int wtap = tid / (NW4 / 9), wq = tid - wtap * (NW4 / 9);
+    float4 ld[NLD], lw;
+    auto load = [&](int c0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NLD; ++u)
+            ld[u] = buf_load4(rin, eoff[u] == BUF_OOB ? BUF_OOB : eoff[u] + c0 * 4);
+        lw = buf_load4(rw, tid < NW4 ? ((wtap * feat + c0) * 3 + 4 * wq) * 4 : BUF_OOB);
+    };
+    auto stash = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) {
+            const int i = tid + 256 * u;
+            if (NV % 256 == 0 || i < NV) tile[b][i] = ld[u];
+        }
+        if (tid < NW4) wsh[b][tid] = lw;
+    };
+
+    float acc[4][3];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        acc[rr][0] = bias[0];
+        acc[rr][1] = bias[1];
+        acc[rr][2] = bias[2];
+    }
+    load(0);
+    stash(0);
+    __syncthreads();
+    for (int k = 0; k < nch; ++k) {
+        const int c0 = k * CL_CC;
+        if (k + 1 < nch) load(c0 + CL_CC);
+        const float4 *t = tile[k & 1];
+        const float4 *ws = wsh[k & 1];
+        // one tap and 4 channels at a time: their 12 weights (three broadcast
+        // LDS reads) serve the wave's 4 output rows (the tap loop is kept
+        // rolled, so only one tap's operands are live)
+#pragma unroll 1
+        for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+                for (int qq = 0; qq < Q; ++qq) {
+                    const int dy = tap / 3, dx = tap - 3 * (tap / 3);
+                    float wk[12];
+#pragma unroll
+                    for (int f = 0; f < 3; ++f) {
+                        const float4 w4 = ws[tap * (NW4 / 9) + 3 * qq + f];
+                        wk[4 * f + 0] = w4.x;
+                        wk[4 * f + 1] = w4.y;
+                        wk[4 * f + 2] = w4.z;
+                        wk[4 * f + 3] = w4.w;
+                    }
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const float4 v = t[((4 * wave + rr + dy) * TW + lane + dx) * Q + qq];
+                        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            acc[rr][0] = fmaf(wk[3 * u + 0], vv[u], acc[rr][0]);
+                            acc[rr][1] = fmaf(wk[3 * u + 1], vv[u], acc[rr][1]);
+                            acc[rr][2] = fmaf(wk[3 * u + 2], vv[u], acc[rr][2]);
+                        }
+                    }
+                }
+        if (k + 1 < nch) stash((k + 1) & 1);
+        __syncthreads();
+    }
+    const int x = x0 + lane;
+    if (x >= ow) return;
+    const size_t plane = (size_t)oh * ow;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const int y = y0 + 4 * wave + rr;
+        if (y >= oh) break;
+        const size_t o = (size_t)y * ow + x;
+        out[o] = acc[rr][0] * inv_range + m0;
+        out[plane + o] = acc[rr][1] * inv_range + m1;
+        out[2 * plane + o] = acc[rr][2] * inv_range + m2;
+    }
 }
 
 // torch's bicubic resize, as the reference's cpu::bicubic_resize computes it
@@ -1899,7 +1965,9 @@ hipError_t launch_layernorm(const float *x, const float *w, const float *b, cons
     return hipGetLastError();
 }
 
-dim3 conv_last_grid(int oh, int ow) { return dim3((ow + CL_TX - 1) / CL_TX, (oh + CL_TY - 1) / CL_TY); }
+dim3 conv_last_grid(int oh, int ow) {
+    return dim3((ow + CL_COLS - 1) / CL_COLS, (oh + CL_ROWS - 1) / CL_ROWS);
+}
 
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
                                    float *out, int H, int W, int feat, int oh, int ow,
