@@ -6,6 +6,8 @@ Layout of this package:
   abi.py           ctypes binding of the ABI and the `Backend` mirror (HipBackend)
   model.py         architectures, synthetic checkpoints (crate tensor names) and inputs
   tiling.py        the crate's tile loop and memory policy over the Backend interface
+  formats.py       the crate's on-disk formats: converted-checkpoint safetensors with the
+                   __metadata__ validation, SW2F golden fixtures, PNG IO
 
 The directory name is not an identifier, so callers load it with
 `load_package()` from the repository root (see __graft_entry__.py).
@@ -13,4 +15,5 @@ The directory name is not an identifier, so callers load it with
 from . import model  # noqa: F401
 from . import hip  # noqa: F401
 from . import tiling  # noqa: F401
+from . import formats  # noqa: F401
 from .abi import HipBackend, S2SError, device_info, load_library  # noqa: F401
