@@ -1122,7 +1122,10 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     const int colq = (lseg * C + 2 * hg * HD + 4 * lc4) * 4;       // bytes in a qkv row
     float *const ldsq = tile + wave * RS + lseg * W + 4 * lc4;      // + 4u * RS
     const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qkv, (size_t)g.hp * g.wp * ld * 4);
-    auto load_window = [&](int wi, float4 (&buf)[16]) __attribute__((always_inline)) {
+    // (loads u0 .. u1-1 of a window: the 16 are issued in four parts spread
+    // over the math, so the texture address unit's queue never fills and
+    // stalls the instructions behind them)
+    auto load_window = [&](int wi, float4 (&buf)[16], int u0, int u1) __attribute__((always_inline)) {
         const int wv = wi < g.nw ? wi : 0;  // past the end: any in-range window
         const int wh = wv / g.nww;
         const int ww = wv - wh * g.nww;
@@ -1131,7 +1134,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
         int x1 = 8 * ww + 4 + wave + shift;
         if (x1 >= g.wp) x1 -= g.wp;
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = u0; u < u1; ++u) {
             int y = 8 * wh + (u >> 1) + shift;
             if (y >= g.hp) y -= g.hp;
             const int pix = y * g.wp + ((u & 1) ? x1 : x0);
@@ -1174,8 +1177,9 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     constexpr int NST = 4;              // output stores per thread
     int wi = xcd + 8 * ws;
     float4 buf[16];
-    load_window(wi, buf);
+    load_window(wi, buf, 0, 12);
     load_bias();
+    load_window(wi, buf, 12, 16);
     // as many dropped stores as a window's output has: the loop is then entered
     // with the same queue (loads, then stores) as it loops back with, and the
     // compiler's waits for the slices need not drain the previous stores
@@ -1195,10 +1199,12 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
         }
         lds_sync();
         const int wn = wi + wstep;
-        load_window(wn, buf);  // in flight under this window's math
+        load_window(wn, buf, 0, 4);  // the next window, in flight under this one's math
         const int wh = wi / g.nww;
         const int ww = wi - wh * g.nww;
 
+        float inv = 0.f;
+        f16v o;
         if (active) {
             // q operands (this lane's query, its half of d), normalised and scaled
             float qop[NS];
@@ -1246,7 +1252,9 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             for (int j = 0; j < NS; ++j)
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt) s[kt] = MFMA32(kop[kt][j], qop[j], s[kt]);
-
+        }
+        load_window(wn, buf, 4, 8);
+        if (active) {
             // bias, shift mask, softmax over the query's 64 keys (2 lanes). The
             // mask bands (win_band) are all 0 except in the last window row and
             // column of a shifted block, where a token's band is 1 or 2 by
@@ -1282,13 +1290,14 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                     sum += p;
                 }
             sum += __shfl_xor(sum, 32, 64);
-            const float inv = 1.0f / sum;
-
+            inv = 1.0f / sum;
+        }
+        load_window(wn, buf, 8, 12);
+        if (active) {
             // O^T = V^T P^T: lane r supplies V[key][d = r]. Rows d >= HD of
             // O^T are never stored, so lanes r >= HD may feed any value: they
             // read column HD-1. A key tile's 16 values are read before its
             // MFMAs, so the LDS latency is paid once per tile.
-            f16v o;
 #pragma unroll
             for (int e = 0; e < 16; ++e) o[e] = 0.f;
             const float *vcol = tile + 2 * W + hl * HD + min(r, HD - 1);
@@ -1301,7 +1310,10 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) o = MFMA32(vv[e], s[kt][e], o);
             }
-            load_bias();  // the accumulators are free again: the next window's bias
+        }
+        load_bias();  // the accumulators are free again: the next window's bias
+        load_window(wn, buf, 12, 16);
+        if (active) {
             // into this wave's own q rows (the other head's waves read other
             // columns of them), as float2s: register pairs (e, e+1) hold d, d+1
             // with d even, and HD is even, so d < HD covers the pair
