@@ -1086,6 +1086,13 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     constexpr int PER_TOK = 3 * V4MAX;  // float4s of one token's slices
     static_assert(PER_TOK <= 64 && V4MAX <= 16, "a token's slices fit one wave");
     __shared__ float tile[64 * RS];
+    // The softmax denominators come out of the AV product: lane r = HD supplies
+    // a column of ones (the first padding float of every tile row, never
+    // written by the copies), so row HD of O^T is sum_k P[k][q]. Needs a spare
+    // O^T row (HD < 32).
+    constexpr bool MSUM = HD < 32;
+    constexpr int SUM_E = 4 * (HD / 8) + (HD % 8) % 4;   // d = 8(e/4) + 4hh + e%4
+    constexpr int SUM_HH = (HD % 8) / 4;
 
     const int HG = (g.heads + 1) >> 1;
     const int xcd = blockIdx.x & 7;
@@ -1175,6 +1182,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     };
 
     constexpr int NST = 4;              // output stores per thread
+    if (MSUM && tid < 64) tile[tid * RS + 6 * HD] = 1.0f;
     int wi = xcd + 8 * ws;
     float4 buf[16];
     load_window(wi, buf, 0, 12);
@@ -1287,10 +1295,12 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                 for (int e = 0; e < 16; ++e) {
                     const float p = __expf(s[kt][e] - mx);
                     s[kt][e] = p;
-                    sum += p;
+                    if (!MSUM) sum += p;
                 }
-            sum += __shfl_xor(sum, 32, 64);
-            inv = 1.0f / sum;
+            if (!MSUM) {
+                sum += __shfl_xor(sum, 32, 64);
+                inv = 1.0f / sum;
+            }
         }
         load_window(wn, buf, 8, 12);
         if (active) {
@@ -1300,7 +1310,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             // MFMAs, so the LDS latency is paid once per tile.
 #pragma unroll
             for (int e = 0; e < 16; ++e) o[e] = 0.f;
-            const float *vcol = tile + 2 * W + hl * HD + min(r, HD - 1);
+            const float *vcol = (MSUM && r == HD) ? tile + 6 * HD : tile + 2 * W + hl * HD + min(r, HD - 1);
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
                 float vv[16];
@@ -1309,6 +1319,12 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                     vv[e] = vcol[(32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3)) * RS];
 #pragma unroll
                 for (int e = 0; e < 16; ++e) o = MFMA32(vv[e], s[kt][e], o);
+            }
+            if (MSUM) {
+                // row HD of O^T is the sum of the query's probabilities: lane
+                // half SUM_HH, register SUM_E
+                const float sum = __shfl(o[SUM_E], r + 32 * SUM_HH, 64);
+                inv = 1.0f / sum;
             }
         }
         load_bias();  // the accumulators are free again: the next window's bias
