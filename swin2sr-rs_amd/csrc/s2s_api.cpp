@@ -139,6 +139,13 @@ struct s2s_ctx {
     int upload(const std::vector<float> &host, float **dev);
     int alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what);
     int plan_body(int hp, int wp);
+    // qkv buffer floats: the plane layout, or the attention unit layout
+    size_t qkv_floats(int hp, int wp) const {
+        const size_t plane = (size_t)hp * wp * 3 * c;
+        return qkv_unit_layout(arch.heads, hd, c)
+                   ? std::max(plane, attn_unit_floats(hp, wp, arch.heads, hd))
+                   : plane;
+    }
     int plan_image(int h, int w);
     hipEvent_t event();
     int drain();
@@ -222,7 +229,7 @@ int s2s_ctx::plan_body(int hp, int wp) {
     const size_t P = (size_t)hp * wp;
     if (alloc(body_allocs, P * c, &cur, "cur") || alloc(body_allocs, P * c, &wk, "work") ||
         alloc(body_allocs, P * c, &tmp, "tmp") || alloc(body_allocs, P * c, &body, "body") ||
-        alloc(body_allocs, P * 3 * c, &qkv, "qkv") || alloc(body_allocs, P * c, &o, "attn") ||
+        alloc(body_allocs, qkv_floats(hp, wp), &qkv, "qkv") || alloc(body_allocs, P * c, &o, "attn") ||
         alloc(body_allocs, P * hidden, &hid, "mlp")) {
         free_list(body_allocs);
         return -1;
@@ -382,11 +389,20 @@ GemmArgs conv_gemm(const float *in, int H, int W, int cin, const float *wt, cons
 int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *x_in,
                        float *x_out) {
     const int P = hp * wp;
+    // qkv straight into the window attention's unit layout where its kernel
+    // takes the head shape, else the plane layout [P][3c]
+    const bool unit = qkv_unit_layout(arch.heads, hd, c);
     GemmArgs g = rows_gemm(x_in, c, b.wqkv, c, b.bqkv, qkv, 3 * c, P, 3 * c, c);
-    if (gemm("qkv", g, ALOAD_ROWS, EPI_STORE)) return -1;
+    g.H = hp;
+    g.W = wp;
+    g.shift = shift;
+    g.heads = arch.heads;
+    g.hd = hd;
+    if (gemm("qkv", g, ALOAD_ROWS, unit ? EPI_QKV_WIN : EPI_STORE)) return -1;
 
     AttnArgs a{};
     a.qkv = qkv;
+    a.unit = unit;
     a.cpbt = b.cpbt;
     a.logit_scale = b.ls;
     a.out = o;

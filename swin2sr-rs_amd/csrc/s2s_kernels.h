@@ -19,9 +19,28 @@ enum {
     EPI_LRELU = 5,   // out = leaky_relu(acc + bias, slope)
     EPI_SHUFFLE = 6,  // pixel_shuffle(2) store into a 2H x 2W channel-last plane (+ res
                       // in that layout when res is set)
-    EPI_SHUFFLE_FINISH = 7  // pixel_shuffle(scale) of a 3*scale^2-channel conv, denormalised
-                            // and cropped into the planar [3][oh][ow] output
+    EPI_SHUFFLE_FINISH = 7,  // pixel_shuffle(scale) of a 3*scale^2-channel conv, denormalised
+                             // and cropped into the planar [3][oh][ow] output
+    EPI_QKV_WIN = 8  // out = acc + bias, A rows read window by window in the shifted-window
+                     // order and stored in the attention unit layout (attn_unit_stride)
 };
+
+// The window-attention unit layout of qkv (written by the qkv GEMM under
+// EPI_QKV_WIN, read by the window attention): one unit per (window, head
+// pair) of the shifted plane, units in (window, pair) order, each 64 token
+// rows of attn_unit_stride(hd) floats - the pair's q columns (2*hd), then its
+// k and v columns, then 2 padding floats. Token t of window (wh, ww) is plane
+// pixel ((8wh + t/8 + shift) mod hp, (8ww + t%8 + shift) mod wp). A lone last
+// head (odd head count) leaves its pair's second-head columns unwritten.
+__host__ __device__ constexpr int attn_unit_stride(int hd) { return 6 * hd + 2; }
+inline size_t attn_unit_floats(int hp, int wp, int heads, int hd) {
+    return (size_t)(hp / 8) * (wp / 8) * ((heads + 1) / 2) * 64 * attn_unit_stride(hd);
+}
+// The window attention that reads the unit layout takes these head shapes.
+bool attn_unit_eligible(int heads, int hd, int c);
+// The forward writes qkv in the unit layout (one GEMM, then the unit
+// attention) for these shapes, in the plane layout [P][3c] otherwise.
+bool qkv_unit_layout(int heads, int hd, int c);
 
 struct GemmArgs {
     // A operand: ALOAD_ROWS -> A[m*lda + k]; ALOAD_IM2COL -> the 3x3 im2col
@@ -40,6 +59,9 @@ struct GemmArgs {
     const float *ln_w, *ln_b;
     float slope;
     int feat;  // EPI_SHUFFLE: output channels (N = 4*feat)
+    // EPI_QKV_WIN: the plane is H x W, the block's shift, heads of head_dim
+    // hd (N = 3 * heads * hd)
+    int shift, heads, hd;
     // EPI_SHUFFLE_FINISH: scale, output crop, img_range and the RGB mean
     int scale, oh, ow;
     float img_range, mean[3];
@@ -63,10 +85,13 @@ struct BsArgs {
     float slope;
     int M, N, K;
     int P, ngw;
+    // EPI_QKV_WIN: plane hp x wp (nww windows per row), shift, head shape
+    int hp, wp, nww, shift, heads, hd;
 };
 
 struct AttnArgs {
-    const float *qkv;          // [hp*wp][3c] plane order: q | k | v
+    const float *qkv;          // unit ? the unit layout : [hp*wp][3c] plane order q | k | v
+    int unit;                  // qkv is in the unit layout (needs attn_unit_eligible)
     const float *cpbt;         // [heads][64][64]
     const float *logit_scale;  // [heads]
     float *out;                // [hp*wp][c]

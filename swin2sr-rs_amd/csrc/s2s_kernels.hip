@@ -467,6 +467,13 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float *lds, int 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
                                              off, 0, 0, 0);
 }
+// ... with a wave-uniform part of the offset in the instruction's SGPR offset
+// (only for copies whose whole offset is in range: the range check sees the
+// per-lane part alone)
+__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, float *lds, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                             voff, soff, 0, 0);
+}
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
 // expcnt and lgkmcnt left at their maxima).
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
@@ -508,6 +515,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int KT = KPW * KS;
     constexpr bool HAS_RES = EPI == EPI_RES || EPI == EPI_LN_RES;
     constexpr bool HAS_LN = EPI == EPI_LN || EPI == EPI_LN_RES;
+    // EPI_QKV_WIN: task k is tokens TR*(k % TPW) .. of shifted window k / TPW
+    constexpr bool WIN = EPI == EPI_QKV_WIN;
+    constexpr int TPW = 64 / TR;
     // A tile: TR rows x KT floats, contiguous in HBM and in LDS; copied in
     // 1 KiB chunks, NCA per wave
     constexpr int CA = (TR * KT * 4 + 1023) / 1024;
@@ -549,7 +559,11 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 
     const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(g.A, (size_t)g.M * g.lda * 4);
     const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
-    const __amdgpu_buffer_rsrc_t ro_rs = buf_rsrc(g.out, (size_t)g.M * g.ldo * 4);
+    // EPI_QKV_WIN: a unit is 64 rows of RSU floats, HG units per window
+    const int RSU = WIN ? attn_unit_stride(g.hd) : 0;
+    const int HGU = WIN ? ((g.heads + 1) >> 1) * 64 * RSU : 0;
+    const __amdgpu_buffer_rsrc_t ro_rs =
+        buf_rsrc(g.out, WIN ? (size_t)(g.M / 64) * HGU * 4 : (size_t)g.M * g.ldo * 4);
     // The epilogue: with K split over two wave sets, each finishes half of the
     // accumulator registers (rows 4q + R0 .. 4q + R0 + NR - 1 of a 16-row tile).
     constexpr int NR = KS == 2 ? 2 : 4;
@@ -561,7 +575,19 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
         const int cl = 48 * cg + 16 * t + j;
-        colo[t] = cl < gw ? (unsigned)(gc0 + cl) * 4u : (unsigned)BUF_OOB;
+        if (WIN) {
+            // column seg*C + head*hd + d -> unit (head/2), segment seg, the
+            // head's half of it, d
+            const int c = gc0 + cl;
+            const int C = g.heads * g.hd;
+            const int seg = c / C;
+            const int head = (c - seg * C) / g.hd;
+            const int d = c - seg * C - head * g.hd;
+            colo[t] = cl < gw ? (unsigned)((head >> 1) * 64 * RSU + (2 * seg + (head & 1)) * g.hd + d) * 4u
+                              : (unsigned)BUF_OOB;
+        } else {
+            colo[t] = cl < gw ? (unsigned)(gc0 + cl) * 4u : (unsigned)BUF_OOB;
+        }
     }
     const __amdgpu_buffer_rsrc_t rr_rs = buf_rsrc(HAS_RES ? g.res : g.out,
                                                   HAS_RES ? (size_t)g.M * g.ldr * 4 : 0);
@@ -591,7 +617,49 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     }
 
     const int ntask = (g.M + TR - 1) / TR;
+    // EPI_QKV_WIN: float4 c*256 + 4*lane of the tile is column `col` of tile
+    // row `tr` (token tr of the task): its plane offset from the task's first
+    // pixel, when no token of the window wraps around the plane edge
+    int avo[WIN ? NCA : 1];
+    if (WIN) {
+#pragma unroll
+        for (int u = 0; u < NCA; ++u) {
+            const int f = min((wave + NW * u) * 256 + 4 * lane, TR * KT - 4);
+            const int tr = f / KT;
+            const int col = f - tr * KT;
+            avo[u] = (((tr >> 3) * g.wp + (tr & 7)) * g.lda + col) * 4;
+        }
+    }
     auto dma_a = [&](int task, float *dst) {
+        if (WIN) {
+            // the task's tokens, gathered from the plane (the shifted window's
+            // pixels); a window in the last row or column of a shifted plane
+            // wraps around its edges and takes the per-token path
+            const int wi = task / TPW;
+            const int tk0 = (task - wi * TPW) * TR;
+            const int wh = wi / g.nww;
+            const int ww = wi - wh * g.nww;
+            const bool wrap = g.shift && (8 * wh + 8 >= g.hp || 8 * ww + 8 >= g.wp);
+            if (!wrap) {
+                const int soff = ((8 * wh + (tk0 >> 3) + g.shift) * g.wp + 8 * ww + g.shift) * g.lda * 4;
+#pragma unroll
+                for (int u = 0; u < NCA; ++u) dma16s(ra_rs, dst + (wave + NW * u) * 256, avo[u], soff);
+            } else {
+#pragma unroll
+                for (int u = 0; u < NCA; ++u) {
+                    const int f = min((wave + NW * u) * 256 + 4 * lane, TR * KT - 4);
+                    const int tr = f / KT;
+                    const int col = f - tr * KT;
+                    const int tk = tk0 + tr;
+                    int y = 8 * wh + (tk >> 3) + g.shift;
+                    if (y >= g.hp) y -= g.hp;
+                    int x = 8 * ww + (tk & 7) + g.shift;
+                    if (x >= g.wp) x -= g.wp;
+                    dma16(ra_rs, dst + (wave + NW * u) * 256, ((y * g.wp + x) * g.lda + col) * 4);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < NCA; ++u) {
             const int c = wave + NW * u;
@@ -621,7 +689,12 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                 const int r = R0 + rr;
                 const int row = rb * 16 + 4 * q + r;
                 const int m = task * TR + row;
-                const unsigned rowo = m < g.M ? (unsigned)m * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
+                unsigned rowo = m < g.M ? (unsigned)m * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
+                if (WIN) {
+                    // token tk0 + row of window task / TPW (every task is whole)
+                    const int wi = task / TPW;
+                    rowo = (unsigned)(wi * HGU + ((task - wi * TPW) * TR + row) * RSU) * 4u;
+                }
                 float rstd = 1.f, mr = 0.f;
                 if (HAS_LN) {
                     const float a1 = (prst[0][row][0] + prst[1][row][0]) +
@@ -1038,40 +1111,38 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 
 // ---------------------------------------------------------------------------
 // k_wattn: the same window attention, persistent workgroups that each own one
-// head pair and walk a list of windows.
+// head pair and walk a list of windows, reading qkv in the unit layout.
 //
-// A unit of work is (window, head pair). The window's q, k and v slices of its
-// two heads (64 tokens x 3 x 2*hd floats) are loaded with coalesced float4
-// loads - each token's slice is a contiguous 8*hd-byte run of its qkv row -
-// into LDS, [token][q | k | v] rows of 6*hd + 2 floats (an odd number of
-// float2s, so 16 consecutive rows read by a ds_read_b64 land in distinct bank
-// pairs). The loads of the NEXT window are issued into registers before the
-// current window is computed, so they are in flight under its MFMAs and
-// softmax (a non-persistent workgroup would load, then compute, then store,
-// and the workgroups of a CU fall into step with each other). Wave w handles
-// head 2*hg + w/2 and query tile w%2 (32 queries):
+// A unit of work is (window, head pair), and its q, k and v slices (64 tokens
+// x 3 x 2*hd floats) are one contiguous unit written by the qkv GEMM: rows of
+// 6*hd + 2 floats, [q | k | v | 2 padding], an odd number of float2s, so 16
+// consecutive rows read by a ds_read_b64 land in distinct bank pairs. The
+// unit is copied straight into LDS (buffer_load ... lds, 1 KiB per wave
+// instruction, no VGPR staging). Wave w handles head 2*hg + w/2 and query
+// tile w%2 (32 queries):
 //   - its q row and the 64 k rows come out of LDS as MFMA operands (step j of
 //     lane half hh covers d = 4(j/2) + 2hh + j%2, then d = hd-2+hh for the odd
 //     tail pair), scaled in registers by exp(min(ls, ln 100))/|q| and 1/|k|;
 //   - S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x2f32 with the softmax in
-//     registers between them, as in k_attention; the bias table values a lane
-//     needs (32 floats) depend on the head only, so they are loaded once;
+//     registers between them, as in k_attention; S^T starts from the bias (an
+//     L2-resident table, the same for every window), loaded as soon as AV has
+//     consumed the accumulators;
 //   - O^T goes back into the wave's own q rows of the LDS tile (no other wave
-//     reads them), and after a barrier the workgroup writes the window's output
-//     slices with coalesced float4 stores.
-// Two workgroups share a CU at hd = 30 (46.6 KB of LDS each). Barriers are
-// LDS-only (lds_sync): the output stores and the next window's loads stay in
-// flight across them.
+//     reads them); after a barrier every thread reads its share of the
+//     window's output slices, after another the next window's unit is copied
+//     in, and the output goes out with coalesced float4 stores behind it.
+// Three workgroups share a CU at hd = 30 (46 KB of LDS each), so one
+// workgroup's copy overlaps the others' math. Barriers are LDS-only
+// (lds_sync): the output stores stay in flight across them.
 //
 // Work assignment: workgroup b runs on XCD b % 8 (round-robin dispatch); its
 // slot s = b / 8 on that XCD fixes the head pair hg = s % HG and a window lane
 // ws = s / HG, and it takes windows xcd + 8 * (ws + nws * k), k = 0, 1, ...
 // where nws is the number of window lanes per XCD. All head pairs of a window
-// then run at the same time on the same XCD and share the 128-byte lines their
-// slices straddle in that XCD's L2.
+// then run at the same time on the same XCD.
 // ---------------------------------------------------------------------------
-// Resident workgroups per CU: 3 by LDS (46.6 KB each at hd = 30) and by
-// registers; at hd = 32 the registers leave room for 2 without spilling.
+// Resident workgroups per CU: 3 by LDS (46 KB each at hd = 30) and by
+// registers; at hd = 32 the tile leaves room for 3 but the registers for 2.
 __host__ __device__ constexpr int wattn_per_cu(int hd) { return hd > 30 ? 2 : 3; }
 
 template <int HD>
@@ -1081,14 +1152,14 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     constexpr int G4 = HD / 4;          // float2 pairs of steps
     constexpr bool TAIL = (HD % 4) != 0;
     constexpr int W = 2 * HD;           // floats per segment (two heads)
-    constexpr int RS = 6 * HD + 2;      // LDS row stride
-    constexpr int V4MAX = W / 4;        // float4s per segment
-    constexpr int PER_TOK = 3 * V4MAX;  // float4s of one token's slices
-    static_assert(PER_TOK <= 64 && V4MAX <= 16, "a token's slices fit one wave");
-    __shared__ float tile[64 * RS];
+    constexpr int RS = attn_unit_stride(HD);  // LDS row stride = unit row
+    constexpr int UF = 64 * RS;         // floats per unit
+    constexpr int NCH = (UF + 255) / 256;   // 1 KiB copies per unit
+    constexpr int NCW = (NCH + 3) / 4;      // ... per wave (at most)
+    __shared__ __attribute__((aligned(16))) float tile[NCH * 256];
     // The softmax denominators come out of the AV product: lane r = HD supplies
-    // a column of ones (the first padding float of every tile row, never
-    // written by the copies), so row HD of O^T is sum_k P[k][q]. Needs a spare
+    // a column of ones (the first padding float of every tile row, set after
+    // each copy has landed), so row HD of O^T is sum_k P[k][q]. Needs a spare
     // O^T row (HD < 32).
     constexpr bool MSUM = HD < 32;
     constexpr int SUM_E = 4 * (HD / 8) + (HD % 8) % 4;   // d = 8(e/4) + 4hh + e%4
@@ -1113,39 +1184,18 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     const int head = 2 * hg + hl;
     const bool active = hl < nh;
     const int C = g.c;
-    const int ld = 3 * C;
     const int qtok = 32 * qt + r;
 
-    // Copy-in: wave w moves tokens 4u + w (u = 0..15), one token per
-    // instruction, lane l taking float4 l of the token's q | k | v slices.
-    // Token (row u/2, column 4(u%2) + w of the window) is the same for the
-    // whole wave, so its pixel offset is scalar work and goes in the
-    // instruction's SGPR offset; the lane's column offset is fixed. Lanes past
-    // the slices (and float4s past a one-head group's) repeat an earlier
-    // float4: same address, same value, no branch.
-    const int li = lane % PER_TOK;
-    const int lseg = li / V4MAX;
-    const int lc4 = min(li - lseg * V4MAX, v4 - 1);
-    const int colq = (lseg * C + 2 * hg * HD + 4 * lc4) * 4;       // bytes in a qkv row
-    float *const ldsq = tile + wave * RS + lseg * W + 4 * lc4;      // + 4u * RS
-    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qkv, (size_t)g.hp * g.wp * ld * 4);
-    // (loads u0 .. u1-1 of a window: the 16 are issued in four parts spread
-    // over the math, so the texture address unit's queue never fills and
-    // stalls the instructions behind them)
-    auto load_window = [&](int wi, float4 (&buf)[16], int u0, int u1) __attribute__((always_inline)) {
-        const int wv = wi < g.nw ? wi : 0;  // past the end: any in-range window
-        const int wh = wv / g.nww;
-        const int ww = wv - wh * g.nww;
-        int x0 = 8 * ww + wave + shift;
-        if (x0 >= g.wp) x0 -= g.wp;
-        int x1 = 8 * ww + 4 + wave + shift;
-        if (x1 >= g.wp) x1 -= g.wp;
+    // Copy-in: chunk c = wave + 4u of the unit (floats 256c .. 256c + 255),
+    // lane l moving float4 l of it; the unit's last chunk runs past it into
+    // the next unit (or out of range: zeros) and lands in the tile's slack.
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qkv, (size_t)g.nw * HG * UF * 4);
+    auto copy_unit = [&](int wi) __attribute__((always_inline)) {
+        const int base = (wi * HG + hg) * UF * 4;
 #pragma unroll
-        for (int u = u0; u < u1; ++u) {
-            int y = 8 * wh + (u >> 1) + shift;
-            if (y >= g.hp) y -= g.hp;
-            const int pix = y * g.wp + ((u & 1) ? x1 : x0);
-            buf[u] = buf_load4s(rq, colq, pix * ld * 4);
+        for (int u = 0; u < NCW; ++u) {
+            const int c = wave + 4 * u;
+            if (u < NCW - 1 || c < NCH) dma16(rq, tile + c * 256, base + c * 1024 + 16 * lane);
         }
     };
 
@@ -1163,10 +1213,6 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     const float ls = active ? __expf(fminf(g.logit_scale[head], 4.605170185988092f)) : 0.f;
     const float *cp = g.cpbt + ((size_t)(active ? head : 0) * 64 + qtok) * 64 + 4 * hh;
 
-    // S^T starts from the bias (an L2-resident table, the same for every
-    // window): the values for the next window are loaded as soon as AV has
-    // consumed the accumulators, so they are in flight across the output
-    // stores and the copy-in, and they are older than the next prefetch.
     f16v s[2];
     auto load_bias = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -1181,33 +1227,30 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             }
     };
 
+    // The ones column: a wave sets the padding floats that lie in chunks it
+    // copied itself, after its own wait for them (another wave's copy may
+    // still land up to the barrier and would overwrite an earlier write).
+    const bool own_one = MSUM && ((lane * RS + 6 * HD) >> 8) % 4 == wave;
+
     constexpr int NST = 4;              // output stores per thread
-    if (MSUM && tid < 64) tile[tid * RS + 6 * HD] = 1.0f;
     int wi = xcd + 8 * ws;
-    float4 buf[16];
-    load_window(wi, buf, 0, 12);
+    if (wi < g.nw) copy_unit(wi);
     load_bias();
-    load_window(wi, buf, 12, 16);
     // as many dropped stores as a window's output has: the loop is then entered
-    // with the same queue (loads, then stores) as it loops back with, and the
-    // compiler's waits for the slices need not drain the previous stores
+    // with the same queue (copies and bias loads, then stores) as it loops back
+    // with, and the wait for the copies need not drain the previous stores
     {
         const __amdgpu_buffer_rsrc_t rnull = buf_rsrc(g.out, 0);  // every offset out of range
 #pragma unroll
         for (int u = 0; u < NST; ++u) buf_store4(rnull, 16 * u, make_float4(0.f, 0.f, 0.f, 0.f));
     }
     while (wi < g.nw) {
-        // ---- this window's slices -> LDS (the previous window's output
-        // stores have read the tile: barrier at the end of the loop) ----
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            float *dst = ldsq + 4 * u * RS;
-            *reinterpret_cast<float2 *>(dst) = make_float2(buf[u].x, buf[u].y);
-            *reinterpret_cast<float2 *>(dst + 2) = make_float2(buf[u].z, buf[u].w);
-        }
+        // ---- this window's unit has landed (outstanding: at most the
+        // previous window's stores) ----
+        WAIT_VMCNT(NST);
+        if (own_one) tile[lane * RS + 6 * HD] = 1.0f;
         lds_sync();
         const int wn = wi + wstep;
-        load_window(wn, buf, 0, 4);  // the next window, in flight under this one's math
         const int wh = wi / g.nww;
         const int ww = wi - wh * g.nww;
 
@@ -1260,9 +1303,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             for (int j = 0; j < NS; ++j)
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt) s[kt] = MFMA32(kop[kt][j], qop[j], s[kt]);
-        }
-        load_window(wn, buf, 4, 8);
-        if (active) {
+
             // bias, shift mask, softmax over the query's 64 keys (2 lanes). The
             // mask bands (win_band) are all 0 except in the last window row and
             // column of a shifted block, where a token's band is 1 or 2 by
@@ -1271,22 +1312,23 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             const bool ex = shift && (ww * 8 + 8 >= g.wp);
             const bool qy = (qtok >> 3) < 8 - shift;
             const bool qx = (qtok & 7) < 8 - shift;
-            float mx = -INFINITY;
+            if (ey || ex) {  // the same for the whole workgroup: one branch
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+                for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    float v = s[kt][e];
-                    if (ey || ex) {
+                    for (int e = 0; e < 16; ++e) {
                         const int krow = 4 * kt + (e >> 2);        // key >> 3
                         const int kcol = 4 * hh + (e & 3);         // key & 7
                         const bool dy = ey && ((krow < 8 - shift) != qy);
                         const bool dx = ex && ((kcol < 8 - shift) != qx);
-                        if (dy || dx) v -= 100.f;
+                        if (dy || dx) s[kt][e] -= 100.f;
                     }
-                    s[kt][e] = v;
-                    mx = fmaxf(mx, v);
-                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             float sum = 0.f;
 #pragma unroll
@@ -1301,9 +1343,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                 sum += __shfl_xor(sum, 32, 64);
                 inv = 1.0f / sum;
             }
-        }
-        load_window(wn, buf, 8, 12);
-        if (active) {
+
             // O^T = V^T P^T: lane r supplies V[key][d = r]. Rows d >= HD of
             // O^T are never stored, so lanes r >= HD may feed any value: they
             // read column HD-1. A key tile's 16 values are read before its
@@ -1328,7 +1368,6 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             }
         }
         load_bias();  // the accumulators are free again: the next window's bias
-        load_window(wn, buf, 12, 16);
         if (active) {
             // into this wave's own q rows (the other head's waves read other
             // columns of them), as float2s: register pairs (e, e+1) hold d, d+1
@@ -1342,6 +1381,16 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             }
         }
         lds_sync();
+        float4 ov[NST];
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const float *src = ldso + 16 * u * RS;
+            const float2 a = *reinterpret_cast<const float2 *>(src);
+            const float2 b = *reinterpret_cast<const float2 *>(src + 2);
+            ov[u] = make_float4(a.x, a.y, b.x, b.y);
+        }
+        lds_sync();  // every wave has read the tile: the next unit may land
+        if (wn < g.nw) copy_unit(wn);
 
         // ---- the window's output slices, coalesced ----
         {
@@ -1350,15 +1399,11 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             const int xo = x * C * 4 + colo;
 #pragma unroll
             for (int u = 0; u < NST; ++u) {
-                const float *src = ldso + 16 * u * RS;
-                const float2 a = *reinterpret_cast<const float2 *>(src);
-                const float2 b = *reinterpret_cast<const float2 *>(src + 2);
                 int y = 8 * wh + 2 * u + (wave >> 1) + shift;
                 if (y >= g.hp) y -= g.hp;
-                buf_store4s(ro, xo, y * g.wp * C * 4, make_float4(a.x, a.y, b.x, b.y));
+                buf_store4s(ro, xo, y * g.wp * C * 4, ov[u]);
             }
         }
-        lds_sync();
         wi = wn;
     }
 }
@@ -1738,14 +1783,15 @@ static hipError_t run_gemm_v(const GemmArgs &g, int aload, int epi, hipStream_t 
 
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
     (void)g;
-    static const char *names[3][8] = {
+    static const char *names[3][9] = {
         {"gemm_rows_store", "gemm_rows_gelu", "gemm_rows_res", "gemm_rows_ln", "gemm_rows_ln_res",
-         "gemm_rows_lrelu", "gemm_rows_shuffle", "gemm_rows_shuffle_finish"},
+         "gemm_rows_lrelu", "gemm_rows_shuffle", "gemm_rows_shuffle_finish", "gemm_rows_qkv_win"},
         {"conv3x3_store", "conv3x3_gelu", "conv3x3_res", "conv3x3_ln", "conv3x3_ln_res",
-         "conv3x3_lrelu", "conv3x3_shuffle", "conv3x3_shuffle_finish"},
+         "conv3x3_lrelu", "conv3x3_shuffle", "conv3x3_shuffle_finish", "conv3x3_qkv_win"},
         {"conv3x3_up2_store", "conv3x3_up2_gelu", "conv3x3_up2_res", "conv3x3_up2_ln",
          "conv3x3_up2_ln_res", "conv3x3_up2_lrelu", "conv3x3_up2_shuffle",
-         "conv3x3_up2_shuffle_finish"}};
+         "conv3x3_up2_shuffle_finish", "conv3x3_up2_qkv_win"}};
+    if (aload < 0 || aload > 2 || epi < 0 || epi > 8) return "gemm_unknown";
     return names[aload][epi];
 }
 
@@ -1821,6 +1867,12 @@ static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks
         return false;
     }
     if ((epi == EPI_LN || epi == EPI_LN_RES) && g.N > 192) return false;
+    if (epi == EPI_QKV_WIN) {
+        // whole windows of the plane, three head-major column blocks
+        if (g.H <= 0 || g.W <= 0 || g.H % 8 || g.W % 8 || g.M != g.H * g.W) return false;
+        if (g.heads <= 0 || g.hd <= 0 || g.N != 3 * g.heads * g.hd) return false;
+        if (g.shift < 0 || g.shift >= 8) return false;
+    }
     return true;
 }
 
@@ -1864,6 +1916,12 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     a.K = g.K;
     a.P = P;
     a.ngw = ngw;
+    a.hp = g.H;
+    a.wp = g.W;
+    a.nww = g.W / 8;
+    a.shift = g.shift;
+    a.heads = g.heads;
+    a.hd = g.hd;
     hipLaunchKernelGGL((k_bsgemm<KPW, KS, RB, EPI>), grid, dim3(256 * KS), 0, st, a);
     return hipGetLastError();
 }
@@ -1874,6 +1932,7 @@ static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool laun
     case EPI_STORE: return run_bs<KPW, KS, RB, EPI_STORE>(g, st, launch, grid);
     case EPI_GELU: return run_bs<KPW, KS, RB, EPI_GELU>(g, st, launch, grid);
     case EPI_LRELU: return run_bs<KPW, KS, RB, EPI_LRELU>(g, st, launch, grid);
+    case EPI_QKV_WIN: return run_bs<KPW, KS, RB, EPI_QKV_WIN>(g, st, launch, grid);
     default: break;
     }
     // residual and LayerNorm epilogues run with 16-row tasks only (bs_rb)
@@ -1894,7 +1953,7 @@ static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool laun
 // 16 otherwise.
 static int bs_rb(const GemmArgs &g, int ks, int epi) {
     const int ng = (g.N + 191) / 192;
-    const bool simple = epi == EPI_STORE || epi == EPI_GELU || epi == EPI_LRELU;
+    const bool simple = epi == EPI_STORE || epi == EPI_GELU || epi == EPI_LRELU || epi == EPI_QKV_WIN;
     (void)ks;
     return (ng >= 2 && simple) ? 2 : 1;
 }
@@ -1933,14 +1992,23 @@ hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
     return launch_gemm_variant(g, aload, epi, gemm_pick(g, aload, epi), st);
 }
 
-// k_wattn takes every even head_dim it is built for whose head-pair slices are
-// float4-aligned (all released checkpoints: 30 and 10); k_attention the rest.
-static bool wattn_eligible(const AttnArgs &g) {
-    const int hd = g.head_dim;
+// k_wattn takes every even head_dim it is built for whose head-pair output
+// slices are float4-aligned (all released checkpoints: 30 and 10) from the
+// unit layout; k_attention the rest, from the plane layout.
+bool attn_unit_eligible(int heads, int hd, int c) {
     if (hd != 2 && hd != 10 && hd != 30 && hd != 32) return false;
-    if ((2 * hd) % 4 || g.c % 4) return false;
-    if ((g.heads & 1) && hd % 4) return false;  // a lone last head's slice must be float4s
+    if (heads <= 0 || c != heads * hd || c % 4) return false;
+    if ((heads & 1) && hd % 4) return false;  // a lone last head's slice must be float4s
     return true;
+}
+
+bool qkv_unit_layout(int heads, int hd, int c) {
+    // the qkv GEMM (K = c) must run on k_bsgemm, which writes the layout
+    return attn_unit_eligible(heads, hd, c) && (c == 180 || c == 60 || c == 360 || c == 120);
+}
+
+static bool wattn_eligible(const AttnArgs &g) {
+    return g.unit && attn_unit_eligible(g.heads, g.head_dim, g.c);
 }
 
 // k_wattn's persistent grid: 8 XCDs x HG head pairs x nws window lanes, about
@@ -1966,6 +2034,7 @@ hipError_t launch_attention(const AttnArgs &g0, hipStream_t st, unsigned *grid_o
         }
         return hipGetLastError();
     }
+    if (g0.unit) return hipErrorInvalidValue;  // no unit-layout kernel for this head shape
     const AttnArgs &g = g0;
     const unsigned grid = (unsigned)((g.nw * g.heads + 3) / 4);
     if (grid_out) *grid_out = grid;

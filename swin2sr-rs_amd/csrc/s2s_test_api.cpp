@@ -105,9 +105,31 @@ int s2s_test_attention(int hp, int wp, int win, int heads, int head_dim, int shi
         for (int k = 0; k < n; ++k)
             for (int h = 0; h < heads; ++h)
                 cpbt[((size_t)h * n + q) * n + k] = cpb[((size_t)q * n + k) * heads + h];
+    // the shapes the unit-layout kernel takes get their qkv in that layout
+    // (the qkv GEMM writes it in the forward; here the host lays it out)
+    const bool unit = attn_unit_eligible(heads, head_dim, c);
+    std::vector<float> ql;
+    if (unit) {
+        const int RS = attn_unit_stride(head_dim), HG = (heads + 1) / 2;
+        const int nww = wp / 8, nw = (hp / 8) * nww;
+        ql.assign(attn_unit_floats(hp, wp, heads, head_dim), 0.f);
+        for (int wi = 0; wi < nw; ++wi)
+            for (int t = 0; t < 64; ++t) {
+                const int y = (8 * (wi / nww) + t / 8 + shift) % hp;
+                const int x = (8 * (wi % nww) + t % 8 + shift) % wp;
+                const float *src = qkv + ((size_t)y * wp + x) * 3 * c;
+                for (int h = 0; h < heads; ++h)
+                    for (int seg = 0; seg < 3; ++seg)
+                        for (int dd = 0; dd < head_dim; ++dd)
+                            ql[(((size_t)wi * HG + h / 2) * 64 + t) * RS +
+                               (2 * seg + (h & 1)) * head_dim + dd] =
+                                src[seg * c + h * head_dim + dd];
+            }
+    }
     Dev d;
     AttnArgs a{};
-    a.qkv = d.up(qkv, P * 3 * c);
+    a.unit = unit;
+    a.qkv = unit ? d.up(ql.data(), ql.size()) : d.up(qkv, P * 3 * c);
     a.cpbt = d.up(cpbt.data(), cpbt.size());
     a.logit_scale = d.up(logit_scale, heads);
     a.out = d.alloc<float>(P * c);

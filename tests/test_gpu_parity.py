@@ -40,7 +40,7 @@ def test_window_map_bit_exact(pkg, orc, hp, wp, shift):
     assert np.array_equal(reg, want_reg)
 
 
-@pytest.mark.parametrize("heads,hd", [(2, 2), (6, 30), (6, 10), (3, 32)])
+@pytest.mark.parametrize("heads,hd", [(2, 2), (6, 30), (6, 10), (3, 32), (2, 12), (3, 4)])
 @pytest.mark.parametrize("shift", [0, 4])
 @pytest.mark.parametrize("hp,wp", [(16, 16), (40, 72)])
 def test_attention(pkg, orc, heads, hd, shift, hp, wp):
