@@ -495,9 +495,9 @@ int s2s_ctx::head(int h, int w, float *d_out) {
     const int P = hp * wp;
     const int oh = h * s, ow = w * s;
     GemmArgs g{};
-    auto last = [&](const float *f, int H, int W) {
+    auto last = [&](const float *f, int H, int W, int chunk8) {
         return run("conv_last_finish", conv_last_grid(oh, ow), dim3(256), [&] {
-            return launch_conv_last_finish(f, last_w, last_b, d_out, H, W, feat, oh, ow,
+            return launch_conv_last_finish(f, last_w, last_b, d_out, H, W, feat, chunk8, oh, ow,
                                            arch.img_range, arch.mean, stream);
         });
     };
@@ -528,16 +528,21 @@ int s2s_ctx::head(int h, int w, float *d_out) {
                 return -1;
         }
         int H = hp, W = wp;
+        const bool slabs = feat % 8 == 0 && !aux;
         for (int oc = 0; oc < octaves; ++oc) {
             g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
             g.feat = feat;
             if (aux && oc == octaves - 1) g.res = bicf;  // + the bicubic branch
+            // the last octave's plane goes to conv_last in 8-channel slabs
+            // (not with the bicubic branch: that residual is the same buffer,
+            // updated in place, so each value must land where it was read)
+            g.chunk8 = oc == octaves - 1 && slabs;
             const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
             if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
             H *= 2;
             W *= 2;
         }
-        return last(fplanes[octaves], H, W);
+        return last(fplanes[octaves], H, W, slabs);
     }
     case S2S_PIXELSHUFFLE_DIRECT: {
         // one conv to 3*s^2 channels, stored through pixel_shuffle(s) straight
@@ -564,7 +569,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
         g = conv_gemm(fplanes[2], 4 * hp, 4 * wp, feat, hr_w, hr_b, fplanes[3], feat, feat);
         g.slope = 0.2f;
         if (gemm("conv_hr", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
-        return last(fplanes[3], 4 * hp, 4 * wp);
+        return last(fplanes[3], 4 * hp, 4 * wp, 0);
     }
     default:
         return fail("unknown upsampler " + std::to_string(arch.upsampler));

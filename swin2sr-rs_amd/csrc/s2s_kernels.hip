@@ -79,13 +79,15 @@ __device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, 
 // The coefficients (halved, so the sum is erfc(t)/2 directly) are a
 // relative-error fit of erfcx(t)/u on t in [0, 8]
 // (iteratively reweighted least squares against scipy.special.erfcx; maximum
-// relative error 3.8e-8 in exact arithmetic). Phi(v) is 1 - erfc(t)/2 for
-// v > 0 and erfc(t)/2 otherwise, so the negative side keeps its relative
-// accuracy instead of cancelling in 1 + erf. Absolute error against the exact
-// GELU is below 4e-7 on [-12, 12], the same as the erff form's rounding. One
-// reciprocal, one exp2 and 12 other VALU operations, with no divergent branch
-// (a library erff evaluates two polynomial branches when a wavefront holds
-// both small and large arguments).
+// relative error 3.8e-8 in exact arithmetic). With q = erfc(t)/2, Phi(v) is
+// 1 - q for v > 0 and q otherwise, so v Phi(v) = max(v, 0) - |v| q: one max
+// and one fused multiply-add instead of a compare, a select, a subtraction
+// and a multiply, and the negative side keeps its relative accuracy instead
+// of cancelling in 1 + erf. Absolute error against the exact GELU is below
+// 2.5e-7 on [-12, 12], within the erff form's rounding. One reciprocal, one
+// exp2 and 14 other VALU operations, with no divergent branch (a library erff
+// evaluates two polynomial branches when a wavefront holds both small and
+// large arguments).
 __device__ __forceinline__ float gelu_erf(float v) {
     const float t = fabsf(v) * 0.70710678118654752440f;
     const float u = __builtin_amdgcn_rcpf(fmaf(0.5f, t, 1.0f));
@@ -100,7 +102,7 @@ __device__ __forceinline__ float gelu_erf(float v) {
     p = fmaf(p, u, 0.14104808866977692f);
     // exp(-t^2) = 2^(v^2 * (-log2(e) / 2)); q = erfc(t) / 2
     const float q = u * p * __builtin_amdgcn_exp2f(v * v * -0.72134752044448170368f);
-    return v * (v > 0.0f ? 1.0f - q : q);
+    return fmaf(-fabsf(v), q, fmaxf(v, 0.0f));
 }
 
 // ---------------------------------------------------------------------------
@@ -343,9 +345,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         // (2dy+dx)*feat + ch, m a pixel (y, x) of the H x W plane; the value
         // lands at pixel (2y + dy, 2x + dx) of the 2H x 2W channel-last plane.
         // Per column: the sub-pixel offset and channel; per row: the pixel
-        // (one division per row tile, the rest by carrying x past W).
-        int qoff[WTN], chn[WTN];
+        // (one division per row tile, the rest by carrying x past W). The
+        // stored offset is pixel * pstride + cterm: channel-last (pstride =
+        // feat, cterm = channel) or in 8-channel slabs (pstride = 8, cterm =
+        // slab * plane * 8 + channel % 8).
+        int qoff[WTN], chn[WTN], cterm[WTN];
         float bvs[WTN];
+        const size_t plane2 = (size_t)4 * g.H * g.W;
+        const int pstride = g.chunk8 ? 8 : g.feat;
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
             const int n = n0 + (wn * WTN + j) * 32 + lr;
@@ -353,6 +360,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             chn[j] = n < g.N ? n - q * g.feat : -1;
             qoff[j] = (q >> 1) * (2 * g.W) + (q & 1);
             bvs[j] = (n < g.N && g.bias) ? g.bias[n] : 0.f;
+            cterm[j] = g.chunk8 ? (int)((chn[j] >> 3) * plane2 * 8) + (chn[j] & 7) : chn[j];
         }
 #pragma unroll
         for (int i = 0; i < WTM; ++i) {
@@ -372,10 +380,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
                 for (int j = 0; j < WTN; ++j) {
                     if (chn[j] < 0) continue;
-                    const size_t o = (size_t)(pbase + qoff[j]) * g.feat + chn[j];
+                    const size_t px = (size_t)(pbase + qoff[j]);
                     float v = acc[i][j][r] + bvs[j];
-                    if (g.res) v += g.res[o];
-                    g.out[o] = v;
+                    if (g.res) v += g.res[px * g.feat + chn[j]];
+                    g.out[px * pstride + cterm[j]] = v;
                 }
             }
         }
@@ -1504,7 +1512,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
                                                              const float *__restrict__ wt,
                                                              const float *__restrict__ bias,
                                                              float *__restrict__ out, int H, int W,
-                                                             int feat, int oh, int ow,
+                                                             int feat, int chunk8, int oh, int ow,
                                                              float inv_range, float m0, float m1,
                                                              float m2) {
     constexpr int TH = CL_ROWS + 2, TW = CL_COLS + 2;
@@ -1522,7 +1530,12 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
     const __amdgpu_buffer_rsrc_t rin = buf_rsrc(in, (size_t)H * W * feat * 4);
 
     // this thread's halo elements: (pixel p, float4 q) = divmod(tid + 256u, Q),
-    // out-of-plane taps (the zero padding) and elements past the halo read zero
+    // out-of-plane taps (the zero padding) and elements past the halo read zero.
+    // In 8-channel slabs a chunk is one slab: a halo row is one contiguous run
+    // (whole cache lines), where channel-last reads 32 of every pixel's 256
+    // bytes per chunk and the lines come back from memory once per chunk.
+    const int pstride = chunk8 ? CL_CC : feat;
+    const int cstep = chunk8 ? H * W * CL_CC * 4 : CL_CC * 4;  // bytes per chunk
     int eoff[NLD];
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
@@ -1530,7 +1543,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
         const int p = i / Q, q = i - p * Q;
         const int sy = y0 - 1 + p / TW, sx = x0 - 1 + p % TW;
         const bool ok = i < NV && sy >= 0 && sy < H && sx >= 0 && sx < W;
-        eoff[u] = ok ? ((sy * W + sx) * feat + 4 * q) * 4 : BUF_OOB;
+        eoff[u] = ok ? ((sy * W + sx) * pstride + 4 * q) * 4 : BUF_OOB;
     }
     // the chunk's weights [tap][ci 0..7][3] as float4s: thread t < NW4 takes
     // float4 t (tap t / 6, then 6 float4s of 8 channels x 3)
@@ -1538,9 +1551,10 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
     const int wtap = tid / (NW4 / 9), wq = tid - wtap * (NW4 / 9);
     float4 ld[NLD], lw;
     auto load = [&](int c0) __attribute__((always_inline)) {
+        const int coff = (c0 / CL_CC) * cstep;
 #pragma unroll
         for (int u = 0; u < NLD; ++u)
-            ld[u] = buf_load4(rin, eoff[u] == BUF_OOB ? BUF_OOB : eoff[u] + c0 * 4);
+            ld[u] = buf_load4(rin, eoff[u] == BUF_OOB ? BUF_OOB : eoff[u] + coff);
         lw = buf_load4(rw, tid < NW4 ? ((wtap * feat + c0) * 3 + 4 * wq) * 4 : BUF_OOB);
     };
     auto stash = [&](int b) __attribute__((always_inline)) {
@@ -2067,12 +2081,12 @@ dim3 conv_last_grid(int oh, int ow) {
 }
 
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
-                                   float *out, int H, int W, int feat, int oh, int ow,
+                                   float *out, int H, int W, int feat, int chunk8, int oh, int ow,
                                    float img_range, const float *mean, hipStream_t st) {
     if (feat % CL_CC) return hipErrorInvalidValue;
     const dim3 grid = conv_last_grid(oh, ow);
     hipLaunchKernelGGL(k_conv_last_finish, grid, dim3(256), 0, st, in, wt, bias, out, H, W, feat,
-                       oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+                       chunk8, oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
 
