@@ -103,6 +103,7 @@ struct s2s_ctx {
     std::vector<StageW> stages;
     float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C]
     std::vector<float *> up_w, up_b;           // octave convs, shuffle-permuted [4F][9*F]
+    bool last_slabs = false;                   // the last octave writes 8-channel slabs
     float *last_w = nullptr, *last_b = nullptr;  // conv_last [9][F][3]
     // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [3][9*F], conv_after_aux [F][9*4]
     float *bc_w = nullptr, *bc_b = nullptr, *ax_w = nullptr, *ax_b = nullptr;
@@ -528,15 +529,12 @@ int s2s_ctx::head(int h, int w, float *d_out) {
                 return -1;
         }
         int H = hp, W = wp;
-        const bool slabs = feat % 8 == 0 && !aux;
+        const bool slabs = last_slabs;
         for (int oc = 0; oc < octaves; ++oc) {
             g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
             g.feat = feat;
             if (aux && oc == octaves - 1) g.res = bicf;  // + the bicubic branch
-            // the last octave's plane goes to conv_last in 8-channel slabs
-            // (not with the bicubic branch: that residual is the same buffer,
-            // updated in place, so each value must land where it was read)
-            g.chunk8 = oc == octaves - 1 && slabs;
+            g.chunk8 = oc == octaves - 1 && slabs;  // (weights uploaded in slab order)
             const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
             if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
             H *= 2;
@@ -635,6 +633,18 @@ std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vect
 std::vector<int> shuffle_perm(int feat) {
     std::vector<int> p(4 * feat);
     for (int co = 0; co < 4 * feat; ++co) p[co] = (co % 4) * feat + co / 4;
+    return p;
+}
+
+// The last octave's order when its plane is stored in 8-channel slabs:
+// co = 4ch + 2dy + dx -> row (ch/8*4 + 2dy+dx)*8 + ch%8, so a 32-column tile
+// is one slab's 8 channels at the 4 sub-pixels.
+std::vector<int> slab_perm(int feat) {
+    std::vector<int> p(4 * feat);
+    for (int co = 0; co < 4 * feat; ++co) {
+        const int ch = co / 4, q = co % 4;
+        p[co] = ((ch / 8) * 4 + q) * 8 + ch % 8;
+    }
     return p;
 }
 
@@ -838,7 +848,11 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             ctx->octaves = oct;
             rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
-            std::vector<int> perm = shuffle_perm(F);
+            const std::vector<int> perm = shuffle_perm(F), sperm = slab_perm(F);
+            // the last octave's plane goes to conv_last in 8-channel slabs (not
+            // with the bicubic branch: that residual is the same buffer, updated
+            // in place, so each value must land where it was read)
+            ctx->last_slabs = F % 8 == 0 && A.upsampler != S2S_PIXELSHUFFLE_AUX;
             for (int o = 0; !rc && o < oct; ++o) {
                 const s2s_tensor *uw, *ub;
                 const std::string base = "upsample." + std::to_string(2 * o);
@@ -847,8 +861,9 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 if (rc) break;
                 float *dw, *db;
                 std::vector<float> bb(4 * F);
-                for (int co = 0; co < 4 * F; ++co) bb[perm[co]] = ub->data[co];
-                rc = ctx->upload(conv_relayout(uw->data, 4 * F, F, &perm), &dw) || ctx->upload(bb, &db);
+                const std::vector<int> &pm = (ctx->last_slabs && o == oct - 1) ? sperm : perm;
+                for (int co = 0; co < 4 * F; ++co) bb[pm[co]] = ub->data[co];
+                rc = ctx->upload(conv_relayout(uw->data, 4 * F, F, &pm), &dw) || ctx->upload(bb, &db);
                 ctx->up_w.push_back(dw);
                 ctx->up_b.push_back(db);
             }

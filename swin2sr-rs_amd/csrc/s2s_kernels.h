@@ -60,7 +60,8 @@ struct GemmArgs {
     float slope;
     int feat;  // EPI_SHUFFLE: output channels (N = 4*feat)
     // EPI_SHUFFLE: store the 2H x 2W plane in 8-channel slabs ([feat/8][P][8],
-    // the layout conv_last reads) instead of channel-last [P][feat]; a residual
+    // the layout conv_last reads) instead of channel-last [P][feat], from
+    // weights in the slab column order (ch/8*4 + 2dy+dx)*8 + ch%8; a residual
     // is still read channel-last
     int chunk8;
     // EPI_QKV_WIN: the plane is H x W, the block's shift, heads of head_dim

@@ -342,8 +342,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
     if constexpr (EPI == EPI_SHUFFLE) {
         // pixel_shuffle(2) store: n is the permuted output channel
-        // (2dy+dx)*feat + ch, m a pixel (y, x) of the H x W plane; the value
-        // lands at pixel (2y + dy, 2x + dx) of the 2H x 2W channel-last plane.
+        // (2dy+dx)*feat + ch (in slabs: (ch/8*4 + 2dy+dx)*8 + ch%8), m a pixel
+        // (y, x) of the H x W plane; the value lands at pixel (2y + dy, 2x + dx)
+        // of the 2H x 2W plane.
         // Per column: the sub-pixel offset and channel; per row: the pixel
         // (one division per row tile, the rest by carrying x past W). The
         // stored offset is pixel * pstride + cterm: channel-last (pstride =
@@ -356,11 +357,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
             const int n = n0 + (wn * WTN + j) * 32 + lr;
-            const int q = n / g.feat;
-            chn[j] = n < g.N ? n - q * g.feat : -1;
+            // column n: channel-last, (sub-pixel q)*feat + channel; in slabs,
+            // (slab*4 + q)*8 + channel%8, so 32 columns are one slab's 8
+            // channels at the 4 sub-pixels: two 64-byte runs per store
+            int q, ch;
+            if (g.chunk8) {
+                q = (n >> 3) & 3;
+                ch = ((n >> 5) << 3) + (n & 7);
+            } else {
+                q = n / g.feat;
+                ch = n - q * g.feat;
+            }
+            chn[j] = n < g.N ? ch : -1;
             qoff[j] = (q >> 1) * (2 * g.W) + (q & 1);
             bvs[j] = (n < g.N && g.bias) ? g.bias[n] : 0.f;
-            cterm[j] = g.chunk8 ? (int)((chn[j] >> 3) * plane2 * 8) + (chn[j] & 7) : chn[j];
+            cterm[j] = g.chunk8 ? (int)((ch >> 3) * plane2 * 8) + (ch & 7) : ch;
         }
 #pragma unroll
         for (int i = 0; i < WTM; ++i) {
