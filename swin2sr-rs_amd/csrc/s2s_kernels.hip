@@ -74,32 +74,28 @@ __device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, 
 // The erf GELU, 0.5 v (1 + erf(v/sqrt2)) = v * Phi(v), evaluated through the
 // complementary error function so that one branch-free formula covers every v:
 // with t = |v|/sqrt2, erfc(t) = exp(-t^2) * erfcx(t), and the scaled function
-// erfcx is smooth and bounded on [0, inf), so it is a degree-8 polynomial in
-// u = 1/(1 + t/2) (u in (0, 1]; the substitution of Numerical Recipes' erfcc).
-// The coefficients (halved, so the sum is erfc(t)/2 directly) are a
-// relative-error fit of erfcx(t)/u on t in [0, 8]
-// (iteratively reweighted least squares against scipy.special.erfcx; maximum
-// relative error 3.8e-8 in exact arithmetic). With q = erfc(t)/2, Phi(v) is
-// 1 - q for v > 0 and q otherwise, so v Phi(v) = max(v, 0) - |v| q: one max
-// and one fused multiply-add instead of a compare, a select, a subtraction
-// and a multiply, and the negative side keeps its relative accuracy instead
-// of cancelling in 1 + erf. Absolute error against the exact GELU is below
-// 2.5e-7 on [-12, 12], within the erff form's rounding. One reciprocal, one
-// exp2 and 14 other VALU operations, with no divergent branch (a library erff
-// evaluates two polynomial branches when a wavefront holds both small and
-// large arguments).
+// erfcx is smooth and bounded on [0, inf), so it is u times a degree-4
+// polynomial in u = 1/(1 + 0.478 t) (u in (0, 1]; the substitution of
+// Abramowitz & Stegun 7.1.26 with a refitted p). The five coefficients
+// (halved, so the result is erfc(t)/2 directly) are a fit of erfcx on
+// t in [0, 9] weighted by what an error costs the GELU (|v| exp(-t^2) / 2),
+// iterated toward equal ripple against scipy.special.erfcx: 4.3e-8 absolute
+// on the GELU in exact arithmetic, below float32 rounding. With q = erfc(t)/2,
+// Phi(v) is 1 - q for v > 0 and q otherwise, so v Phi(v) = max(v, 0) - |v| q:
+// one max and one fused multiply-add, and the negative side keeps its
+// relative accuracy instead of cancelling in 1 + erf. Evaluated in float32
+// the absolute error against the exact GELU is below 2.6e-7 on [-12, 12], the
+// same as the erff form's rounding. One reciprocal, one exp2 and 11 other
+// VALU operations, with no divergent branch (a library erff evaluates two
+// polynomial branches when a wavefront holds both small and large arguments).
 __device__ __forceinline__ float gelu_erf(float v) {
-    const float t = fabsf(v) * 0.70710678118654752440f;
-    const float u = __builtin_amdgcn_rcpf(fmaf(0.5f, t, 1.0f));
-    float p = -0.028918050229549408f;
-    p = fmaf(p, u, 0.13924627006053925f);
-    p = fmaf(p, u, -0.23722104728221893f);
-    p = fmaf(p, u, 0.13162502646446228f);
-    p = fmaf(p, u, -0.00811781082302332f);
-    p = fmaf(p, u, 0.0990985706448555f);
-    p = fmaf(p, u, 0.12213370949029922f);
-    p = fmaf(p, u, 0.14110521972179413f);
-    p = fmaf(p, u, 0.14104808866977692f);
+    // u = 1 / (1 + 0.478 |v| / sqrt2)
+    const float u = __builtin_amdgcn_rcpf(fmaf(fabsf(v), 0.33799704f, 1.0f));
+    float p = -0.10729234942429587f;
+    p = fmaf(p, u, 0.34028711412207455f);
+    p = fmaf(p, u, -0.05061983683614841f);
+    p = fmaf(p, u, 0.18978627981436072f);
+    p = fmaf(p, u, 0.12783743829594208f);
     // exp(-t^2) = 2^(v^2 * (-log2(e) / 2)); q = erfc(t) / 2
     const float q = u * p * __builtin_amdgcn_exp2f(v * v * -0.72134752044448170368f);
     return fmaf(-fabsf(v), q, fmaxf(v, 0.0f));
@@ -756,7 +752,13 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int t = 0; t < 3; ++t) acc[rb][t] = f4v{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < 3; ++t) {
+                // the accumulators start from the bias (the reference's CPU
+                // order: bias first, then the K sum); with K split, one half
+                // carries it
+                const float bv = (KS == 1 || kq == 0) ? prm[0][48 * cg + 16 * t + j] : 0.f;
+                acc[rb][t] = f4v{bv, bv, bv, bv};
+            }
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             float av[RB][4];
@@ -813,17 +815,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                             ksum[(((((1 - kq) * 4 + cg) * RB + rb) * 3 + t) * 2 + rr) * 64 + lane];
         }
 
-        // bias, and the row statistics when a LayerNorm follows (single-pass,
-        // as the reference's channel LayerNorm computes them; padding columns
-        // hold exact zeros)
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-            const float bv = prm[0][48 * cg + 16 * t + j];
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                for (int rr = 0; rr < NR; ++rr) acc[rb][t][R0 + rr] += bv;
-        }
+        // the row statistics when a LayerNorm follows (single-pass, as the
+        // reference's channel LayerNorm computes them; padding columns hold
+        // exact zeros)
         if (HAS_LN) {
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
