@@ -94,10 +94,17 @@ struct BsArgs {
     int hp, wp, nww, shift, heads, hd;
 };
 
+// The attention kernels run the softmax in base 2: logits scaled by log2(e)
+// (the CPB table cpbt is stored scaled, the logit scale and the mask constant
+// carry the factor), so each probability is one v_exp_f32 of (s - max)
+// instead of a multiply and the exp. exp(s - m) = 2^((s - m) log2 e), and the
+// maximum is unchanged by the positive factor.
+#define ATTN_LOG2E 1.4426950408889634f
+
 struct AttnArgs {
     const float *qkv;          // unit ? the unit layout : [hp*wp][3c] plane order q | k | v
     int unit;                  // qkv is in the unit layout (needs attn_unit_eligible)
-    const float *cpbt;         // [heads][64][64]
+    const float *cpbt;         // [heads][64][64], CPB bias x ATTN_LOG2E
     const float *logit_scale;  // [heads]
     float *out;                // [hp*wp][c]
     int hp, wp, nww, nw;

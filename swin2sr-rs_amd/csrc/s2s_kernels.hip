@@ -960,7 +960,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
 
     auto pix = [&](int t) -> int { return win_pixel(wh, ww, t, shift, g.hp, g.wp); };
 
-    const float ls = __expf(fminf(g.logit_scale[h], 4.605170185988092f));
+    const float ls = ATTN_LOG2E * __expf(fminf(g.logit_scale[h], 4.605170185988092f));
 
     // Every global read of the wave is issued here, before any arithmetic, so
     // their latencies overlap: q and k rows (lane half hh takes d = 16hh..+15,
@@ -1068,7 +1068,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
                     if (shift) {
                         const int by = win_band(wh * 8 + (key >> 3), g.hp, shift);
                         const int bx = win_band(ww * 8 + (key & 7), g.wp, shift);
-                        if (by != bq_y[qt] || bx != bq_x[qt]) v -= 100.f;
+                        if (by != bq_y[qt] || bx != bq_x[qt]) v -= 100.f * ATTN_LOG2E;
                     }
                     s[kt][qt][4 * a + b] = v;
                     mx = fmaxf(mx, v);
@@ -1081,7 +1081,7 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs g) {
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float p = __expf(s[kt][qt][e] - mx);
+                const float p = __builtin_amdgcn_exp2f(s[kt][qt][e] - mx);
                 s[kt][qt][e] = p;
                 sum += p;
             }
@@ -1223,7 +1223,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 
     // the clamped logit scale (per head, the same for every window) and the
     // bias values this lane adds: query 32qt + r, keys 32kt + 8a + 4hh + b
-    const float ls = active ? __expf(fminf(g.logit_scale[head], 4.605170185988092f)) : 0.f;
+    const float ls = active ? ATTN_LOG2E * __expf(fminf(g.logit_scale[head], 4.605170185988092f)) : 0.f;
     const float *cp = g.cpbt + ((size_t)(active ? head : 0) * 64 + qtok) * 64 + 4 * hh;
 
     f16v s[2];
@@ -1334,7 +1334,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                         const int kcol = 4 * hh + (e & 3);         // key & 7
                         const bool dy = ey && ((krow < 8 - shift) != qy);
                         const bool dx = ex && ((kcol < 8 - shift) != qx);
-                        if (dy || dx) s[kt][e] -= 100.f;
+                        if (dy || dx) s[kt][e] -= 100.f * ATTN_LOG2E;
                     }
             }
             float mx = -INFINITY;
@@ -1348,7 +1348,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = __expf(s[kt][e] - mx);
+                    const float p = __builtin_amdgcn_exp2f(s[kt][e] - mx);
                     s[kt][e] = p;
                     if (!MSUM) sum += p;
                 }
@@ -1743,7 +1743,7 @@ __global__ void k_cpb_gather(const float *__restrict__ tab, float *__restrict__ 
     const int q = qk / n, k = qk - (qk / n) * n;
     const int idx = ((q / win) - (k / win) + win - 1) * side + ((q % win) - (k % win) + win - 1);
     const float v = tab[h * side * side + idx];
-    cpbt[i] = 16.0f / (1.0f + expf(-v));
+    cpbt[i] = ATTN_LOG2E * (16.0f / (1.0f + expf(-v)));  // (base-2 softmax)
 }
 
 // ---------------------------------------------------------------------------

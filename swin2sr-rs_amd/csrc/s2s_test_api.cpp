@@ -104,7 +104,7 @@ int s2s_test_attention(int hp, int wp, int win, int heads, int head_dim, int shi
     for (int q = 0; q < n; ++q)
         for (int k = 0; k < n; ++k)
             for (int h = 0; h < heads; ++h)
-                cpbt[((size_t)h * n + q) * n + k] = cpb[((size_t)q * n + k) * heads + h];
+                cpbt[((size_t)h * n + q) * n + k] = ATTN_LOG2E * cpb[((size_t)q * n + k) * heads + h];
     // the shapes the unit-layout kernel takes get their qkv in that layout
     // (the qkv GEMM writes it in the forward; here the host lays it out)
     const bool unit = attn_unit_eligible(heads, head_dim, c);
@@ -166,7 +166,7 @@ int s2s_test_cpb_table(int win, int heads, const float *w0, const float *b0, con
     for (int q = 0; q < n; ++q)
         for (int k = 0; k < n; ++k)
             for (int h = 0; h < heads; ++h)
-                out[((size_t)q * n + k) * heads + h] = t[((size_t)h * n + q) * n + k];
+                out[((size_t)q * n + k) * heads + h] = t[((size_t)h * n + q) * n + k] / ATTN_LOG2E;
     return 0;
 }
 
