@@ -138,7 +138,8 @@ struct s2s_ctx {
 
     ~s2s_ctx();
     int upload(const std::vector<float> &host, float **dev);
-    int alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what);
+    int alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what,
+              bool wide = false);
     int plan_body(int hp, int wp);
     // qkv buffer floats: the plane layout, or the attention unit layout
     size_t qkv_floats(int hp, int wp) const {
@@ -192,19 +193,25 @@ int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
     return 0;
 }
 
-// The kernels address a buffer with 32-bit byte offsets (raw buffer loads and
-// stores whose bounds check is the out-of-range mechanism), so no single
-// buffer may reach 2 GiB. A plane that would need one is refused like an
-// allocation failure: the message says "out of memory", which is what the
-// crate's tile-halving retry keys on (src/main.rs:655-662), and a smaller tile
-// then fits.
-static constexpr size_t kMaxBufferBytes = 0x7fffffffu;
+// The kernels address buffers with raw buffer loads and stores: 32-bit byte
+// offsets from a base, with the resource's bounds check as the out-of-range
+// mechanism. The large buffers (qkv, the head's feature planes, the output)
+// are only reached through resources based per task, tile or window, or
+// through 64-bit pointers, so they may have any size ("wide"); the others
+// (planes of C or 2C channels, read whole as GEMM operands) must stay below
+// the resource limit, which holds for every plane up to 1.49 M pixels, above
+// the crate's GPU_MAX_PLANE_PIXELS (65535 x 16, src/backend.rs:230). A plane
+// that would pass it is refused like an allocation failure: the message says
+// "out of memory", which is what the crate's tile-halving retry keys on
+// (src/main.rs:655-662), and a smaller tile then fits.
+static constexpr size_t kMaxBufferBytes = 0x7fff0000u;  // BUF_MAX_BYTES of the kernels
 
-int s2s_ctx::alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what) {
-    if (floats > kMaxBufferBytes / sizeof(float))
+int s2s_ctx::alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what,
+                   bool wide) {
+    if (!wide && floats > kMaxBufferBytes / sizeof(float))
         return fail(std::string("hipMalloc(") + what + ", " + std::to_string(floats * sizeof(float)) +
-                    " bytes) refused: above the 2 GiB per-buffer limit of the kernels' 32-bit "
-                    "offsets (out of memory for one pass; tile the image)");
+                    " bytes) refused: above the 2 GiB limit of the kernels' 32-bit offsets into "
+                    "this buffer (out of memory for one pass; tile the image)");
     float *p = nullptr;
     hipError_t e = hipMalloc(&p, std::max<size_t>(floats, 1) * sizeof(float));
     if (e != hipSuccess) {
@@ -230,7 +237,8 @@ int s2s_ctx::plan_body(int hp, int wp) {
     const size_t P = (size_t)hp * wp;
     if (alloc(body_allocs, P * c, &cur, "cur") || alloc(body_allocs, P * c, &wk, "work") ||
         alloc(body_allocs, P * c, &tmp, "tmp") || alloc(body_allocs, P * c, &body, "body") ||
-        alloc(body_allocs, qkv_floats(hp, wp), &qkv, "qkv") || alloc(body_allocs, P * c, &o, "attn") ||
+        alloc(body_allocs, qkv_floats(hp, wp), &qkv, "qkv", true) ||
+        alloc(body_allocs, P * c, &o, "attn") ||
         alloc(body_allocs, P * hidden, &hid, "mlp")) {
         free_list(body_allocs);
         return -1;
@@ -253,7 +261,7 @@ int s2s_ctx::plan_image(int h, int w) {
     const int s = arch.scale;
     int rc = alloc(head_allocs, (size_t)3 * h * w, &in_dev, "input") ||
              alloc(head_allocs, P * 4, &in4, "padded input") ||
-             alloc(head_allocs, (size_t)3 * h * s * w * s, &out_dev, "output");
+             alloc(head_allocs, (size_t)3 * h * s * w * s, &out_dev, "output", true);
     // the head's feature planes: one per octave for the pixel-shuffle heads,
     // P, 4P, 16P, 16P for nearest+conv, none for pixelshuffledirect
     std::vector<size_t> planes;
@@ -265,14 +273,14 @@ int s2s_ctx::plan_image(int h, int w) {
     }
     for (size_t i = 0; rc == 0 && i < planes.size(); ++i) {
         float *f = nullptr;
-        rc = alloc(head_allocs, planes[i] * feat, &f, "head plane");
+        rc = alloc(head_allocs, planes[i] * feat, &f, "head plane", true);
         fplanes.push_back(f);
     }
     if (rc == 0 && arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
         const size_t Q = P * s * s;
         rc = alloc(head_allocs, P * 4, &aux4, "aux conv") ||
              alloc(head_allocs, P * 3, &auxp, "aux image") ||
-             alloc(head_allocs, Q * 4, &bic4, "bicubic input");
+             alloc(head_allocs, Q * 4, &bic4, "bicubic input", true);
         // the bicubic branch's conv lands in the last octave's plane, which the
         // last shuffle then updates in place (each element read, added, written
         // by one thread)

@@ -43,9 +43,12 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 // memory instructions on every path - which lets the compiler count them
 // exactly in its s_waitcnt instead of draining the queue.
 #define BUF_OOB 0x7ffffff0
+// The size is capped below BUF_OOB, so that offset stays out of range even
+// for a resource based inside a larger buffer (whose own offsets stay small).
+#define BUF_MAX_BYTES 0x7fff0000u
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
-                                             (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu),
+                                             (int)(bytes < BUF_MAX_BYTES ? bytes : BUF_MAX_BYTES),
                                              0x00020000);
 }
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
@@ -166,9 +169,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // loads: an element outside A or B (rows past M or N, k past K, a tap
     // outside the plane) reads zero from an out-of-range offset, without a
     // branch.
-    const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(
-        g.A, ALOAD == ALOAD_ROWS ? (size_t)g.M * g.lda * 4
-                                 : (size_t)g.H * g.W * g.cin * 4 / (ALOAD == ALOAD_IM2COL_UP2 ? 4 : 1));
+    // A through a resource based at the first row (pixel) this tile can
+    // touch, so the offsets stay small whatever the size of the plane
+    const int pb = ALOAD == ALOAD_ROWS     ? m0
+                   : ALOAD == ALOAD_IM2COL ? max(m0 - g.W - 1, 0)
+                                           : max((m0 / g.W - 1) >> 1, 0) * (g.W >> 1);
+    const int arow = ALOAD == ALOAD_ROWS ? g.lda : g.cin;
+    const size_t afloats = ALOAD == ALOAD_ROWS ? (size_t)g.M * g.lda
+                                               : (size_t)g.H * g.W * g.cin / (ALOAD == ALOAD_IM2COL_UP2 ? 4 : 1);
+    const __amdgpu_buffer_rsrc_t ra_rs =
+        buf_rsrc(g.A + (size_t)pb * arow, (afloats - (size_t)pb * arow) * 4);
     const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
     const int kq = (tid & 7) * 4;
     int am[AV], ay[AV], ax[AV], bo[BV];
@@ -200,17 +210,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
     auto load_chunk = [&](int k0) __attribute__((always_inline)) {
         const bool kok = k0 + kq < g.K;
-        const int shift_px = dy * g.W + dx;
+        const int shift_px = dy * g.W + dx - (ALOAD == ALOAD_IM2COL ? pb : 0);
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
             int off;
             if (ALOAD == ALOAD_ROWS) {
-                off = (am[i] < g.M && kok) ? (am[i] * g.lda + k0 + kq) * 4 : BUF_OOB;
+                off = (am[i] < g.M && kok) ? ((am[i] - pb) * g.lda + k0 + kq) * 4 : BUF_OOB;
             } else {
                 const int sy = ay[i] + dy, sx = ax[i] + dx;
                 const bool ok = am[i] < g.M && kok && (unsigned)sy < (unsigned)g.H &&
                                 (unsigned)sx < (unsigned)g.W;
-                const int px = ALOAD == ALOAD_IM2COL_UP2 ? (sy >> 1) * (g.W >> 1) + (sx >> 1)
+                // (the tap's shift carries the resource base for IM2COL)
+                const int px = ALOAD == ALOAD_IM2COL_UP2 ? (sy >> 1) * (g.W >> 1) + (sx >> 1) - pb
                                                          : am[i] + shift_px;
                 off = ok ? (px * g.cin + ci) * 4 : BUF_OOB;
             }
@@ -577,8 +588,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     // EPI_QKV_WIN: a unit is 64 rows of RSU floats, HG units per window
     const int RSU = WIN ? attn_unit_stride(g.hd) : 0;
     const int HGU = WIN ? ((g.heads + 1) >> 1) * 64 * RSU : 0;
-    const __amdgpu_buffer_rsrc_t ro_rs =
-        buf_rsrc(g.out, WIN ? (size_t)(g.M / 64) * HGU * 4 : (size_t)g.M * g.ldo * 4);
+    const size_t out_floats = WIN ? (size_t)(g.M / 64) * HGU : (size_t)g.M * g.ldo;
+    const bool out_wide = out_floats * 4 >= BUF_MAX_BYTES;
+    const __amdgpu_buffer_rsrc_t ro_all = buf_rsrc(g.out, out_floats * 4);
     // The epilogue: with K split over two wave sets, each finishes half of the
     // accumulator registers (rows 4q + R0 .. 4q + R0 + NR - 1 of a 16-row tile).
     constexpr int NR = KS == 2 ? 2 : 4;
@@ -697,6 +709,13 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     auto finish = [&](int task, const float (*prst)[TR][2], const float *pres)
         __attribute__((always_inline)) {
         const float invn = 1.0f / (float)gw;
+        // an output past the resource limit is stored through a resource
+        // based at the task's first output row, so the offsets stay small
+        const int wi = task / TPW;
+        const size_t tbase = out_wide ? (WIN ? (size_t)wi * HGU : (size_t)task * TR * g.ldo) : 0;
+        const __amdgpu_buffer_rsrc_t ro_rs =
+            out_wide ? buf_rsrc(g.out + tbase, (out_floats - tbase) * 4) : ro_all;
+        const unsigned tofs = out_wide ? 0u : (unsigned)(WIN ? (size_t)wi * HGU : (size_t)task * TR * g.ldo) * 4u;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -704,12 +723,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                 const int r = R0 + rr;
                 const int row = rb * 16 + 4 * q + r;
                 const int m = task * TR + row;
-                unsigned rowo = m < g.M ? (unsigned)m * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
-                if (WIN) {
-                    // token tk0 + row of window task / TPW (every task is whole)
-                    const int wi = task / TPW;
-                    rowo = (unsigned)(wi * HGU + ((task - wi * TPW) * TR + row) * RSU) * 4u;
-                }
+                unsigned rowo = m < g.M ? tofs + (unsigned)row * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
+                // EPI_QKV_WIN: token tk0 + row of window task / TPW (every
+                // task is whole)
+                if (WIN) rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
                 float rstd = 1.f, mr = 0.f;
                 if (HAS_LN) {
                     const float a1 = (prst[0][row][0] + prst[1][row][0]) +
@@ -1202,9 +1219,20 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
     // Copy-in: chunk c = wave + 4u of the unit (floats 256c .. 256c + 255),
     // lane l moving float4 l of it; the unit's last chunk runs past it into
     // the next unit (or out of range: zeros) and lands in the tile's slack.
-    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qkv, (size_t)g.nw * HG * UF * 4);
-    auto copy_unit = [&](int wi) __attribute__((always_inline)) {
-        const int base = (wi * HG + hg) * UF * 4;
+    // (a qkv buffer past the resource limit is reached through a resource
+    // based at each unit, so the offsets stay small; the last chunk's tail
+    // then reads zeros)
+    const size_t qkv_bytes = (size_t)g.nw * HG * UF * 4;
+    const bool qkv_wide = qkv_bytes >= BUF_MAX_BYTES;
+    const __amdgpu_buffer_rsrc_t rq_all = buf_rsrc(g.qkv, qkv_bytes);
+    // (the resource and base of a unit, computed ahead of the copy so that
+    // the scalar arithmetic is off the path from the barrier to the copy)
+    auto unit_rsrc = [&](int wi, int &base) __attribute__((always_inline)) {
+        const size_t ub = (size_t)(wi * HG + hg) * UF;
+        base = qkv_wide ? 0 : (int)ub * 4;
+        return qkv_wide ? buf_rsrc(g.qkv + ub, UF * 4) : rq_all;
+    };
+    auto copy_unit = [&](__amdgpu_buffer_rsrc_t rq, int base) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < NCW; ++u) {
             const int c = wave + 4 * u;
@@ -1247,7 +1275,11 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 
     constexpr int NST = 4;              // output stores per thread
     int wi = xcd + 8 * ws;
-    if (wi < g.nw) copy_unit(wi);
+    if (wi < g.nw) {
+        int b0;
+        const __amdgpu_buffer_rsrc_t r0 = unit_rsrc(wi, b0);
+        copy_unit(r0, b0);
+    }
     load_bias();
     // as many dropped stores as a window's output has: the loop is then entered
     // with the same queue (copies and bias loads, then stores) as it loops back
@@ -1264,6 +1296,8 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
         if (own_one) tile[lane * RS + 6 * HD] = 1.0f;
         lds_sync();
         const int wn = wi + wstep;
+        int nbase;
+        const __amdgpu_buffer_rsrc_t nrq = unit_rsrc(wn < g.nw ? wn : wi, nbase);
         const int wh = wi / g.nww;
         const int ww = wi - wh * g.nww;
 
@@ -1403,7 +1437,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             ov[u] = make_float4(a.x, a.y, b.x, b.y);
         }
         lds_sync();  // every wave has read the tile: the next unit may land
-        if (wn < g.nw) copy_unit(wn);
+        if (wn < g.nw) copy_unit(nrq, nbase);
 
         // ---- the window's output slices, coalesced ----
         {
@@ -1532,15 +1566,19 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
     const int wave = tid >> 6;
     const int x0 = blockIdx.x * CL_COLS, y0 = blockIdx.y * CL_ROWS;
     const int nch = feat / CL_CC;
-    const __amdgpu_buffer_rsrc_t rin = buf_rsrc(in, (size_t)H * W * feat * 4);
 
     // this thread's halo elements: (pixel p, float4 q) = divmod(tid + 256u, Q),
     // out-of-plane taps (the zero padding) and elements past the halo read zero.
     // In 8-channel slabs a chunk is one slab: a halo row is one contiguous run
     // (whole cache lines), where channel-last reads 32 of every pixel's 256
     // bytes per chunk and the lines come back from memory once per chunk.
+    // Offsets are taken from the tile's first halo row (a resource per chunk
+    // based there), so they stay small whatever the size of the plane.
     const int pstride = chunk8 ? CL_CC : feat;
-    const int cstep = chunk8 ? H * W * CL_CC * 4 : CL_CC * 4;  // bytes per chunk
+    const size_t cstep = chunk8 ? (size_t)H * W * CL_CC : CL_CC;  // floats per chunk
+    const int ybase = max(y0 - 1, 0);
+    const size_t pbase = (size_t)ybase * W * pstride;              // floats
+    const size_t cfloats = chunk8 ? (size_t)H * W * CL_CC : (size_t)H * W * feat;
     int eoff[NLD];
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
@@ -1548,7 +1586,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
         const int p = i / Q, q = i - p * Q;
         const int sy = y0 - 1 + p / TW, sx = x0 - 1 + p % TW;
         const bool ok = i < NV && sy >= 0 && sy < H && sx >= 0 && sx < W;
-        eoff[u] = ok ? ((sy * W + sx) * pstride + 4 * q) * 4 : BUF_OOB;
+        eoff[u] = ok ? (((sy - ybase) * W + sx) * pstride + 4 * q) * 4 : BUF_OOB;
     }
     // the chunk's weights [tap][ci 0..7][3] as float4s: thread t < NW4 takes
     // float4 t (tap t / 6, then 6 float4s of 8 channels x 3)
@@ -1556,10 +1594,12 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
     const int wtap = tid / (NW4 / 9), wq = tid - wtap * (NW4 / 9);
     float4 ld[NLD], lw;
     auto load = [&](int c0) __attribute__((always_inline)) {
-        const int coff = (c0 / CL_CC) * cstep;
+        // chunk c0 / CL_CC: its slab, or its 8 channels of every pixel
+        const size_t cb = (size_t)(c0 / CL_CC) * cstep + pbase;
+        const __amdgpu_buffer_rsrc_t rin =
+            buf_rsrc(in + cb, chunk8 ? (cfloats * (c0 / CL_CC + 1) - cb) * 4 : (cfloats - cb) * 4);
 #pragma unroll
-        for (int u = 0; u < NLD; ++u)
-            ld[u] = buf_load4(rin, eoff[u] == BUF_OOB ? BUF_OOB : eoff[u] + coff);
+        for (int u = 0; u < NLD; ++u) ld[u] = buf_load4(rin, eoff[u]);
         lw = buf_load4(rw, tid < NW4 ? ((wtap * feat + c0) * 3 + 4 * wq) * 4 : BUF_OOB);
     };
     auto stash = [&](int b) __attribute__((always_inline)) {

@@ -257,20 +257,48 @@ def test_forward_rejects_tiny_image(pkg):
         be.close()
 
 
-def test_forward_refuses_buffers_past_2gib(pkg):
-    """A plane whose head buffer would pass the kernels' 32-bit byte offsets
-    (1008^2 padded pixels x 16 x 64 channels x 4 B = 4.2 GB at x4) is refused
-    with an "out of memory" message - the condition the crate's tile-halving
-    retry keys on - and the context still runs a small image afterwards."""
+def test_forward_with_buffers_past_2gib(pkg):
+    """A plane whose qkv buffer (1008^2 x 546 floats = 2.2 GB) and last head
+    plane (1008^2 x 16 x 64 floats = 4.2 GB) pass 2 GiB runs: those buffers are
+    reached through resources based per task, tile or window. The input repeats
+    a random 16 x 16 patch, so away from the borders (the reflect padding and
+    the shifted-window mask live there) every window, conv tap and pixel sees
+    what it sees in a 200 x 200 image of the same pattern, and the outputs
+    there must agree bit for bit (every kernel's per-output arithmetic is
+    independent of where the output sits in the launch)."""
     M = pkg.model
-    arch = M.Arch(upsampler="pixelshuffle", scale=4, embed=24, heads=2, depths=[1])
+    arch = M.Arch(upsampler="pixelshuffle", scale=4, embed=180, heads=6, depths=[1])
+    be = pkg.abi.HipBackend(arch, M.make_weights(arch, seed=1, perturb=True))
+    patch = np.random.default_rng(3).uniform(0, 1, (3, 16, 16)).astype(np.float32)
+    try:
+        outs = []
+        for n in (1000, 200):
+            img = np.tile(patch, (1, n // 16 + 1, n // 16 + 1))[:, :n, :n]
+            outs.append(be.forward(n, n, M.adjust(arch, np.ascontiguousarray(img))))
+        big, small = outs
+        assert big.shape == (3, 4000, 4000) and np.isfinite(big).all()
+        sl = (slice(None), slice(4 * 64, 4 * 128), slice(4 * 64, 4 * 128))
+        assert np.array_equal(big[sl], small[sl])
+    finally:
+        be.close()
+
+
+def test_forward_refuses_plane_past_buffer_limit(pkg):
+    """A plane whose MLP hidden buffer would pass the 32-bit offsets of the
+    GEMM that reads it whole (1248^2 padded pixels x 360 x 4 B = 2.24 GB) is
+    refused with an "out of memory" message - the condition the crate's
+    tile-halving retry keys on - and the context still runs a small image
+    afterwards. (The limit, 1.49 M pixels, is above the crate's
+    GPU_MAX_PLANE_PIXELS of 65535 x 16.)"""
+    M = pkg.model
+    arch = M.Arch(upsampler="pixelshuffle", scale=2, embed=180, heads=6, depths=[1])
     be = pkg.abi.HipBackend(arch, M.make_weights(arch, seed=1))
     try:
         with pytest.raises(pkg.abi.S2SError, match="out of memory"):
-            be.forward(1000, 1000, np.zeros((3, 1000, 1000), np.float32))
+            be.forward(1240, 1240, np.zeros((3, 1240, 1240), np.float32))
         x = M.adjust(arch, M.to_unit(M.input_sinusoids(16, 16, seed=2)))
         y = be.forward(16, 16, x)
-        assert y.shape == (3, 64, 64) and np.isfinite(y).all()
+        assert y.shape == (3, 32, 32) and np.isfinite(y).all()
     finally:
         be.close()
 
