@@ -4,18 +4,20 @@
 // row-major in the plane. That one choice removes the reference's window
 // gather and scatter copies (reference cuda/swin2sr.cu:99-154): every per-token
 // op (the projections, LayerNorm, the MLP, the residuals) runs on the plane in
-// raster order, and only window attention needs the cyclic-shift window map,
-// which it evaluates in registers when it reads its 64 tokens and again when it
-// writes them back (reference src/plan.rs:72-108).
+// raster order, and only window attention needs the cyclic-shift window map
+// (reference src/plan.rs:72-108): the qkv GEMM reads its rows through it, the
+// attention writes its output back through it.
 //
-// Dense contractions run on `v_mfma_f32_32x32x2f32` (fp32 in, fp32 accumulate):
-//   - k_gemm: token GEMMs (qkv, proj, fc1, fc2, the 1x1 convs) and the 3x3
-//     convolutions as implicit GEMMs (im2col done by the operand loader), with
-//     the elementwise work fused into the epilogue: bias, erf-GELU, residual
-//     add, LeakyReLU, LayerNorm (+ residual) over the full 180-wide row, and the
-//     pixel-shuffle store of the head's octaves.
-//   - k_attention: one wavefront per (window, head) computes S^T = K Q^T and
-//     O^T = V^T P^T on MFMA with the softmax in registers between them.
+// Dense contractions run on fp32 MFMA (fp32 in, fp32 accumulate):
+//   - k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2, the 1x1 convs), weights
+//     stationary in registers, with the elementwise work fused into the
+//     epilogue: bias, erf-GELU, residual, LeakyReLU, LayerNorm (+ residual)
+//     over the full row, and the qkv store in the attention's unit layout;
+//   - k_gemm: the 3x3 convolutions as implicit GEMMs (im2col done by the
+//     operand loader), with the same epilogues and the pixel-shuffle store of
+//     the head's octaves;
+//   - k_wattn (k_attention for other head shapes): S^T = K Q^T and
+//     O^T = V^T P^T per (window, head) with the softmax in registers between.
 // Memory-bound leftovers (input padding, the standalone final LayerNorm and
 // the 64->3 conv_last with the crop/denormalisation) are plain streaming
 // kernels.
@@ -1478,59 +1480,74 @@ __global__ void k_pad_input(const float *__restrict__ in, float *__restrict__ ou
 }
 
 // Channel LayerNorm over a channel-last plane (reference cpu::channel_layer_norm,
-// src/cpu.rs:1019-1073, single-pass statistics): 16 lanes per pixel, float4.
-// Optional residual: out = res + LN(x).
+// src/cpu.rs:1019-1073, single-pass statistics). A pixel is one 16-lane DPP
+// row (float4s l, l+16, l+32, ... of its channels, all loaded before any is
+// used), its sums reduced with four DPP adds; each row takes LN_PIX pixels,
+// every load of all of them issued up front so that many bytes are in flight
+// per thread. Optional residual: out = res + LN(x). C <= 192.
+#define LN_PIX 2
 __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x,
                                                    const float *__restrict__ w,
                                                    const float *__restrict__ b,
                                                    const float *__restrict__ res,
                                                    float *__restrict__ out, int P, int C) {
-    const int pix = blockIdx.x * 16 + (threadIdx.x >> 4);
     const int l = threadIdx.x & 15;
+    const int pix0 = (blockIdx.x * 16 + (threadIdx.x >> 4)) * LN_PIX;
     const int nv = C >> 2;
-    float4 v[4];
-    float s1 = 0.f, s2 = 0.f;
-    const bool live = pix < P;
+    float4 v[LN_PIX][3];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int q = l + 16 * i;
-        if (live && q < nv) {
-            v[i] = *reinterpret_cast<const float4 *>(x + (size_t)pix * C + 4 * q);
-            s1 += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-            s2 += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-        } else {
-            v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < LN_PIX; ++k)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int q = l + 16 * i;
+            const int pix = pix0 + k;
+            v[k][i] = (pix < P && q < nv)
+                          ? *reinterpret_cast<const float4 *>(x + (size_t)pix * C + 4 * q)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    }
+    float4 ww[3], bb[3];
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) {
-        s1 += __shfl_xor(s1, o, 16);
-        s2 += __shfl_xor(s2, o, 16);
+    for (int i = 0; i < 3; ++i) {
+        const int q = min(l + 16 * i, nv - 1);
+        ww[i] = *reinterpret_cast<const float4 *>(w + 4 * q);
+        bb[i] = *reinterpret_cast<const float4 *>(b + 4 * q);
     }
-    if (!live) return;
-    const float mean = s1 / (float)C;
-    float var = s2 / (float)C - mean * mean;
-    var = var > 0.f ? var : 0.f;
-    const float rstd = 1.0f / sqrtf(var + 1e-5f);
+    const float invc = 1.0f / (float)C;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int q = l + 16 * i;
-        if (q >= nv) continue;
-        const float4 ww = *reinterpret_cast<const float4 *>(w + 4 * q);
-        const float4 bb = *reinterpret_cast<const float4 *>(b + 4 * q);
-        float4 y;
-        y.x = (v[i].x - mean) * rstd * ww.x + bb.x;
-        y.y = (v[i].y - mean) * rstd * ww.y + bb.y;
-        y.z = (v[i].z - mean) * rstd * ww.z + bb.z;
-        y.w = (v[i].w - mean) * rstd * ww.w + bb.w;
-        if (res) {
-            const float4 rr = *reinterpret_cast<const float4 *>(res + (size_t)pix * C + 4 * q);
-            y.x += rr.x;
-            y.y += rr.y;
-            y.z += rr.z;
-            y.w += rr.w;
+    for (int k = 0; k < LN_PIX; ++k) {
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            s1 += (v[k][i].x + v[k][i].y) + (v[k][i].z + v[k][i].w);
+            s2 += (v[k][i].x * v[k][i].x + v[k][i].y * v[k][i].y) +
+                  (v[k][i].z * v[k][i].z + v[k][i].w * v[k][i].w);
         }
-        *reinterpret_cast<float4 *>(out + (size_t)pix * C + 4 * q) = y;
+        s1 = row16_sum(s1);
+        s2 = row16_sum(s2);
+        const int pix = pix0 + k;
+        if (pix >= P) continue;
+        const float mean = s1 * invc;
+        float var = s2 * invc - mean * mean;
+        var = var > 0.f ? var : 0.f;
+        const float rstd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int q = l + 16 * i;
+            if (q >= nv) continue;
+            float4 y;
+            y.x = (v[k][i].x - mean) * rstd * ww[i].x + bb[i].x;
+            y.y = (v[k][i].y - mean) * rstd * ww[i].y + bb[i].y;
+            y.z = (v[k][i].z - mean) * rstd * ww[i].z + bb[i].z;
+            y.w = (v[k][i].w - mean) * rstd * ww[i].w + bb[i].w;
+            if (res) {
+                const float4 rr = *reinterpret_cast<const float4 *>(res + (size_t)pix * C + 4 * q);
+                y.x += rr.x;
+                y.y += rr.y;
+                y.z += rr.z;
+                y.w += rr.w;
+            }
+            *reinterpret_cast<float4 *>(out + (size_t)pix * C + 4 * q) = y;
+        }
     }
 }
 
@@ -2118,7 +2135,9 @@ hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, i
 
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,
                             float *out, int P, int C, hipStream_t st) {
-    hipLaunchKernelGGL(k_layernorm, dim3((P + 15) / 16), dim3(256), 0, st, x, w, b, res, out, P,
+    if (C > 192 || C % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_layernorm, dim3((P + 16 * LN_PIX - 1) / (16 * LN_PIX)), dim3(256), 0, st, x,
+                       w, b, res, out, P,
                        C);
     return hipGetLastError();
 }
