@@ -74,6 +74,10 @@ __device__ __forceinline__ float4 buf_load4s(__amdgpu_buffer_rsrc_t r, int voff,
 __device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, int soff, float4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, voff, soff, 0);
 }
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void buf_store2(__amdgpu_buffer_rsrc_t r, int off, float2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, v), r, off, 0, 0);
+}
 
 
 // The erf GELU, 0.5 v (1 + erf(v/sqrt2)) = v * Phi(v), evaluated through the
@@ -469,14 +473,23 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 //     operands are 4 consecutive floats of a weight row), and k = 16G + Rq + t
 //     for the R-step tail. The permutation reorders the reduction, not the
 //     result.
+//   - the MFMA computes the transposed tile, weights as its A operand and the
+//     token rows as its B operand, so a lane ends up holding ONE output row
+//     (row l%16 of the tile) and 4 consecutive columns of it per MFMA tile
+//     (4(l/16) .. 4(l/16) + 3): 12 values of the row in 3 tiles. The epilogue
+//     then stores float4s (float2s with K split), reads the residual and the
+//     LayerNorm weights as float4s, and the row statistics need only the
+//     lane's own 12 values plus one reduction over the 4 lane groups
+//     (v_permlane16_swap / v_permlane32_swap) before the 4 column waves (x2
+//     K halves) meet in LDS;
 //   - the whole row is inside the workgroup, so LayerNorm (+ residual) is an
-//     epilogue: row sums over the lane's 3 tiles, over the 16 lanes of a lane
-//     group, then over the 4 column waves through LDS.
+//     epilogue.
 // Blocks are numbered ng*P + p with P a multiple of 8, so the column groups
 // that read the same A tile run on the same XCD and share its L2.
 //
 // MFMA 16x16x4 f32 lane layout: lane l supplies A[l%16][k] and B[k][l%16] for
 // its k (above); accumulator register r of lane l holds D[4*(l/16) + r][l%16].
+// With A = weights and B = tokens, D is the transposed output tile.
 // ---------------------------------------------------------------------------
 
 typedef float f4v __attribute__((ext_vector_type(4)));
@@ -534,6 +547,22 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// Sum over the four 16-lane rows, into lanes 0-15 (lane l < 16 gets lanes l,
+// l+16, l+32, l+48; the other lanes get partial sums). v_permlane16_swap(v, 0)
+// leaves rows (v0, 0, v2, 0) in v and (v1, 0, v3, 0) in the zero operand,
+// v_permlane32_swap(w, 0) the low half of w in lanes 0-31 of w and the high
+// half in lanes 0-31 of the other (gfx950). Inline assembly: the compiler's
+// builtins for these swaps have added one result to itself instead of to the
+// other one; the s_nop covers the VALU-write-then-permlane hazard.
+__device__ __forceinline__ float xrow_sum0(float v) {
+    float z = 0.f;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(v), "+v"(z));
+    v += z;
+    float z2 = 0.f;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(v), "+v"(z2));
+    return v + z2;
+}
+
 template <int KPW, int KS, int RB, int EPI>
 __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int NT = 256 * KS;
@@ -557,7 +586,14 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int CR = HAS_RES ? (TR * 192 * 4 + 1023) / 1024 : 0;
     constexpr int NCR = HAS_RES ? (CR + NW - 1) / NW : 0;
     constexpr int RTILE = HAS_RES ? NCR * NW * 256 : 1;
-    constexpr int NSTORE = (KS == 2 ? 2 : 4) * 3 * RB;  // buffer stores per lane per task
+    // The MFMA computes the transposed tile (a lane holds one row, 4
+    // consecutive columns per tile) except for the unit-layout store, whose
+    // 8-byte-aligned rows take one dword per column: there a lane holds one
+    // column and 4 rows per tile, and 16 lanes store 64 contiguous bytes.
+    constexpr bool TT = !WIN;
+    // buffer stores per lane per task: a float4 per tile (float2 with K
+    // split), or one dword per value for the unit layout
+    constexpr int NSTORE = TT ? 3 * RB : (KS == 2 ? 2 : 4) * 3 * RB;
     static_assert(KPW % 4 == 0, "K must be a multiple of 4");
     (void)NT;
 
@@ -570,9 +606,11 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     // K halves swap the accumulator registers the other half finishes:
     // [sender half][column wave][rb][tile][register pair][lane]
     __shared__ float ksum[KS == 2 ? 2 * 4 * RB * 3 * 2 * 64 : 1];
-    __shared__ float rst0[4][TR][2];
-    __shared__ float rst1[4][TR][2];
-    __shared__ float prm[3][192];              // bias, LN weight, LN bias of the group's columns
+    // row statistics: [K half * 4 + column wave][row][sum, sum of squares]
+    __shared__ float rst0[4 * KS][TR][2];
+    __shared__ float rst1[4 * KS][TR][2];
+    // bias, LN weight, LN bias of the group's columns
+    __shared__ __attribute__((aligned(16))) float prm[3][192];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -596,7 +634,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const bool out_wide = out_floats * 4 >= BUF_MAX_BYTES;
     const __amdgpu_buffer_rsrc_t ro_all = buf_rsrc(g.out, out_floats * 4);
     // The epilogue: with K split over two wave sets, each finishes half of the
-    // accumulator registers (rows 4q + R0 .. 4q + R0 + NR - 1 of a 16-row tile).
+    // accumulator registers (columns 4q + R0 .. 4q + R0 + NR - 1 of a tile).
     constexpr int NR = KS == 2 ? 2 : 4;
     const int R0 = KS == 2 ? 2 * kq : 0;
     // output byte offsets: a column part per tile (out of range past the
@@ -605,7 +643,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     unsigned colo[3];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
-        const int cl = 48 * cg + 16 * t + j;
+        // the first of the NR consecutive columns this lane finishes in tile t
+        // (a run never straddles the group's end, a multiple of 4), or the
+        // lane's column for the unit layout
+        const int cl = TT ? 48 * cg + 16 * t + 4 * q + R0 : 48 * cg + 16 * t + j;
         if (WIN) {
             // column seg*C + head*hd + d -> unit (head/2), segment seg, the
             // head's half of it, d
@@ -627,7 +668,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     float bw[3][S];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
-        const int cl = 48 * cg + 16 * t + j;
+        const int cl = 48 * cg + 16 * t + j;  // (the MFMA's A row l%16: an output column)
         const int boff = cl < gw ? ((gc0 + cl) * g.ldb + kbase) * 4 : BUF_OOB;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
@@ -720,42 +761,95 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         const __amdgpu_buffer_rsrc_t ro_rs =
             out_wide ? buf_rsrc(g.out + tbase, (out_floats - tbase) * 4) : ro_all;
         const unsigned tofs = out_wide ? 0u : (unsigned)(WIN ? (size_t)wi * HGU : (size_t)task * TR * g.ldo) * 4u;
+        if constexpr (!TT) {
+            // unit layout (no LayerNorm, no residual): register r of tile t is
+            // row 4q + r, the lane's column j; one dword store per value
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int rr = 0; rr < NR; ++rr) {
-                const int r = R0 + rr;
-                const int row = rb * 16 + 4 * q + r;
-                const int m = task * TR + row;
-                unsigned rowo = m < g.M ? tofs + (unsigned)row * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
-                // EPI_QKV_WIN: token tk0 + row of window task / TPW (every
-                // task is whole)
-                if (WIN) rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
-                float rstd = 1.f, mr = 0.f;
+                for (int rr = 0; rr < NR; ++rr) {
+                    const int r = R0 + rr;
+                    const int row = rb * 16 + 4 * q + r;
+                    const unsigned rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
+#pragma unroll
+                    for (int t = 0; t < 3; ++t)
+                        buf_store1(ro_rs, (int)(rowo + colo[t]), pacc[rb][t][r]);
+                }
+            return;
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int row = rb * 16 + j;
+            const int m = task * TR + row;
+            unsigned rowo = m < g.M ? tofs + (unsigned)row * (unsigned)g.ldo * 4u : (unsigned)BUF_OOB;
+            // EPI_QKV_WIN: token tk0 + row of window task / TPW (every task is
+            // whole)
+            if (WIN) rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
+            float rstd = 1.f, mr = 0.f;
+            if (HAS_LN) {
+                float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+                for (int c = 0; c < 4 * KS; ++c) {
+                    a1 += prst[c][row][0];
+                    a2 += prst[c][row][1];
+                }
+                const float mean = a1 * invn;
+                float var = a2 * invn - mean * mean;
+                var = var > 0.f ? var : 0.f;
+                rstd = __builtin_amdgcn_rsqf(var + 1e-5f);
+                mr = mean * rstd;
+            }
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                // columns cl .. cl + NR - 1; columns past the group read
+                // inside the tile's allocation and are dropped at the store
+                const int cl = 48 * cg + 16 * t + 4 * q + R0;
+                float v[NR], lw[NR], lb[NR], rs[NR];
+#pragma unroll
+                for (int rr = 0; rr < NR; ++rr) v[rr] = pacc[rb][t][R0 + rr];
                 if (HAS_LN) {
-                    const float a1 = (prst[0][row][0] + prst[1][row][0]) +
-                                     (prst[2][row][0] + prst[3][row][0]);
-                    const float a2 = (prst[0][row][1] + prst[1][row][1]) +
-                                     (prst[2][row][1] + prst[3][row][1]);
-                    const float mean = a1 * invn;
-                    float var = a2 * invn - mean * mean;
-                    var = var > 0.f ? var : 0.f;
-                    rstd = __builtin_amdgcn_rsqf(var + 1e-5f);
-                    mr = mean * rstd;
+                    if (NR == 4) {
+                        const float4 w4 = *reinterpret_cast<const float4 *>(&prm[1][cl]);
+                        const float4 b4 = *reinterpret_cast<const float4 *>(&prm[2][cl]);
+                        lw[0] = w4.x; lw[1] = w4.y; lw[2 % NR] = w4.z; lw[3 % NR] = w4.w;
+                        lb[0] = b4.x; lb[1] = b4.y; lb[2 % NR] = b4.z; lb[3 % NR] = b4.w;
+                    } else {
+                        const float2 w2 = *reinterpret_cast<const float2 *>(&prm[1][cl]);
+                        const float2 b2 = *reinterpret_cast<const float2 *>(&prm[2][cl]);
+                        lw[0] = w2.x; lw[1] = w2.y;
+                        lb[0] = b2.x; lb[1] = b2.y;
+                    }
+                }
+                if (HAS_RES) {
+                    if (NR == 4) {
+                        const float4 r4 = *reinterpret_cast<const float4 *>(&pres[row * g.ldr + cl]);
+                        rs[0] = r4.x; rs[1] = r4.y; rs[2 % NR] = r4.z; rs[3 % NR] = r4.w;
+                    } else {
+                        const float2 r2 = *reinterpret_cast<const float2 *>(&pres[row * g.ldr + cl]);
+                        rs[0] = r2.x; rs[1] = r2.y;
+                    }
                 }
 #pragma unroll
-                for (int t = 0; t < 3; ++t) {
-                    const int cl = 48 * cg + 16 * t + j;
-                    float v = pacc[rb][t][r];
-                    if (HAS_LN) v = fmaf(fmaf(v, rstd, -mr), prm[1][cl], prm[2][cl]);
-                    if (EPI == EPI_GELU) v = gelu_erf(v);
-                    if (EPI == EPI_LRELU) v = v < 0.f ? v * g.slope : v;
-                    // columns past the group read inside the tile's allocation
-                    // and are dropped at the store
-                    if (HAS_RES) v += pres[row * g.ldr + cl];
-                    buf_store1(ro_rs, (int)(rowo + colo[t]), v);
+                for (int rr = 0; rr < NR; ++rr) {
+                    float x = v[rr];
+                    if (HAS_LN) x = fmaf(fmaf(x, rstd, -mr), lw[rr], lb[rr]);
+                    if (EPI == EPI_GELU) x = gelu_erf(x);
+                    if (EPI == EPI_LRELU) x = x < 0.f ? x * g.slope : x;
+                    if (HAS_RES) x += rs[rr];
+                    v[rr] = x;
+                }
+                const int off = (int)(rowo + colo[t]);
+                if (NR == 4 && !WIN) {
+                    buf_store4(ro_rs, off, make_float4(v[0], v[1], v[2 % NR], v[3 % NR]));
+                } else if (NR == 4) {
+                    buf_store2(ro_rs, off, make_float2(v[0], v[1]));
+                    buf_store2(ro_rs, colo[t] == (unsigned)BUF_OOB ? BUF_OOB : off + 8,
+                               make_float2(v[2 % NR], v[3 % NR]));
+                } else {
+                    buf_store2(ro_rs, off, make_float2(v[0], v[1]));
                 }
             }
+        }
     };
 
     // One task: the next A tile streams into `nxt_buf` while this one
@@ -775,10 +869,17 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
             for (int t = 0; t < 3; ++t) {
                 // the accumulators start from the bias (the reference's CPU
-                // order: bias first, then the K sum); with K split, one half
-                // carries it
-                const float bv = (KS == 1 || kq == 0) ? prm[0][48 * cg + 16 * t + j] : 0.f;
-                acc[rb][t] = f4v{bv, bv, bv, bv};
+                // order: bias first, then the K sum) of the lane's 4 columns;
+                // with K split, one half carries it
+                if (TT) {
+                    const float4 b4 = (KS == 1 || kq == 0)
+                                          ? *reinterpret_cast<const float4 *>(&prm[0][48 * cg + 16 * t + 4 * q])
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                    acc[rb][t] = f4v{b4.x, b4.y, b4.z, b4.w};
+                } else {
+                    const float bv = (KS == 1 || kq == 0) ? prm[0][48 * cg + 16 * t + j] : 0.f;
+                    acc[rb][t] = f4v{bv, bv, bv, bv};
+                }
             }
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
@@ -798,7 +899,8 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                     for (int t = 0; t < 3; ++t)
-                        acc[rb][t] = MFMA16(av[rb][i], bw[t][4 * gi + i], acc[rb][t]);
+                        acc[rb][t] = TT ? MFMA16(bw[t][4 * gi + i], av[rb][i], acc[rb][t])
+                                        : MFMA16(av[rb][i], bw[t][4 * gi + i], acc[rb][t]);
             // the previous task's epilogue, issued while these MFMAs run
             if constexpr (HP) {
                 if (gi == 0) finish(prev_task, prst, pres);
@@ -810,7 +912,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             for (int rb = 0; rb < RB; ++rb) {
                 const float a = cur[(rb * 16 + j) * KT + kbase + 16 * G + R * q + i];
 #pragma unroll
-                for (int t = 0; t < 3; ++t) acc[rb][t] = MFMA16(a, bw[t][4 * G + i], acc[rb][t]);
+                for (int t = 0; t < 3; ++t)
+                    acc[rb][t] = TT ? MFMA16(bw[t][4 * G + i], a, acc[rb][t])
+                                    : MFMA16(a, bw[t][4 * G + i], acc[rb][t]);
             }
         }
 
@@ -840,20 +944,26 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         // reference's channel LayerNorm computes them; padding columns hold
         // exact zeros)
         if (HAS_LN) {
+            // this row's sums over the lane's NR x 3 columns, then over the 4
+            // lane groups (the row's other columns in this wave)
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
+            for (int rb = 0; rb < RB; ++rb) {
+                float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-                for (int rr = 0; rr < NR; ++rr) {
-                    const int r = R0 + rr;
-                    const float s1 = row16_sum((acc[rb][0][r] + acc[rb][1][r]) + acc[rb][2][r]);
-                    const float s2 = row16_sum(
-                        (acc[rb][0][r] * acc[rb][0][r] + acc[rb][1][r] * acc[rb][1][r]) +
-                        acc[rb][2][r] * acc[rb][2][r]);
-                    if (j == 0) {
-                        wrst[cg][rb * 16 + 4 * q + r][0] = s1;
-                        wrst[cg][rb * 16 + 4 * q + r][1] = s2;
+                for (int t = 0; t < 3; ++t)
+#pragma unroll
+                    for (int rr = 0; rr < NR; ++rr) {
+                        const float x = acc[rb][t][R0 + rr];
+                        s1 += x;
+                        s2 = fmaf(x, x, s2);
                     }
+                s1 = xrow_sum0(s1);
+                s2 = xrow_sum0(s2);
+                if (q == 0) {
+                    wrst[kq * 4 + cg][rb * 16 + j][0] = s1;
+                    wrst[kq * 4 + cg][rb * 16 + j][1] = s2;
                 }
+            }
         }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
@@ -1932,6 +2042,13 @@ static int cu_count() {
 static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks) {
     if (aload != ALOAD_ROWS || epi == EPI_SHUFFLE) return false;
     if (g.lda % 4 || g.ldb % 4 || g.M <= 0 || g.N <= 0) return false;
+    // each lane stores runs of 4 (2) consecutive columns as one float4 (float2):
+    // the column groups and the row strides are multiples of 4
+    {
+        const int ng = (g.N + 191) / 192;
+        if (g.N % 4 || ((g.N + ng - 1) / ng) % 4 || g.ldo % 4) return false;
+        if ((epi == EPI_RES || epi == EPI_LN_RES) && g.ldr % 4) return false;
+    }
     // the A tile (and the residual tile) are copied as contiguous blocks
     if (g.lda != g.K) return false;
     if ((epi == EPI_RES || epi == EPI_LN_RES) && (g.ldr != g.N || g.N > 192)) return false;
