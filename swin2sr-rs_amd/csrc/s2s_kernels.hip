@@ -153,8 +153,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     const int wave = tid >> 6;
     const int wm = wave / WN;
     const int wn = wave % WN;
-    const int m0 = blockIdx.x * MT;
-    const int n0 = blockIdx.y * NT;
+    // XCD-aware tile order over a 1-D grid: workgroup b runs on XCD b % 8, so
+    // XCD x takes the contiguous range [x*per + min(x, rem), ...) of the tiles
+    // in row-major order (row tile outer, column tiles of one row tile
+    // adjacent). The tiles resident on one XCD at a time then share their A
+    // rows, and an im2col tile's halo rows, in that XCD's L2; with the
+    // hardware's round-robin order over a 2-D grid every column tile pass and
+    // every XCD re-read the whole plane from memory.
+    const int ntn = (g.N + NT - 1) / NT;
+    const int ntiles = ((g.M + MT - 1) / MT) * ntn;
+    const int xcd = blockIdx.x & 7;
+    const int lin = xcd * (ntiles >> 3) + min(xcd, ntiles & 7) + (int)(blockIdx.x >> 3);
+    const int m0 = (lin / ntn) * MT;
+    const int n0 = (lin - (lin / ntn) * ntn) * NT;
     const int lr = lane & 31;
     const int lh = lane >> 5;
 
@@ -1921,7 +1932,8 @@ __global__ void k_cpb_gather(const float *__restrict__ tab, float *__restrict__ 
 
 template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
 static hipError_t run_gemm_t(const GemmArgs &g, hipStream_t st) {
-    dim3 grid((g.M + MT - 1) / MT, (g.N + NT - 1) / NT);
+    // one workgroup per tile, in k_gemm's XCD-aware order
+    const dim3 grid((unsigned)(((g.M + MT - 1) / MT) * ((g.N + NT - 1) / NT)));
     hipLaunchKernelGGL((k_gemm<MT, NT, WM, WN, ALOAD, EPI>), grid, dim3(256), 0, st, g);
     return hipGetLastError();
 }
@@ -2177,7 +2189,7 @@ void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *bloc
     }
     unsigned gx, gy;
     gemm_grid(g, aload, epi, &gx, &gy);
-    *grid = dim3(gx, gy);
+    *grid = dim3(gx * gy);  // the 1-D launch of k_gemm's tiles
     *block = dim3(256);
 }
 
