@@ -107,7 +107,12 @@ __device__ __forceinline__ float gelu_erf(float v) {
     p = fmaf(p, u, 0.12783743829594208f);
     // exp(-t^2) = 2^(v^2 * (-log2(e) / 2)); q = erfc(t) / 2
     const float q = u * p * __builtin_amdgcn_exp2f(v * v * -0.72134752044448170368f);
-    return fmaf(-fabsf(v), q, fmaxf(v, 0.0f));
+    // max(v, 0) as one v_max_f32: fmaxf (and every builtin the compiler
+    // recognises as a max) adds a NaN-quieting max(v, v) in front of it (a
+    // NaN in v still gives a NaN through the fma)
+    float m;
+    asm("v_max_f32 %0, 0, %1" : "=v"(m) : "v"(v));
+    return fmaf(-fabsf(v), q, m);
 }
 
 // ---------------------------------------------------------------------------
@@ -614,9 +619,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     __shared__ __attribute__((aligned(16))) float As1[ATILE];
     __shared__ __attribute__((aligned(16))) float Rs0[RTILE];
     __shared__ __attribute__((aligned(16))) float Rs1[RTILE];
-    // K halves swap the accumulator registers the other half finishes:
-    // [sender half][column wave][rb][tile][register pair][lane]
-    __shared__ float ksum[KS == 2 ? 2 * 4 * RB * 3 * 2 * 64 : 1];
+    // K halves swap their accumulators: [sender half][column wave][rb][tile]
+    // [lane][register]
+    __shared__ __attribute__((aligned(16))) float ksum[KS == 2 ? 2 * 4 * RB * 3 * 4 * 64 : 1];
     // row statistics: [K half * 4 + column wave][row][sum, sum of squares]
     __shared__ float rst0[4 * KS][TR][2];
     __shared__ float rst1[4 * KS][TR][2];
@@ -645,7 +650,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const bool out_wide = out_floats * 4 >= BUF_MAX_BYTES;
     const __amdgpu_buffer_rsrc_t ro_all = buf_rsrc(g.out, out_floats * 4);
     // The epilogue: with K split over two wave sets, each finishes half of the
-    // accumulator registers (columns 4q + R0 .. 4q + R0 + NR - 1 of a tile).
+    // accumulator registers (columns 4q + R0 .. 4q + R0 + NR - 1 of a tile, or
+    // rows for the unit layout), which the K exchange leaves in registers
+    // 0 .. NR - 1.
     constexpr int NR = KS == 2 ? 2 : 4;
     const int R0 = KS == 2 ? 2 * kq : 0;
     // output byte offsets: a column part per tile (out of range past the
@@ -773,18 +780,17 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             out_wide ? buf_rsrc(g.out + tbase, (out_floats - tbase) * 4) : ro_all;
         const unsigned tofs = out_wide ? 0u : (unsigned)(WIN ? (size_t)wi * HGU : (size_t)task * TR * g.ldo) * 4u;
         if constexpr (!TT) {
-            // unit layout (no LayerNorm, no residual): register r of tile t is
-            // row 4q + r, the lane's column j; one dword store per value
+            // unit layout (no LayerNorm, no residual): register rr of tile t is
+            // row 4q + R0 + rr, the lane's column j; one dword store per value
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int rr = 0; rr < NR; ++rr) {
-                    const int r = R0 + rr;
-                    const int row = rb * 16 + 4 * q + r;
+                    const int row = rb * 16 + 4 * q + R0 + rr;
                     const unsigned rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
 #pragma unroll
                     for (int t = 0; t < 3; ++t)
-                        buf_store1(ro_rs, (int)(rowo + colo[t]), pacc[rb][t][r]);
+                        buf_store1(ro_rs, (int)(rowo + colo[t]), pacc[rb][t][rr]);
                 }
             return;
         }
@@ -817,7 +823,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                 const int cl = 48 * cg + 16 * t + 4 * q + R0;
                 float v[NR], lw[NR], lb[NR], rs[NR];
 #pragma unroll
-                for (int rr = 0; rr < NR; ++rr) v[rr] = pacc[rb][t][R0 + rr];
+                for (int rr = 0; rr < NR; ++rr) v[rr] = pacc[rb][t][rr];
                 if (HAS_LN) {
                     if (NR == 4) {
                         const float4 w4 = *reinterpret_cast<const float4 *>(&prm[1][cl]);
@@ -930,25 +936,29 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         }
 
         if (KS == 2) {
-            // the two K halves' partial sums meet in LDS: each half sends the
-            // register pair the other half finishes and adds the pair it gets
+            // the two K halves' partial sums meet in LDS: each half writes its
+            // four registers of a tile as one float4 and reads back the pair it
+            // finishes, its own and the other half's, at addresses that depend
+            // on the half (indexing the registers by the half instead would
+            // cost a select per register); own + other, as before the swap
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int t = 0; t < 3; ++t)
-#pragma unroll
-                    for (int rr = 0; rr < 2; ++rr)
-                        ksum[((((kq * 4 + cg) * RB + rb) * 3 + t) * 2 + rr) * 64 + lane] =
-                            acc[rb][t][2 * (1 - kq) + rr];
+                    *reinterpret_cast<f4v *>(&ksum[((((kq * 4 + cg) * RB + rb) * 3 + t) * 64 + lane) * 4]) =
+                        acc[rb][t];
             lds_sync();
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
-#pragma unroll
-                    for (int rr = 0; rr < 2; ++rr)
-                        acc[rb][t][R0 + rr] +=
-                            ksum[(((((1 - kq) * 4 + cg) * RB + rb) * 3 + t) * 2 + rr) * 64 + lane];
+                for (int t = 0; t < 3; ++t) {
+                    const float2 own = *reinterpret_cast<const float2 *>(
+                        &ksum[((((kq * 4 + cg) * RB + rb) * 3 + t) * 64 + lane) * 4 + R0]);
+                    const float2 oth = *reinterpret_cast<const float2 *>(
+                        &ksum[(((((1 - kq) * 4 + cg) * RB + rb) * 3 + t) * 64 + lane) * 4 + R0]);
+                    acc[rb][t][0] = own.x + oth.x;
+                    acc[rb][t][1] = own.y + oth.y;
+                }
         }
 
         // the row statistics when a LayerNorm follows (single-pass, as the
@@ -964,7 +974,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                 for (int t = 0; t < 3; ++t)
 #pragma unroll
                     for (int rr = 0; rr < NR; ++rr) {
-                        const float x = acc[rb][t][R0 + rr];
+                        const float x = acc[rb][t][rr];
                         s1 += x;
                         s2 = fmaf(x, x, s2);
                     }
