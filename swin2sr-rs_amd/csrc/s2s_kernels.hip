@@ -563,20 +563,22 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Sum over the four 16-lane rows, into lanes 0-15 (lane l < 16 gets lanes l,
-// l+16, l+32, l+48; the other lanes get partial sums). v_permlane16_swap(v, 0)
-// leaves rows (v0, 0, v2, 0) in v and (v1, 0, v3, 0) in the zero operand,
-// v_permlane32_swap(w, 0) the low half of w in lanes 0-31 of w and the high
-// half in lanes 0-31 of the other (gfx950). Inline assembly: the compiler's
-// builtins for these swaps have added one result to itself instead of to the
-// other one; the s_nop covers the VALU-write-then-permlane hazard.
-__device__ __forceinline__ float xrow_sum0(float v) {
-    float z = 0.f;
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(v), "+v"(z));
-    v += z;
-    float z2 = 0.f;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(v), "+v"(z2));
-    return v + z2;
+// Two sums over the four 16-lane rows at once: lane j of row 0 (lanes 0-15)
+// gets a[j] + a[j+16] + a[j+32] + a[j+48], lane j of row 1 the same sum of b
+// (rows 2 and 3 repeat rows 0 and 1). v_permlane16_swap(a, b) leaves rows
+// (a0, b0, a2, b2) in a and (a1, b1, a3, b3) in b, so a + b holds the pair
+// sums of a in rows 0 and 2 and of b in rows 1 and 3; v_permlane32_swap(c, d)
+// with d a copy of c leaves rows (c0, c1, c0, c1) in c and (c2, c3, c2, c3) in
+// d (gfx950). The order is (x0 + x1) + (x2 + x3) for both. Inline assembly:
+// the compiler's builtins for these swaps have added one result to itself
+// instead of to the other one; the s_nop covers the VALU-write-then-permlane
+// hazard.
+__device__ __forceinline__ float xrow_sum2(float a, float b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    float c = a + b;
+    float d = c;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+    return c + d;
 }
 
 template <int KPW, int KS, int RB, int EPI>
@@ -804,9 +806,9 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             if (WIN) rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
             float rstd = 1.f, mr = 0.f;
             if (HAS_LN) {
-                float a1 = 0.f, a2 = 0.f;
+                float a1 = prst[0][row][0], a2 = prst[0][row][1];
 #pragma unroll
-                for (int c = 0; c < 4 * KS; ++c) {
+                for (int c = 1; c < 4 * KS; ++c) {
                     a1 += prst[c][row][0];
                     a2 += prst[c][row][1];
                 }
@@ -969,21 +971,18 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             // lane groups (the row's other columns in this wave)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                float s1 = 0.f, s2 = 0.f;
+                float s1 = acc[rb][0][0], s2 = acc[rb][0][0] * acc[rb][0][0];
 #pragma unroll
                 for (int t = 0; t < 3; ++t)
 #pragma unroll
-                    for (int rr = 0; rr < NR; ++rr) {
+                    for (int rr = (t == 0 ? 1 : 0); rr < NR; ++rr) {
                         const float x = acc[rb][t][rr];
                         s1 += x;
                         s2 = fmaf(x, x, s2);
                     }
-                s1 = xrow_sum0(s1);
-                s2 = xrow_sum0(s2);
-                if (q == 0) {
-                    wrst[kq * 4 + cg][rb * 16 + j][0] = s1;
-                    wrst[kq * 4 + cg][rb * 16 + j][1] = s2;
-                }
+                // row 0 of the wave holds the row's sum, row 1 its sum of squares
+                const float tot = xrow_sum2(s1, s2);
+                if (q < 2) wrst[kq * 4 + cg][rb * 16 + j][q] = tot;
             }
         }
 #pragma unroll
