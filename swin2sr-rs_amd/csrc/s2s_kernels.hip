@@ -217,8 +217,34 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         const int n = n0 + (tid >> 3) + 32 * i;
         bo[i] = n < g.N ? (n * g.ldb + kq) * 4 : -1;
     }
-    // (tap, ci) of k = k0 + kq for the chunk at k0, and the tap's shift
+    // IM2COL: each of the thread's rows as a byte offset from the resource
+    // base, and a mask of the 3x3 taps (bit 3(dy+1) + dx+1) that read inside
+    // the plane (none for rows past M); a chunk then costs an add, a bit test
+    // and a select per row instead of the bounds checks and a multiply
+    int aro[AV];
+    unsigned tmask[AV];
+    if (ALOAD == ALOAD_IM2COL) {
+#pragma unroll
+        for (int i = 0; i < AV; ++i) {
+            aro[i] = (am[i] - pb) * g.cin * 4;
+            unsigned msk = 0;
+            if (am[i] < g.M) {
+#pragma unroll
+                for (int ty = 0; ty < 3; ++ty)
+#pragma unroll
+                    for (int tx = 0; tx < 3; ++tx)
+                        if ((unsigned)(ay[i] + ty - 1) < (unsigned)g.H && (unsigned)(ax[i] + tx - 1) < (unsigned)g.W)
+                            msk |= 1u << (3 * ty + tx);
+            }
+            tmask[i] = msk;
+        }
+    }
+    // (tap, ci) of k = k0 + kq for the chunk at k0, and the tap's shift; for
+    // IM2COL also tapoff = ((dy * W + dx) * cin + ci) * 4, the byte offset of
+    // that element from its row's pixel (unchanged when ci wraps into the
+    // next tap of the same kernel row; + (W - 3) * cin * 4 into the next row)
     int tap = 0, ci = kq, dy = -1, dx = -1;
+    int tapoff = ALOAD == ALOAD_IM2COL ? ((-g.W - 1) * g.cin + kq) * 4 : 0;
     auto norm_k = [&]() __attribute__((always_inline)) {
         if (ALOAD == ALOAD_ROWS) return;
         while (ci >= g.cin) {
@@ -227,6 +253,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             if (++dx > 1) {
                 dx = -1;
                 ++dy;
+                tapoff += (g.W - 3) * g.cin * 4;
             }
         }
     };
@@ -234,19 +261,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
     auto load_chunk = [&](int k0) __attribute__((always_inline)) {
         const bool kok = k0 + kq < g.K;
-        const int shift_px = dy * g.W + dx - (ALOAD == ALOAD_IM2COL ? pb : 0);
+        // (tap <= 8 while k < K = 9 * cin; bit 31 of a tap mask is never set)
+        const int tsel = kok ? tap : 31;
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
             int off;
             if (ALOAD == ALOAD_ROWS) {
                 off = (am[i] < g.M && kok) ? ((am[i] - pb) * g.lda + k0 + kq) * 4 : BUF_OOB;
+            } else if (ALOAD == ALOAD_IM2COL) {
+                off = ((tmask[i] >> tsel) & 1u) ? aro[i] + tapoff : BUF_OOB;
             } else {
                 const int sy = ay[i] + dy, sx = ax[i] + dx;
                 const bool ok = am[i] < g.M && kok && (unsigned)sy < (unsigned)g.H &&
                                 (unsigned)sx < (unsigned)g.W;
-                // (the tap's shift carries the resource base for IM2COL)
-                const int px = ALOAD == ALOAD_IM2COL_UP2 ? (sy >> 1) * (g.W >> 1) + (sx >> 1) - pb
-                                                         : am[i] + shift_px;
+                const int px = (sy >> 1) * (g.W >> 1) + (sx >> 1) - pb;
                 off = ok ? (px * g.cin + ci) * 4 : BUF_OOB;
             }
             ra[i] = buf_load4(ra_rs, off);
@@ -256,6 +284,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             rb[i] = buf_load4(rb_rs, (bo[i] >= 0 && kok) ? bo[i] + k0 * 4 : BUF_OOB);
         // on to the next chunk's k
         ci += KC;
+        tapoff += KC * 4;
         norm_k();
     };
 
