@@ -71,6 +71,9 @@ __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int off, fl
 __device__ __forceinline__ float4 buf_load4s(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+__device__ __forceinline__ void buf_store1s(__amdgpu_buffer_rsrc_t r, int voff, int soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
+}
 __device__ __forceinline__ void buf_store4s(__amdgpu_buffer_rsrc_t r, int voff, int soff, float4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, voff, soff, 0);
 }
@@ -812,17 +815,22 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         const unsigned tofs = out_wide ? 0u : (unsigned)(WIN ? (size_t)wi * HGU : (size_t)task * TR * g.ldo) * 4u;
         if constexpr (!TT) {
             // unit layout (no LayerNorm, no residual): register rr of tile t is
-            // row 4q + R0 + rr, the lane's column j; one dword store per value
+            // row 16rb + 4q + R0 + rr, the lane's column j; one dword store per
+            // value. The lane's part of the offset (row 4q + R0 of the task,
+            // its column; out of range past the group) goes in the VGPR, the
+            // wave-uniform row step 16rb + rr in the SGPR offset: every row of
+            // a task lies in its window's unit, so the whole address stays in
+            // the buffer
+            const unsigned tro = tofs + (unsigned)(((task - wi * TPW) * TR + 4 * q + R0) * RSU) * 4u;
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
+            for (int t = 0; t < 3; ++t) {
+                const int vo = (int)(tro + colo[t]);
 #pragma unroll
-                for (int rr = 0; rr < NR; ++rr) {
-                    const int row = rb * 16 + 4 * q + R0 + rr;
-                    const unsigned rowo = tofs + (unsigned)(((task - wi * TPW) * TR + row) * RSU) * 4u;
+                for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int t = 0; t < 3; ++t)
-                        buf_store1(ro_rs, (int)(rowo + colo[t]), pacc[rb][t][rr]);
-                }
+                    for (int rr = 0; rr < NR; ++rr)
+                        buf_store1s(ro_rs, vo, (rb * 16 + rr) * RSU * 4, pacc[rb][t][rr]);
+            }
             return;
         }
 #pragma unroll
