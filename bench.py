@@ -57,8 +57,8 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "proj_ln_res": ("mfma", 2 * P * C * C, f * P * 3 * C),
         "fc1_gelu": ("mfma", 2 * P * Hd * C, f * P * (C + Hd)),
         "fc2_ln_res": ("mfma", 2 * P * C * Hd, f * P * (Hd + 2 * C)),
-        "conv3x3_stage": ("mfma", 2 * P * C * 9 * C, f * P * 2 * C),
-        "conv1x1_res": ("mfma", 2 * P * C * C, f * P * 3 * C),
+        # the stage close: the 3x3 conv with the 1x1 folded in, + the residual
+        "conv3x3_stage": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),
         "conv_first": ("mfma", 2 * P * C * 27, f * P * (4 + C)),
         "patch_embed_ln": ("mfma", 2 * P * C * C, f * P * 2 * C),
         "conv_after_body_res": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),

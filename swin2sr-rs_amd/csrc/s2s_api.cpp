@@ -64,7 +64,8 @@ struct BlockW {
 
 struct StageW {
     std::vector<BlockW> blocks;
-    float *conv_w = nullptr, *conv_b = nullptr, *pe_w = nullptr, *pe_b = nullptr;
+    // the stage close: its 3x3 conv with the 1x1 patch_embed conv folded in
+    float *conv_w = nullptr, *conv_b = nullptr;
 };
 
 struct ProfKey {
@@ -456,12 +457,21 @@ int s2s_ctx::stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out) {
         if (block_fwd(st.blocks[bi], hp, wp, shift, src, wk)) return -1;
         src = wk;
     }
-    GemmArgs g = conv_gemm(src, hp, wp, c, st.conv_w, st.conv_b, tmp, c, c);
-    if (gemm("conv3x3_stage", g, ALOAD_IM2COL, EPI_STORE)) return -1;
-    g = rows_gemm(tmp, c, st.pe_w, c, st.pe_b, x_out, c, P, c, c);
+    // The stage close (reference src/gpu.rs:526-528: the 3x3 conv, the 1x1
+    // patch_embed conv, the stage's residual) as one conv launch: the two
+    // convolutions are folded into one at upload, and the residual is its
+    // epilogue, element by element, so it may write over x_in; it goes through
+    // tmp only when the conv would read the plane it writes (no blocks).
+    float *dst = src == x_out ? tmp : x_out;
+    GemmArgs g = conv_gemm(src, hp, wp, c, st.conv_w, st.conv_b, dst, c, c);
     g.res = x_in;
     g.ldr = c;
-    return gemm("conv1x1_res", g, ALOAD_ROWS, EPI_RES);
+    if (gemm("conv3x3_stage", g, ALOAD_IM2COL, EPI_RES)) return -1;
+    if (dst != x_out) {
+        const hipError_t e = hipMemcpyAsync(x_out, dst, (size_t)P * c * 4, hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess) return fail(hip_msg("hipMemcpyAsync(stage)", e));
+    }
+    return 0;
 }
 
 int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
@@ -742,10 +752,38 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
     for (int s = 0; !rc && s < A.n_stages; ++s) {
         StageW &st = ctx->stages[s];
         const std::string sp = "layers." + std::to_string(s) + ".";
-        rc = rc || upconv(sp + "conv.weight", C, C, &st.conv_w, nullptr);
-        rc = rc || up(sp + "conv.bias", {C}, &st.conv_b);
-        rc = rc || up(sp + "patch_embed.proj.weight", {C, C, 1, 1}, &st.pe_w);
-        rc = rc || up(sp + "patch_embed.proj.bias", {C}, &st.pe_b);
+        {
+            // The stage close is the 3x3 conv, then the 1x1 patch_embed conv,
+            // then the stage residual, with nothing between the two
+            // convolutions (reference src/gpu.rs:526-528, src/cpu.rs:1577-1581):
+            // one linear map, uploaded as a single 3x3 conv with
+            //   W[o][i][t] = sum_m P[o][m] W3[m][i][t],
+            //   b[o]       = sum_m P[o][m] b3[m] + b1[o],
+            // accumulated in double and rounded once.
+            const s2s_tensor *w3, *b3, *w1, *b1;
+            rc = rc || ts.get(sp + "conv.weight", {C, C, 3, 3}, &w3);
+            rc = rc || ts.get(sp + "conv.bias", {C}, &b3);
+            rc = rc || ts.get(sp + "patch_embed.proj.weight", {C, C, 1, 1}, &w1);
+            rc = rc || ts.get(sp + "patch_embed.proj.bias", {C}, &b1);
+            if (rc) break;
+            const size_t kk = (size_t)C * 9;
+            std::vector<float> wf((size_t)C * kk), bf(C);
+            std::vector<double> acc(kk);
+            for (int o = 0; o < C; ++o) {
+                std::fill(acc.begin(), acc.end(), 0.0);
+                double ab = b1->data[o];
+                for (int m = 0; m < C; ++m) {
+                    const double pm = w1->data[(size_t)o * C + m];
+                    ab += pm * b3->data[m];
+                    const float *w3m = w3->data + (size_t)m * kk;
+                    for (size_t k = 0; k < kk; ++k) acc[k] += pm * w3m[k];
+                }
+                for (size_t k = 0; k < kk; ++k) wf[(size_t)o * kk + k] = (float)acc[k];
+                bf[o] = (float)ab;
+            }
+            rc = rc || ctx->upload(conv_relayout(wf.data(), C, C, nullptr), &st.conv_w);
+            rc = rc || ctx->upload(bf, &st.conv_b);
+        }
         st.blocks.resize(A.depths[s]);
         for (int b = 0; !rc && b < A.depths[s]; ++b) {
             BlockW &bw = st.blocks[b];

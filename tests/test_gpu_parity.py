@@ -235,6 +235,17 @@ def test_forward_small_model(pkg, orc, h, w):
     assert d8 <= 1
 
 
+def test_forward_stage_without_blocks(pkg, orc):
+    """A stage with no Swin blocks: its close (the folded 3x3 + 1x1 conv and the
+    stage residual) reads the plane it must write, so it goes through scratch."""
+    M = pkg.model
+    arch = M.Arch(upsampler="pixelshuffle", scale=2, embed=24, heads=2, depths=[0, 2, 0])
+    want, got, got2 = _forward_pair(pkg, orc, arch, 5, 21, 19, perturb=True)
+    assert np.array_equal(got, got2)
+    err = np.abs(got - want).max()
+    assert err < 1e-4, err
+
+
 @pytest.mark.parametrize("h,w,scale", [(37, 29, 4), (48, 72, 2)])
 def test_forward_classical(pkg, orc, h, w, scale):
     M = pkg.model
