@@ -34,6 +34,8 @@ import __graft_entry__ as ge  # noqa: E402
 METRIC = "output Mpix/s classical-x4 256²→1024² fp32 @1 GPU; % MFMA / HBM roofline"
 MFMA_FP32_PEAK = 157.3e12   # MI355X dense fp32 matrix, FLOP/s (AMD spec)
 HBM_PEAK = 8.0e12           # MI355X HBM3E, B/s (AMD spec)
+VALU_FP32_PEAK = 78.6e12    # MI355X fp32 vector FMA (256 CUs x 4 SIMDs x 16 lanes x 2 x 2.4 GHz)
+FLOP_PEAK = {"mfma": MFMA_FP32_PEAK, "valu": VALU_FP32_PEAK}
 
 
 def log(*a):
@@ -67,6 +69,10 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "pad_input": ("hbm", 0, f * (3 * h * w + 4 * P)),
         "conv_last_finish": ("hbm", 2 * (h * s) * (w * s) * 3 * 9 * F,
                              f * ((hp * s) * (wp * s) * F + 3 * h * s * w * s)),
+        # the last octave and conv_last composed: 12 outputs from a 5x5xF
+        # footprint per input pixel whose outputs survive the crop (VALU)
+        "up_last": ("valu", 2 * (h * s // 2) * (w * s // 2) * 12 * 25 * F,
+                    f * ((hp * s // 2) * (wp * s // 2) * F + 3 * h * s * w * s)),
     }
     px = P
     for o in range(arch.octaves):
@@ -126,15 +132,15 @@ def roofline_of(work, kernel, ms, n, traffic=True):
     """The roofline object for `kernel` from its summed event time over n launches."""
     bound, fl, by = work[kernel]
     avg_s = ms / n / 1e3
-    if bound == "mfma":
-        achieved, peak, unit = fl / avg_s / 1e12, MFMA_FP32_PEAK / 1e12, "TFLOP/s"
+    if bound in FLOP_PEAK:
+        achieved, peak, unit = fl / avg_s / 1e12, FLOP_PEAK[bound] / 1e12, "TFLOP/s"
     else:
         achieved, peak, unit = by / avg_s / 1e9, HBM_PEAK / 1e9, "GB/s"
     return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4),
             "traffic": traffic_from_profiles(kernel) if traffic else None,
             "kernel": kernel, "avg_ms": round(avg_s * 1e3, 4), "launches": n,
-            "work_per_launch": fl if bound == "mfma" else by}
+            "work_per_launch": fl if bound in FLOP_PEAK else by}
 
 
 def kernel_table(be, work, steps, rows=None):
@@ -147,13 +153,13 @@ def kernel_table(be, work, steps, rows=None):
     for k, (ms, n) in sorted(rows.items(), key=lambda kv: -kv[1][0]):
         bound, fl, by = work[k]
         avg = ms / n
-        rate = (fl / (avg / 1e3) / 1e12) if bound == "mfma" else (by / (avg / 1e3) / 1e9)
-        unit = "TFLOP/s" if bound == "mfma" else "GB/s"
+        rate = (fl / (avg / 1e3) / 1e12) if bound in FLOP_PEAK else (by / (avg / 1e3) / 1e9)
+        unit = "TFLOP/s" if bound in FLOP_PEAK else "GB/s"
         hbm = by / (avg / 1e3) / 1e9
         log(f"  {k:24s} {n:5d} launches {avg:9.4f} ms avg {100 * ms / total_dev:5.1f}% "
             f"{rate:9.2f} {unit}  ({hbm:7.1f} GB/s algorithmic)")
         table[k] = {"launches": n, "avg_ms": round(avg, 4), "rate": round(rate, 2), "unit": unit,
-                    "frac": round(rate / (MFMA_FP32_PEAK / 1e12 if bound == "mfma" else HBM_PEAK / 1e9), 4),
+                    "frac": round(rate / (FLOP_PEAK[bound] / 1e12 if bound in FLOP_PEAK else HBM_PEAK / 1e9), 4),
                     "algorithmic_GBps": round(hbm, 1)}
     dom = max(rows, key=lambda k: rows[k][0])
     roofline = roofline_of(work, dom, *rows[dom])

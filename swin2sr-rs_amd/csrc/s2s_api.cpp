@@ -104,8 +104,12 @@ struct s2s_ctx {
     std::vector<StageW> stages;
     float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C]
     std::vector<float *> up_w, up_b;           // octave convs, shuffle-permuted [4F][9*F]
-    bool last_slabs = false;                   // the last octave writes 8-channel slabs
     float *last_w = nullptr, *last_b = nullptr;  // conv_last [9][F][3]
+    // pixelshuffle: the last octave's conv and conv_last composed (k_up_last):
+    // interior weights [25][F][12] and bias [12], edge variants [4][12][25][F]
+    // and [4][12]; the last octave's plane is then never materialised
+    bool fuse_last = false;
+    float *ul_w = nullptr, *ul_b = nullptr, *ul_we = nullptr, *ul_be = nullptr;
     // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [3][9*F], conv_after_aux [F][9*4]
     float *bc_w = nullptr, *bc_b = nullptr, *ax_w = nullptr, *ax_b = nullptr;
     float *caa_w = nullptr, *caa_b = nullptr;
@@ -268,7 +272,7 @@ int s2s_ctx::plan_image(int h, int w) {
     std::vector<size_t> planes;
     if (arch.upsampler == S2S_PIXELSHUFFLE || arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
         size_t px = P;
-        for (int o_ = 0; o_ <= octaves; ++o_, px *= 4) planes.push_back(px);
+        for (int o_ = 0; o_ <= octaves - (fuse_last ? 1 : 0); ++o_, px *= 4) planes.push_back(px);
     } else if (arch.upsampler == S2S_NEAREST_CONV) {
         planes = {P, 4 * P, 16 * P, 16 * P};
     }
@@ -514,9 +518,9 @@ int s2s_ctx::head(int h, int w, float *d_out) {
     const int P = hp * wp;
     const int oh = h * s, ow = w * s;
     GemmArgs g{};
-    auto last = [&](const float *f, int H, int W, int chunk8) {
+    auto last = [&](const float *f, int H, int W) {
         return run("conv_last_finish", conv_last_grid(oh, ow), dim3(256), [&] {
-            return launch_conv_last_finish(f, last_w, last_b, d_out, H, W, feat, chunk8, oh, ow,
+            return launch_conv_last_finish(f, last_w, last_b, d_out, H, W, feat, oh, ow,
                                            arch.img_range, arch.mean, stream);
         });
     };
@@ -547,18 +551,21 @@ int s2s_ctx::head(int h, int w, float *d_out) {
                 return -1;
         }
         int H = hp, W = wp;
-        const bool slabs = last_slabs;
-        for (int oc = 0; oc < octaves; ++oc) {
+        for (int oc = 0; oc < octaves - (fuse_last ? 1 : 0); ++oc) {
             g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
             g.feat = feat;
             if (aux && oc == octaves - 1) g.res = bicf;  // + the bicubic branch
-            g.chunk8 = oc == octaves - 1 && slabs;  // (weights uploaded in slab order)
             const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
             if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
             H *= 2;
             W *= 2;
         }
-        return last(fplanes[octaves], H, W, slabs);
+        if (fuse_last)
+            return run("up_last", up_last_grid(oh, ow), dim3(256), [&] {
+                return launch_up_last(fplanes[octaves - 1], ul_w, ul_b, ul_we, ul_be, d_out, H, W,
+                                      feat, oh, ow, arch.img_range, arch.mean, stream);
+            });
+        return last(fplanes[octaves], H, W);
     }
     case S2S_PIXELSHUFFLE_DIRECT: {
         // one conv to 3*s^2 channels, stored through pixel_shuffle(s) straight
@@ -585,7 +592,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
         g = conv_gemm(fplanes[2], 4 * hp, 4 * wp, feat, hr_w, hr_b, fplanes[3], feat, feat);
         g.slope = 0.2f;
         if (gemm("conv_hr", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
-        return last(fplanes[3], 4 * hp, 4 * wp, 0);
+        return last(fplanes[3], 4 * hp, 4 * wp);
     }
     default:
         return fail("unknown upsampler " + std::to_string(arch.upsampler));
@@ -654,16 +661,60 @@ std::vector<int> shuffle_perm(int feat) {
     return p;
 }
 
-// The last octave's order when its plane is stored in 8-channel slabs:
-// co = 4ch + 2dy + dx -> row (ch/8*4 + 2dy+dx)*8 + ch%8, so a 32-column tile
-// is one slab's 8 channels at the 4 sub-pixels.
-std::vector<int> slab_perm(int feat) {
-    std::vector<int> p(4 * feat);
-    for (int co = 0; co < 4 * feat; ++co) {
-        const int ch = co / 4, q = co % 4;
-        p[co] = ((ch / 8) * 4 + q) * 8 + ch % 8;
+// The last pixel-shuffle octave (conv3x3 F -> 4F, PixelShuffle(2); Wo, bo) and
+// conv_last (conv3x3 F -> 3; Wl, bl) composed into one linear map from the
+// octave's input plane (reference src/gpu.rs:601-623). Output (2y + sy,
+// 2x + sx), channel k (s = (2 sy + sx) * 3 + k) reads conv_last's tap (ky, kx)
+// at shuffled position (2y + sy + ky - 1, ...), which is channel
+// 4c + 2 dy' + dx' of the octave's pixel (y + fy, ...), u = sy + ky - 1,
+// fy = floor(u / 2), dy' = u - 2 fy; that in turn reads input pixel
+// (y + fy + ty - 1, ...): offsets -2..2, a 5 x 5 footprint. Variant (ey, ex)
+// drops conv_last's kernel row 0 for sy = 0 (ey) and column 0 for sx = 0 (ex):
+// the taps that fall on conv_last's zero padding at output row 0 / column 0.
+// Accumulated in double, rounded once. wi [25][F][12], bi [12] (variant 0);
+// we [4][12][25][F], be [4][12].
+void compose_up_last(const float *Wo, const float *bo, const float *Wl, const float *bl, int F,
+                     std::vector<float> &wi, std::vector<float> &bi, std::vector<float> &we,
+                     std::vector<float> &be) {
+    std::vector<double> W((size_t)4 * 12 * 25 * F, 0.0), B(4 * 12, 0.0);
+    for (int var = 0; var < 4; ++var) {
+        const bool ey = var >> 1, ex = var & 1;
+        for (int sy = 0; sy < 2; ++sy)
+            for (int sx = 0; sx < 2; ++sx)
+                for (int k = 0; k < 3; ++k) {
+                    const int s = (2 * sy + sx) * 3 + k;
+                    double b = bl[k];
+                    double *w = &W[(size_t)(var * 12 + s) * 25 * F];
+                    for (int ky = 0; ky < 3; ++ky)
+                        for (int kx = 0; kx < 3; ++kx) {
+                            if ((ey && sy == 0 && ky == 0) || (ex && sx == 0 && kx == 0)) continue;
+                            const int u = sy + ky - 1, v = sx + kx - 1;
+                            const int fy = (u + 2) / 2 - 1, fx = (v + 2) / 2 - 1;
+                            const int dyp = u - 2 * fy, dxp = v - 2 * fx;
+                            for (int c = 0; c < F; ++c) {
+                                const double wl = Wl[(((size_t)k * F + c) * 3 + ky) * 3 + kx];
+                                const int co = 4 * c + 2 * dyp + dxp;
+                                b += wl * bo[co];
+                                for (int ci = 0; ci < F; ++ci)
+                                    for (int ty = 0; ty < 3; ++ty)
+                                        for (int tx = 0; tx < 3; ++tx) {
+                                            const int tap = (fy + ty + 1) * 5 + (fx + tx + 1);
+                                            w[(size_t)tap * F + ci] +=
+                                                wl * Wo[(((size_t)co * F + ci) * 3 + ty) * 3 + tx];
+                                        }
+                            }
+                        }
+                    B[var * 12 + s] = b;
+                }
     }
-    return p;
+    wi.assign((size_t)25 * F * 12, 0.f);
+    for (int s = 0; s < 12; ++s)
+        for (int tap = 0; tap < 25; ++tap)
+            for (int ci = 0; ci < F; ++ci)
+                wi[((size_t)tap * F + ci) * 12 + s] = (float)W[((size_t)s * 25 + tap) * F + ci];
+    bi.assign(B.begin(), B.begin() + 12);
+    we.assign(W.begin(), W.end());
+    be.assign(B.begin(), B.end());
 }
 
 }  // namespace
@@ -894,11 +945,10 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             ctx->octaves = oct;
             rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
-            const std::vector<int> perm = shuffle_perm(F), sperm = slab_perm(F);
-            // the last octave's plane goes to conv_last in 8-channel slabs (not
-            // with the bicubic branch: that residual is the same buffer, updated
-            // in place, so each value must land where it was read)
-            ctx->last_slabs = F % 8 == 0 && A.upsampler != S2S_PIXELSHUFFLE_AUX;
+            const std::vector<int> perm = shuffle_perm(F);
+            // the plain pixel-shuffle head composes its last octave with
+            // conv_last (not with the bicubic branch, which is added between)
+            ctx->fuse_last = A.upsampler == S2S_PIXELSHUFFLE && F % 8 == 0;
             for (int o = 0; !rc && o < oct; ++o) {
                 const s2s_tensor *uw, *ub;
                 const std::string base = "upsample." + std::to_string(2 * o);
@@ -907,13 +957,26 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 if (rc) break;
                 float *dw, *db;
                 std::vector<float> bb(4 * F);
-                const std::vector<int> &pm = (ctx->last_slabs && o == oct - 1) ? sperm : perm;
-                for (int co = 0; co < 4 * F; ++co) bb[pm[co]] = ub->data[co];
-                rc = ctx->upload(conv_relayout(uw->data, 4 * F, F, &pm), &dw) || ctx->upload(bb, &db);
+                for (int co = 0; co < 4 * F; ++co) bb[perm[co]] = ub->data[co];
+                rc = ctx->upload(conv_relayout(uw->data, 4 * F, F, &perm), &dw) || ctx->upload(bb, &db);
                 ctx->up_w.push_back(dw);
                 ctx->up_b.push_back(db);
             }
             rc = rc || conv_last(F);
+            if (!rc && ctx->fuse_last) {
+                const s2s_tensor *uw, *ub, *lw, *lb;
+                const std::string base = "upsample." + std::to_string(2 * (oct - 1));
+                rc = rc || ts.get(base + ".weight", {4 * F, F, 3, 3}, &uw);
+                rc = rc || ts.get(base + ".bias", {4 * F}, &ub);
+                rc = rc || ts.get("conv_last.weight", {3, F, 3, 3}, &lw);
+                rc = rc || ts.get("conv_last.bias", {3}, &lb);
+                if (!rc) {
+                    std::vector<float> wi, bi, we, be;
+                    compose_up_last(uw->data, ub->data, lw->data, lb->data, F, wi, bi, we, be);
+                    rc = ctx->upload(wi, &ctx->ul_w) || ctx->upload(bi, &ctx->ul_b) ||
+                         ctx->upload(we, &ctx->ul_we) || ctx->upload(be, &ctx->ul_be);
+                }
+            }
             if (A.upsampler == S2S_PIXELSHUFFLE_AUX) {
                 rc = rc || upconv("conv_bicubic.weight", F, 3, &ctx->bc_w, nullptr);
                 rc = rc || up("conv_bicubic.bias", {F}, &ctx->bc_b);

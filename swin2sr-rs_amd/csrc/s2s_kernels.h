@@ -59,11 +59,6 @@ struct GemmArgs {
     const float *ln_w, *ln_b;
     float slope;
     int feat;  // EPI_SHUFFLE: output channels (N = 4*feat)
-    // EPI_SHUFFLE: store the 2H x 2W plane in 8-channel slabs ([feat/8][P][8],
-    // the layout conv_last reads) instead of channel-last [P][feat], from
-    // weights in the slab column order (ch/8*4 + 2dy+dx)*8 + ch%8; a residual
-    // is still read channel-last
-    int chunk8;
     // EPI_QKV_WIN: the plane is H x W, the block's shift, heads of head_dim
     // hd (N = 3 * heads * hd)
     int shift, heads, hd;
@@ -131,11 +126,19 @@ hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, i
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,
                             float *out, int P, int C, hipStream_t st);
 dim3 conv_last_grid(int oh, int ow);
-// `in` is the H x W x feat plane, channel-last, or in 8-channel slabs
-// [feat/8][H*W][8] when chunk8 is set (EPI_SHUFFLE's chunk8 layout).
+// `in` is the H x W x feat plane, channel-last.
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
-                                   float *out, int H, int W, int feat, int chunk8, int oh, int ow,
+                                   float *out, int H, int W, int feat, int oh, int ow,
                                    float img_range, const float *mean, hipStream_t st);
+// The classical head's last pixel-shuffle octave + conv_last + finish, composed:
+// `in` is the octave's H x W x feat input plane (channel-last), `wt` the
+// composed interior weights [25][feat][12] and `bias` [12], `wedge` the four
+// edge variants [4][12][25][feat] and `bedge` [4][12]; out is [3][oh][ow].
+// Two launches (the interior, then the top row and left column).
+dim3 up_last_grid(int oh, int ow);
+hipError_t launch_up_last(const float *in, const float *wt, const float *bias, const float *wedge,
+                          const float *bedge, float *out, int H, int W, int feat, int oh, int ow,
+                          float img_range, const float *mean, hipStream_t st);
 // torch's bicubic resize (a = -0.75, align_corners = False, edge clamp) of a
 // channel-last [h*w][4] plane to [oh*ow][4] (channel 3 stays 0).
 hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,

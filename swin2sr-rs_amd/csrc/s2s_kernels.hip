@@ -405,36 +405,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
     if constexpr (EPI == EPI_SHUFFLE) {
         // pixel_shuffle(2) store: n is the permuted output channel
-        // (2dy+dx)*feat + ch (in slabs: (ch/8*4 + 2dy+dx)*8 + ch%8), m a pixel
-        // (y, x) of the H x W plane; the value lands at pixel (2y + dy, 2x + dx)
-        // of the 2H x 2W plane.
+        // (2dy+dx)*feat + ch, m a pixel (y, x) of the H x W plane; the value
+        // lands at pixel (2y + dy, 2x + dx) of the channel-last 2H x 2W plane.
         // Per column: the sub-pixel offset and channel; per row: the pixel
-        // (one division per row tile, the rest by carrying x past W). The
-        // stored offset is pixel * pstride + cterm: channel-last (pstride =
-        // feat, cterm = channel) or in 8-channel slabs (pstride = 8, cterm =
-        // slab * plane * 8 + channel % 8).
-        int qoff[WTN], chn[WTN], cterm[WTN];
+        // (one division per row tile, the rest by carrying x past W).
+        int qoff[WTN], chn[WTN];
         float bvs[WTN];
-        const size_t plane2 = (size_t)4 * g.H * g.W;
-        const int pstride = g.chunk8 ? 8 : g.feat;
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
             const int n = n0 + (wn * WTN + j) * 32 + lr;
-            // column n: channel-last, (sub-pixel q)*feat + channel; in slabs,
-            // (slab*4 + q)*8 + channel%8, so 32 columns are one slab's 8
-            // channels at the 4 sub-pixels: two 64-byte runs per store
-            int q, ch;
-            if (g.chunk8) {
-                q = (n >> 3) & 3;
-                ch = ((n >> 5) << 3) + (n & 7);
-            } else {
-                q = n / g.feat;
-                ch = n - q * g.feat;
-            }
+            const int q = n / g.feat;
+            const int ch = n - q * g.feat;
             chn[j] = n < g.N ? ch : -1;
             qoff[j] = (q >> 1) * (2 * g.W) + (q & 1);
             bvs[j] = (n < g.N && g.bias) ? g.bias[n] : 0.f;
-            cterm[j] = g.chunk8 ? (int)((ch >> 3) * plane2 * 8) + (ch & 7) : ch;
         }
 #pragma unroll
         for (int i = 0; i < WTM; ++i) {
@@ -457,7 +441,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                     const size_t px = (size_t)(pbase + qoff[j]);
                     float v = acc[i][j][r] + bvs[j];
                     if (g.res) v += g.res[px * g.feat + chn[j]];
-                    g.out[px * pstride + cterm[j]] = v;
+                    g.out[px * g.feat + chn[j]] = v;
                 }
             }
         }
@@ -1737,7 +1721,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
                                                              const float *__restrict__ wt,
                                                              const float *__restrict__ bias,
                                                              float *__restrict__ out, int H, int W,
-                                                             int feat, int chunk8, int oh, int ow,
+                                                             int feat, int oh, int ow,
                                                              float inv_range, float m0, float m1,
                                                              float m2) {
     constexpr int TH = CL_ROWS + 2, TW = CL_COLS + 2;
@@ -1755,16 +1739,11 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
 
     // this thread's halo elements: (pixel p, float4 q) = divmod(tid + 256u, Q),
     // out-of-plane taps (the zero padding) and elements past the halo read zero.
-    // In 8-channel slabs a chunk is one slab: a halo row is one contiguous run
-    // (whole cache lines), where channel-last reads 32 of every pixel's 256
-    // bytes per chunk and the lines come back from memory once per chunk.
     // Offsets are taken from the tile's first halo row (a resource per chunk
     // based there), so they stay small whatever the size of the plane.
-    const int pstride = chunk8 ? CL_CC : feat;
-    const size_t cstep = chunk8 ? (size_t)H * W * CL_CC : CL_CC;  // floats per chunk
     const int ybase = max(y0 - 1, 0);
-    const size_t pbase = (size_t)ybase * W * pstride;              // floats
-    const size_t cfloats = chunk8 ? (size_t)H * W * CL_CC : (size_t)H * W * feat;
+    const size_t pbase = (size_t)ybase * W * feat;  // floats
+    const size_t cfloats = (size_t)H * W * feat;
     int eoff[NLD];
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
@@ -1772,7 +1751,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
         const int p = i / Q, q = i - p * Q;
         const int sy = y0 - 1 + p / TW, sx = x0 - 1 + p % TW;
         const bool ok = i < NV && sy >= 0 && sy < H && sx >= 0 && sx < W;
-        eoff[u] = ok ? (((sy - ybase) * W + sx) * pstride + 4 * q) * 4 : BUF_OOB;
+        eoff[u] = ok ? (((sy - ybase) * W + sx) * feat + 4 * q) * 4 : BUF_OOB;
     }
     // the chunk's weights [tap][ci 0..7][3] as float4s: thread t < NW4 takes
     // float4 t (tap t / 6, then 6 float4s of 8 channels x 3)
@@ -1780,10 +1759,9 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
     const int wtap = tid / (NW4 / 9), wq = tid - wtap * (NW4 / 9);
     float4 ld[NLD], lw;
     auto load = [&](int c0) __attribute__((always_inline)) {
-        // chunk c0 / CL_CC: its slab, or its 8 channels of every pixel
-        const size_t cb = (size_t)(c0 / CL_CC) * cstep + pbase;
-        const __amdgpu_buffer_rsrc_t rin =
-            buf_rsrc(in + cb, chunk8 ? (cfloats * (c0 / CL_CC + 1) - cb) * 4 : (cfloats - cb) * 4);
+        // chunk c0 / CL_CC: its 8 channels of every pixel
+        const size_t cb = (size_t)c0 + pbase;
+        const __amdgpu_buffer_rsrc_t rin = buf_rsrc(in + cb, (cfloats - cb) * 4);
 #pragma unroll
         for (int u = 0; u < NLD; ++u) ld[u] = buf_load4(rin, eoff[u]);
         lw = buf_load4(rw, tid < NW4 ? ((wtap * feat + c0) * 3 + 4 * wq) * 4 : BUF_OOB);
@@ -1856,6 +1834,201 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
         out[plane + o] = acc[rr][1] * inv_range + m1;
         out[2 * plane + o] = acc[rr][2] * inv_range + m2;
     }
+}
+
+// The classical head's last pixel-shuffle octave and conv_last, composed
+// (reference src/gpu.rs:601-623: upsample = [conv3x3 F -> 4F, PixelShuffle(2)]
+// per octave, then conv_last F -> 3; nothing non-linear between the last
+// octave's conv and conv_last, and the octave's plane feeds nothing else).
+// Output pixel (2y + sy, 2x + sx), channel k, is a linear function of the 5 x 5
+// neighbourhood of pixel (y, x) of the octave's input plane: 12 outputs (4
+// sub-pixels x 3 channels, s = (2 sy + sx) * 3 + k) per input pixel, K = 25 taps
+// x feat. The host composes the weights ([25][feat][12]) and biases; conv_last's
+// zero padding at the top row and left column is left to k_up_last_edge (the
+// bottom and right edges of the padded plane are always cropped away). Fused
+// with cpu::finish (src/cpu.rs:1925-1941) as k_conv_last_finish is.
+//
+// VALU, as k_conv_last_finish (12 outputs would fill 3/4 of an MFMA tile): a
+// workgroup owns an 8 x 64 tile of input pixels, lane = column, wave w = rows
+// 2w, 2w + 1, 24 accumulators per lane; the 12 x 68 halo and the chunk's
+// weights move through LDS 8 channels at a time, double-buffered, the weights
+// read as broadcast float4s (one tap, 4 channels, 12 outputs). Only pixels
+// whose outputs survive the crop are computed.
+#define UL_ROWS 8
+#define UL_COLS 64
+#define UL_CC 8
+__global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in,
+                                                    const float *__restrict__ wt,
+                                                    const float *__restrict__ bias,
+                                                    float *__restrict__ out, int H, int W,
+                                                    int feat, int oh, int ow, float inv_range,
+                                                    float m0, float m1, float m2) {
+    constexpr int TH = UL_ROWS + 4, TW = UL_COLS + 4;
+    constexpr int Q = UL_CC / 4;               // float4s per pixel per chunk
+    constexpr int NV = TH * TW * Q;
+    constexpr int NLD = (NV + 255) / 256;
+    constexpr int NW4 = 25 * UL_CC * 12 / 4;   // the chunk's weights, float4s
+    constexpr int NLW = (NW4 + 255) / 256;
+    constexpr int TW4 = UL_CC * 12 / 4;        // ... per tap
+    __shared__ float4 tile[2][NV];
+    __shared__ float4 wsh[2][NW4];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int x0 = blockIdx.x * UL_COLS, y0 = blockIdx.y * UL_ROWS;
+    const int nch = feat / UL_CC;
+
+    // this thread's halo elements: (pixel p, float4 q) = divmod(tid + 256u, Q);
+    // taps outside the plane (the octave conv's zero padding) and elements past
+    // the halo read zero. Offsets from the tile's first halo row (a resource
+    // per chunk based there), so they stay small whatever the plane's size.
+    const int ybase = max(y0 - 2, 0);
+    const size_t pbase = (size_t)ybase * W * feat;
+    const size_t total = (size_t)H * W * feat;
+    int eoff[NLD];
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+        const int i = tid + 256 * u;
+        const int p = i / Q, q = i - p * Q;
+        const int sy = y0 - 2 + p / TW, sx = x0 - 2 + p % TW;
+        const bool ok = i < NV && sy >= 0 && sy < H && sx >= 0 && sx < W;
+        eoff[u] = ok ? (((sy - ybase) * W + sx) * feat + 4 * q) * 4 : BUF_OOB;
+    }
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wt, (size_t)25 * feat * 12 * 4);
+    int woff[NLW];
+#pragma unroll
+    for (int v = 0; v < NLW; ++v) {
+        const int i = tid + 256 * v;
+        const int tap = i / TW4, r = i - tap * TW4;
+        woff[v] = i < NW4 ? (tap * feat * 12 + 4 * r) * 4 : BUF_OOB;
+    }
+    float4 ld[NLD], lw[NLW];
+    auto load = [&](int c0) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rin = buf_rsrc(in + pbase + c0, (total - pbase - c0) * 4);
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) ld[u] = buf_load4(rin, eoff[u]);
+#pragma unroll
+        for (int v = 0; v < NLW; ++v)
+            lw[v] = buf_load4(rw, woff[v] == BUF_OOB ? BUF_OOB : woff[v] + c0 * 12 * 4);
+    };
+    auto stash = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) {
+            const int i = tid + 256 * u;
+            if (NV % 256 == 0 || i < NV) tile[b][i] = ld[u];
+        }
+#pragma unroll
+        for (int v = 0; v < NLW; ++v) {
+            const int i = tid + 256 * v;
+            if (NW4 % 256 == 0 || i < NW4) wsh[b][i] = lw[v];
+        }
+    };
+
+    float acc[2][12];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+        for (int s = 0; s < 12; ++s) acc[rr][s] = bias[s];
+    load(0);
+    stash(0);
+    __syncthreads();
+    for (int k = 0; k < nch; ++k) {
+        if (k + 1 < nch) load((k + 1) * UL_CC);
+        const float4 *t = tile[k & 1];
+        const float4 *ws = wsh[k & 1];
+        // one tap and 4 channels at a time: their 48 weights (12 broadcast
+        // float4 reads) serve the wave's 2 rows (the tap loop stays rolled, so
+        // only one tap's operands are live)
+#pragma unroll 1
+        for (int tap = 0; tap < 25; ++tap) {
+            const int ty = tap / 5, tx = tap - 5 * (tap / 5);
+#pragma unroll
+            for (int qq = 0; qq < Q; ++qq) {
+                float wk[48];
+#pragma unroll
+                for (int f = 0; f < 12; ++f) {
+                    const float4 w4 = ws[tap * TW4 + 12 * qq + f];
+                    wk[4 * f + 0] = w4.x;
+                    wk[4 * f + 1] = w4.y;
+                    wk[4 * f + 2] = w4.z;
+                    wk[4 * f + 3] = w4.w;
+                }
+#pragma unroll
+                for (int rr = 0; rr < 2; ++rr) {
+                    const float4 v = t[((2 * wave + rr + ty) * TW + lane + tx) * Q + qq];
+                    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                        for (int s = 0; s < 12; ++s)
+                            acc[rr][s] = fmaf(wk[12 * cc + s], vv[cc], acc[rr][s]);
+                }
+            }
+        }
+        if (k + 1 < nch) stash((k + 1) & 1);
+        __syncthreads();
+    }
+    // out[k][2y + sy][2x + sx] = v / img_range + mean[k]; ow and oh are even
+    // (a multiple of the scale), so the two sub-pixel columns of a row go
+    // out as one float2
+    const int x = x0 + lane;
+    if (2 * x >= ow) return;
+    const size_t plane = (size_t)oh * ow;
+    const float mk[3] = {m0, m1, m2};
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        const int y = y0 + 2 * wave + rr;
+        if (2 * y >= oh) break;
+#pragma unroll
+        for (int sy = 0; sy < 2; ++sy)
+#pragma unroll
+            for (int kk = 0; kk < 3; ++kk) {
+                const size_t o = (size_t)kk * plane + (size_t)(2 * y + sy) * ow + 2 * x;
+                *reinterpret_cast<float2 *>(out + o) =
+                    make_float2(acc[rr][(2 * sy) * 3 + kk] * inv_range + mk[kk],
+                                acc[rr][(2 * sy + 1) * 3 + kk] * inv_range + mk[kk]);
+            }
+    }
+}
+
+// The outputs k_up_last gets wrong: row 0 (sub-pixel row 0 of input row 0)
+// and column 0 of the output, where conv_last's zero padding drops taps that
+// the interior composition includes. Each thread recomputes one of them with
+// the composition restricted to the in-plane taps (variant (ey, ex): conv_last's
+// kernel row 0 / column 0 dropped), weights [variant][12][25][feat].
+__global__ __launch_bounds__(256) void k_up_last_edge(const float *__restrict__ in,
+                                                      const float *__restrict__ wv,
+                                                      const float *__restrict__ bv,
+                                                      float *__restrict__ out, int H, int W,
+                                                      int feat, int oh, int ow, float inv_range,
+                                                      float m0, float m1, float m2) {
+    const int cw = ow >> 1, chh = oh >> 1;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (cw + chh - 1) * 12) return;
+    const int b = t / 12, s = t - 12 * b;
+    const int y = b < cw ? 0 : b - cw + 1, x = b < cw ? b : 0;
+    const int kk = s % 3, sy = (s / 3) >> 1, sx = (s / 3) & 1;
+    const int ey = y == 0 && sy == 0, ex = x == 0 && sx == 0;
+    if (!ey && !ex) return;
+    const int var = 2 * ey + ex;
+    const float *w = wv + (size_t)(var * 12 + s) * 25 * feat;
+    float acc = bv[var * 12 + s];
+    for (int tap = 0; tap < 25; ++tap) {
+        const int yy = y + tap / 5 - 2, xx = x + tap % 5 - 2;
+        if (yy < 0 || yy >= H || xx < 0 || xx >= W) continue;
+        const float *px = in + ((size_t)yy * W + xx) * feat;
+        const float *wt = w + tap * feat;
+        for (int ci = 0; ci < feat; ci += 4) {
+            const float4 a = *reinterpret_cast<const float4 *>(px + ci);
+            const float4 c = *reinterpret_cast<const float4 *>(wt + ci);
+            acc = fmaf(c.x, a.x, acc);
+            acc = fmaf(c.y, a.y, acc);
+            acc = fmaf(c.z, a.z, acc);
+            acc = fmaf(c.w, a.w, acc);
+        }
+    }
+    const float mk = kk == 0 ? m0 : (kk == 1 ? m1 : m2);
+    out[(size_t)kk * oh * ow + (size_t)(2 * y + sy) * ow + 2 * x + sx] = acc * inv_range + mk;
 }
 
 // torch's bicubic resize, as the reference's cpu::bicubic_resize computes it
@@ -2322,12 +2495,33 @@ dim3 conv_last_grid(int oh, int ow) {
 }
 
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,
-                                   float *out, int H, int W, int feat, int chunk8, int oh, int ow,
+                                   float *out, int H, int W, int feat, int oh, int ow,
                                    float img_range, const float *mean, hipStream_t st) {
     if (feat % CL_CC) return hipErrorInvalidValue;
     const dim3 grid = conv_last_grid(oh, ow);
     hipLaunchKernelGGL(k_conv_last_finish, grid, dim3(256), 0, st, in, wt, bias, out, H, W, feat,
-                       chunk8, oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+                       oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+    return hipGetLastError();
+}
+
+dim3 up_last_grid(int oh, int ow) {
+    return dim3((ow / 2 + UL_COLS - 1) / UL_COLS, (oh / 2 + UL_ROWS - 1) / UL_ROWS);
+}
+
+hipError_t launch_up_last(const float *in, const float *wt, const float *bias, const float *wedge,
+                          const float *bedge, float *out, int H, int W, int feat, int oh, int ow,
+                          float img_range, const float *mean, hipStream_t st) {
+    // the kernels' assumptions: whole 8-channel chunks, even output sides, and
+    // every computed input pixel inside the plane
+    if (feat % UL_CC || oh % 2 || ow % 2 || oh / 2 > H || ow / 2 > W) return hipErrorInvalidValue;
+    const float ir = 1.0f / img_range;
+    hipLaunchKernelGGL(k_up_last, up_last_grid(oh, ow), dim3(256), 0, st, in, wt, bias, out, H, W,
+                       feat, oh, ow, ir, mean[0], mean[1], mean[2]);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int n = (ow / 2 + oh / 2 - 1) * 12;
+    hipLaunchKernelGGL(k_up_last_edge, dim3((n + 255) / 256), dim3(256), 0, st, in, wedge, bedge,
+                       out, H, W, feat, oh, ow, ir, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
 
