@@ -1993,9 +1993,11 @@ __global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in
 
 // The outputs k_up_last gets wrong: row 0 (sub-pixel row 0 of input row 0)
 // and column 0 of the output, where conv_last's zero padding drops taps that
-// the interior composition includes. Each thread recomputes one of them with
-// the composition restricted to the in-plane taps (variant (ey, ex): conv_last's
-// kernel row 0 / column 0 dropped), weights [variant][12][25][feat].
+// the interior composition includes. They are recomputed with the composition
+// restricted to the in-plane taps (variant (ey, ex): conv_last's kernel row 0 /
+// column 0 dropped), weights [variant][12][25][feat]: one wave per (border
+// pixel, output), lane = input channel (25 taps each, coalesced), then a sum
+// over the wave. Waves whose output needs no variant leave at once.
 __global__ __launch_bounds__(256) void k_up_last_edge(const float *__restrict__ in,
                                                       const float *__restrict__ wv,
                                                       const float *__restrict__ bv,
@@ -2003,32 +2005,29 @@ __global__ __launch_bounds__(256) void k_up_last_edge(const float *__restrict__ 
                                                       int feat, int oh, int ow, float inv_range,
                                                       float m0, float m1, float m2) {
     const int cw = ow >> 1, chh = oh >> 1;
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (cw + chh - 1) * 12) return;
-    const int b = t / 12, s = t - 12 * b;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= (cw + chh - 1) * 12) return;
+    const int b = item / 12, s = item - 12 * b;
     const int y = b < cw ? 0 : b - cw + 1, x = b < cw ? b : 0;
     const int kk = s % 3, sy = (s / 3) >> 1, sx = (s / 3) & 1;
     const int ey = y == 0 && sy == 0, ex = x == 0 && sx == 0;
     if (!ey && !ex) return;
-    const int var = 2 * ey + ex;
-    const float *w = wv + (size_t)(var * 12 + s) * 25 * feat;
-    float acc = bv[var * 12 + s];
+    const float *w = wv + (size_t)((2 * ey + ex) * 12 + s) * 25 * feat;
+    float acc = 0.f;
     for (int tap = 0; tap < 25; ++tap) {
         const int yy = y + tap / 5 - 2, xx = x + tap % 5 - 2;
         if (yy < 0 || yy >= H || xx < 0 || xx >= W) continue;
         const float *px = in + ((size_t)yy * W + xx) * feat;
-        const float *wt = w + tap * feat;
-        for (int ci = 0; ci < feat; ci += 4) {
-            const float4 a = *reinterpret_cast<const float4 *>(px + ci);
-            const float4 c = *reinterpret_cast<const float4 *>(wt + ci);
-            acc = fmaf(c.x, a.x, acc);
-            acc = fmaf(c.y, a.y, acc);
-            acc = fmaf(c.z, a.z, acc);
-            acc = fmaf(c.w, a.w, acc);
-        }
+        for (int ci = lane; ci < feat; ci += 64) acc = fmaf(w[tap * feat + ci], px[ci], acc);
     }
-    const float mk = kk == 0 ? m0 : (kk == 1 ? m1 : m2);
-    out[(size_t)kk * oh * ow + (size_t)(2 * y + sy) * ow + 2 * x + sx] = acc * inv_range + mk;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) {
+        const float mk = kk == 0 ? m0 : (kk == 1 ? m1 : m2);
+        out[(size_t)kk * oh * ow + (size_t)(2 * y + sy) * ow + 2 * x + sx] =
+            (acc + bv[(2 * ey + ex) * 12 + s]) * inv_range + mk;
+    }
 }
 
 // torch's bicubic resize, as the reference's cpu::bicubic_resize computes it
@@ -2519,8 +2518,8 @@ hipError_t launch_up_last(const float *in, const float *wt, const float *bias, c
                        feat, oh, ow, ir, mean[0], mean[1], mean[2]);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int n = (ow / 2 + oh / 2 - 1) * 12;
-    hipLaunchKernelGGL(k_up_last_edge, dim3((n + 255) / 256), dim3(256), 0, st, in, wedge, bedge,
+    const int n = (ow / 2 + oh / 2 - 1) * 12;  // (border pixel, output) pairs, one wave each
+    hipLaunchKernelGGL(k_up_last_edge, dim3((n + 3) / 4), dim3(256), 0, st, in, wedge, bedge,
                        out, H, W, feat, oh, ow, ir, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
