@@ -131,8 +131,8 @@ __device__ __forceinline__ float gelu_erf(float v) {
 // of 32 staged through LDS (row stride 34 floats: 16 consecutive rows start 2
 // banks apart, so each 16-lane group of a float2 operand read covers the 32
 // banks once; a stride of 36 put rows r and r+8 on the same banks and measured
-// 0.5-1% slower), with the next chunk's global loads in flight while the
-// current chunk is multiplied.
+// 0.5-1% slower; chunks of 64 measured 8% slower), with the next chunk's
+// global loads in flight while the current chunk is multiplied.
 //
 // Within a chunk, lane half h (= lane/32) reads k = 4kk + 2h + {0,1} as one
 // float2 and feeds the two halves to two MFMAs: the A and B operands of a lane
@@ -141,7 +141,9 @@ __device__ __forceinline__ float gelu_erf(float v) {
 // ---------------------------------------------------------------------------
 
 #define KC 32
-#define LDS_S 34
+#define LDS_S (KC + 2)
+#define KQ (KC / 4)       // float4s per row of a K chunk
+#define KRP (256 / KQ)    // rows one pass of the 256 threads loads
 
 template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
@@ -188,8 +190,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     float4 ra[AV], rb[BV];
     const int nk = (g.K + KC - 1) / KC;
 
-    // Loader state. Thread t copies float4 (t & 7) of a K chunk for rows
-    // m0 + (t >> 3) + 32i of A and n0 + (t >> 3) + 32i of B, the same k in every
+    // Loader state. Thread t copies float4 t % KQ of a K chunk for rows
+    // m0 + t / KQ + KRP*i of A and n0 + t / KQ + KRP*i of B, the same k in every
     // chunk-relative slot, so everything that depends on the row (its pixel
     // y, x) is computed once, and the k-dependent part (tap, ci and the tap's
     // pixel shift) once per chunk for all of the thread's rows. Raw buffer
@@ -207,17 +209,17 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     const __amdgpu_buffer_rsrc_t ra_rs =
         buf_rsrc(g.A + (size_t)pb * arow, (afloats - (size_t)pb * arow) * 4);
     const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
-    const int kq = (tid & 7) * 4;
+    const int kq = (tid % KQ) * 4;
     int am[AV], ay[AV], ax[AV], bo[BV];
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
-        am[i] = m0 + (tid >> 3) + 32 * i;
+        am[i] = m0 + tid / KQ + KRP * i;
         ay[i] = ALOAD == ALOAD_ROWS ? 0 : am[i] / g.W;
         ax[i] = ALOAD == ALOAD_ROWS ? 0 : am[i] - ay[i] * g.W;
     }
 #pragma unroll
     for (int i = 0; i < BV; ++i) {
-        const int n = n0 + (tid >> 3) + 32 * i;
+        const int n = n0 + tid / KQ + KRP * i;
         bo[i] = n < g.N ? (n * g.ldb + kq) * 4 : -1;
     }
     // IM2COL: each of the thread's rows as a byte offset from the resource
@@ -297,12 +299,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
             const int idx = tid + i * 256;
-            *reinterpret_cast<float4 *>(&As[(idx >> 3) * LDS_S + (idx & 7) * 4]) = ra[i];
+            *reinterpret_cast<float4 *>(&As[(idx / KQ) * LDS_S + (idx % KQ) * 4]) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i) {
             const int idx = tid + i * 256;
-            *reinterpret_cast<float4 *>(&Bs[(idx >> 3) * LDS_S + (idx & 7) * 4]) = rb[i];
+            *reinterpret_cast<float4 *>(&Bs[(idx / KQ) * LDS_S + (idx % KQ) * 4]) = rb[i];
         }
         __syncthreads();
         if (kc + 1 < nk) load_chunk((kc + 1) * KC);
