@@ -98,6 +98,7 @@ struct s2s_ctx {
     uint64_t uploaded = 0;
 
     float *cf_w = nullptr, *cf_b = nullptr;  // conv_first [C][9*4]
+    // patch_embed's 1x1 conv folded into conv_first: [C][9*4], [C]; its LayerNorm
     float *pe_w = nullptr, *pe_b = nullptr, *pe_nw = nullptr, *pe_nb = nullptr;
     float *norm_w = nullptr, *norm_b = nullptr;
     float *cab_w = nullptr, *cab_b = nullptr;  // conv_after_body [C][9*C]
@@ -494,10 +495,12 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
         return -1;
     GemmArgs g = conv_gemm(in4, hp, wp, 4, cf_w, cf_b, body, c, c);
     if (gemm("conv_first", g, ALOAD_IM2COL, EPI_STORE)) return -1;
-    g = rows_gemm(body, c, pe_w, c, pe_b, cur, c, P, c, c);
+    // patch_embed (1x1 conv + LayerNorm) on conv_first's output, as a second
+    // conv of the padded input with the 1x1 folded into conv_first's weights
+    g = conv_gemm(in4, hp, wp, 4, pe_w, pe_b, cur, c, c);
     g.ln_w = pe_nw;
     g.ln_b = pe_nb;
-    if (gemm("patch_embed_ln", g, ALOAD_ROWS, EPI_LN)) return -1;
+    if (gemm("patch_embed_ln", g, ALOAD_IM2COL, EPI_LN)) return -1;
     for (int s = 0; s < arch.n_stages; ++s)
         if (stage_fwd(s, hp, wp, cur, cur)) return -1;
     if (run("layernorm", dim3((P + 15) / 16), dim3(256),
@@ -785,8 +788,34 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
 
     rc = rc || upconv("conv_first.weight", C, 3, &ctx->cf_w, nullptr);
     rc = rc || up("conv_first.bias", {C}, &ctx->cf_b);
-    rc = rc || up("patch_embed.proj.weight", {C, C, 1, 1}, &ctx->pe_w);
-    rc = rc || up("patch_embed.proj.bias", {C}, &ctx->pe_b);
+    {
+        // patch_embed's 1x1 conv (reference src/gpu.rs:474-478) reads nothing
+        // but conv_first's output, so it is uploaded folded into conv_first:
+        // W[o][i][t] = sum_m P[o][m] Wcf[m][i][t], b[o] = sum_m P[o][m] bcf[m]
+        // + bpe[o] (double accumulation, rounded once), a K = 27 conv of the
+        // padded input; conv_first itself still runs for the body's skip
+        const s2s_tensor *wcf, *bcf, *wpe, *bpe;
+        rc = rc || ts.get("conv_first.weight", {C, 3, 3, 3}, &wcf);
+        rc = rc || ts.get("conv_first.bias", {C}, &bcf);
+        rc = rc || ts.get("patch_embed.proj.weight", {C, C, 1, 1}, &wpe);
+        rc = rc || ts.get("patch_embed.proj.bias", {C}, &bpe);
+        if (!rc) {
+            std::vector<float> wf((size_t)C * 27), bf(C);
+            for (int o = 0; o < C; ++o) {
+                double acc[27] = {0.0};
+                double ab = bpe->data[o];
+                for (int m = 0; m < C; ++m) {
+                    const double pm = wpe->data[(size_t)o * C + m];
+                    ab += pm * bcf->data[m];
+                    for (int k = 0; k < 27; ++k) acc[k] += pm * wcf->data[(size_t)m * 27 + k];
+                }
+                for (int k = 0; k < 27; ++k) wf[(size_t)o * 27 + k] = (float)acc[k];
+                bf[o] = (float)ab;
+            }
+            rc = ctx->upload(conv_relayout(wf.data(), C, 3, nullptr), &ctx->pe_w) ||
+                 ctx->upload(bf, &ctx->pe_b);
+        }
+    }
     rc = rc || up("patch_embed.norm.weight", {C}, &ctx->pe_nw);
     rc = rc || up("patch_embed.norm.bias", {C}, &ctx->pe_nb);
     rc = rc || up("norm.weight", {C}, &ctx->norm_w);
