@@ -9,7 +9,7 @@
 // attention writes its output back through it.
 //
 // Dense contractions run on fp32 MFMA (fp32 in, fp32 accumulate):
-//   - k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2, the 1x1 convs), weights
+//   - k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2), weights
 //     stationary in registers, with the elementwise work fused into the
 //     epilogue: bias, erf-GELU, residual, LeakyReLU, LayerNorm (+ residual)
 //     over the full row, and the qkv store in the attention's unit layout;
@@ -18,9 +18,10 @@
 //     the head's octaves;
 //   - k_wattn (k_attention for other head shapes): S^T = K Q^T and
 //     O^T = V^T P^T per (window, head) with the softmax in registers between.
-// Memory-bound leftovers (input padding, the standalone final LayerNorm and
-// the 64->3 conv_last with the crop/denormalisation) are plain streaming
-// kernels.
+// The classical head's last octave and conv_last run composed on the VALU
+// (k_up_last, 12 outputs per input pixel); the memory-bound leftovers (input
+// padding, the standalone final LayerNorm, the other heads' 64->3 conv_last
+// with the crop/denormalisation) are plain streaming kernels.
 //
 // MFMA 32x32x2 f32 lane layout (checked on the device): lane l supplies
 // A[l%32][l/32] and B[l/32][l%32]; accumulator register r of lane l holds
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2, the 1x1 convs) with the
+// k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2) with the
 // WEIGHTS STATIONARY IN REGISTERS.
 //
 // Every token GEMM of the network has K in {C, 2C} and a weight of at most
