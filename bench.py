@@ -74,6 +74,10 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         # footprint per input pixel whose outputs survive the crop (VALU)
         "up_last": ("valu", 2 * (h * s // 2) * (w * s // 2) * 12 * 25 * F,
                     f * ((hp * s // 2) * (wp * s // 2) * F + 3 * h * s * w * s)),
+        # the last two octaves and conv_last composed: a 5x5 conv GEMM to 48
+        # outputs per pixel of the plane before them (scale 4)
+        "up2_last": ("mfma", 2 * (hp * s // 4) * (wp * s // 4) * 48 * 25 * F,
+                     f * ((hp * s // 4) * (wp * s // 4) * F + 3 * h * s * w * s)),
     }
     px = P
     for o in range(arch.octaves):

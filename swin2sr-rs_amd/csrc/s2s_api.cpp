@@ -111,6 +111,12 @@ struct s2s_ctx {
     // and [4][12]; the last octave's plane is then never materialised
     bool fuse_last = false;
     float *ul_w = nullptr, *ul_b = nullptr, *ul_we = nullptr, *ul_be = nullptr;
+    // with two or more octaves the last two compose as well (a 5x5 conv GEMM
+    // to 48 outputs, stored through pixel_shuffle(4)): [48][25F], [48],
+    // [4][48][25][F], [4][48]; the last two octaves' planes are never made
+    bool fuse2 = false;
+    float *u2_w = nullptr, *u2_b = nullptr, *u2_we = nullptr, *u2_be = nullptr;
+    int fused_octaves() const { return fuse2 ? 2 : (fuse_last ? 1 : 0); }
     // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [3][9*F], conv_after_aux [F][9*4]
     float *bc_w = nullptr, *bc_b = nullptr, *ax_w = nullptr, *ax_b = nullptr;
     float *caa_w = nullptr, *caa_b = nullptr;
@@ -273,7 +279,7 @@ int s2s_ctx::plan_image(int h, int w) {
     std::vector<size_t> planes;
     if (arch.upsampler == S2S_PIXELSHUFFLE || arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
         size_t px = P;
-        for (int o_ = 0; o_ <= octaves - (fuse_last ? 1 : 0); ++o_, px *= 4) planes.push_back(px);
+        for (int o_ = 0; o_ <= octaves - fused_octaves(); ++o_, px *= 4) planes.push_back(px);
     } else if (arch.upsampler == S2S_NEAREST_CONV) {
         planes = {P, 4 * P, 16 * P, 16 * P};
     }
@@ -554,7 +560,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
                 return -1;
         }
         int H = hp, W = wp;
-        for (int oc = 0; oc < octaves - (fuse_last ? 1 : 0); ++oc) {
+        for (int oc = 0; oc < octaves - fused_octaves(); ++oc) {
             g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
             g.feat = feat;
             if (aux && oc == octaves - 1) g.res = bicf;  // + the bicubic branch
@@ -562,6 +568,25 @@ int s2s_ctx::head(int h, int w, float *d_out) {
             if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
             H *= 2;
             W *= 2;
+        }
+        if (fuse2) {
+            // the last two octaves and conv_last: one 5x5 conv to 48 channels
+            // stored through pixel_shuffle(4), denormalised and cropped, then
+            // the input row 0 / column 0 outputs recomputed
+            g = conv_gemm(fplanes[octaves - 2], H, W, feat, u2_w, u2_b, d_out, 0, 48);
+            g.ldb = 25 * feat;
+            g.K = 25 * feat;
+            g.scale = 4;
+            g.oh = oh;
+            g.ow = ow;
+            g.img_range = arch.img_range;
+            for (int i = 0; i < 3; ++i) g.mean[i] = arch.mean[i];
+            if (gemm("up2_last", g, ALOAD_IM2COL5, EPI_SHUFFLE_FINISH)) return -1;
+            const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
+            return run("up2_last_edge", dim3((nb + 3) / 4), dim3(256), [&] {
+                return launch_up2_last_edge(fplanes[octaves - 2], u2_we, u2_be, d_out, H, W, feat,
+                                            oh, ow, arch.img_range, arch.mean, stream);
+            });
         }
         if (fuse_last)
             return run("up_last", up_last_grid(oh, ow), dim3(256), [&] {
@@ -718,6 +743,69 @@ void compose_up_last(const float *Wo, const float *bo, const float *Wl, const fl
     bi.assign(B.begin(), B.begin() + 12);
     we.assign(W.begin(), W.end());
     be.assign(B.begin(), B.end());
+}
+
+// The last two octaves and conv_last composed, from the composition of the
+// last one with conv_last (compose_up_last's edge variants ue [4][12][25][F],
+// ub [4][12]) and the octave before it (Wo, bo: conv3x3 F -> 4F,
+// PixelShuffle(2)). Output (4y + a, 4x + b), channel k is up_last's output
+// s12 = (2(a%2) + b%2)*3 + k at pixel (y1, x1) = (2y + a/2, 2x + b/2) of the
+// middle plane Z1, which reads Z1 at (y1 + oy, x1 + ox), |oy|, |ox| <= 2;
+// Z1 there is channel 4c + 2((a/2 + oy) & 1) + ((b/2 + ox) & 1) of the octave's
+// pixel (y + floor((a/2 + oy)/2), ...), which reads input pixel offsets
+// floor((a/2 + oy)/2) + ty - 1 in -2..2: a 5 x 5 footprint again. Variant
+// (ey, ex) is for input row 0 / column 0: up_last's own variant there (its
+// pixel y1 = 0 with sub-row 0, i.e. a = 0) and the Z1 positions above / left of
+// the plane dropped (o1's zero padding). Output s48 = k*16 + a*4 + b (torch's
+// pixel_shuffle(4) channel order); w48 and b48 [4][48] in
+// double, rounded once; wg [48][25*F] (variant 0, the GEMM's [n][k] with
+// k = tap*F + ci) and bg [48]; w48 [4][48][25][F].
+void compose_up2_last(const std::vector<float> &ue, const std::vector<float> &ub, const float *Wo,
+                      const float *bo, int F, std::vector<float> &wg, std::vector<float> &bg,
+                      std::vector<float> &w48, std::vector<float> &b48) {
+    const size_t kk = (size_t)25 * F;
+    std::vector<double> W((size_t)4 * 48 * kk, 0.0), B(4 * 48, 0.0);
+    for (int var = 0; var < 4; ++var) {
+        const bool ey = var >> 1, ex = var & 1;
+        for (int k = 0; k < 3; ++k)
+            for (int a = 0; a < 4; ++a)
+                for (int b = 0; b < 4; ++b) {
+                    const int s48 = k * 16 + a * 4 + b;
+                    const int s12 = (2 * (a % 2) + b % 2) * 3 + k;
+                    const int vu = 2 * (ey && a == 0) + (ex && b == 0);
+                    const float *uw = &ue[(size_t)(vu * 12 + s12) * kk];
+                    double bias = ub[vu * 12 + s12];
+                    double *w = &W[(size_t)(var * 48 + s48) * kk];
+                    for (int oy = -2; oy <= 2; ++oy)
+                        for (int ox = -2; ox <= 2; ++ox) {
+                            const int zy = a / 2 + oy, zx = b / 2 + ox;
+                            if ((ey && zy < 0) || (ex && zx < 0)) continue;
+                            const int fy = zy >= 0 ? zy / 2 : -((1 - zy) / 2);
+                            const int fx = zx >= 0 ? zx / 2 : -((1 - zx) / 2);
+                            const int dyp = zy - 2 * fy, dxp = zx - 2 * fx;
+                            const int ut = (oy + 2) * 5 + (ox + 2);
+                            for (int c = 0; c < F; ++c) {
+                                const double u = uw[(size_t)ut * F + c];
+                                if (u == 0.0) continue;
+                                const int co = 4 * c + 2 * dyp + dxp;
+                                bias += u * bo[co];
+                                for (int ci = 0; ci < F; ++ci)
+                                    for (int ty = 0; ty < 3; ++ty)
+                                        for (int tx = 0; tx < 3; ++tx) {
+                                            const int tap = (fy + ty + 1) * 5 + (fx + tx + 1);
+                                            w[(size_t)tap * F + ci] +=
+                                                u * Wo[(((size_t)co * F + ci) * 3 + ty) * 3 + tx];
+                                        }
+                            }
+                        }
+                    B[var * 48 + s48] = bias;
+                }
+    }
+    wg.assign((size_t)48 * kk, 0.f);
+    for (size_t i = 0; i < (size_t)48 * kk; ++i) wg[i] = (float)W[i];
+    bg.assign(B.begin(), B.begin() + 48);
+    w48.assign(W.begin(), W.end());
+    b48.assign(B.begin(), B.end());
 }
 
 }  // namespace
@@ -1002,8 +1090,22 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 if (!rc) {
                     std::vector<float> wi, bi, we, be;
                     compose_up_last(uw->data, ub->data, lw->data, lb->data, F, wi, bi, we, be);
-                    rc = ctx->upload(wi, &ctx->ul_w) || ctx->upload(bi, &ctx->ul_b) ||
-                         ctx->upload(we, &ctx->ul_we) || ctx->upload(be, &ctx->ul_be);
+                    if (oct >= 2 && F == 64) {  // (the edge kernel's channel count)
+                        const s2s_tensor *u0w, *u0b;
+                        const std::string b0 = "upsample." + std::to_string(2 * (oct - 2));
+                        rc = rc || ts.get(b0 + ".weight", {4 * F, F, 3, 3}, &u0w);
+                        rc = rc || ts.get(b0 + ".bias", {4 * F}, &u0b);
+                        if (!rc) {
+                            std::vector<float> wg, bg, w48, b48;
+                            compose_up2_last(we, be, u0w->data, u0b->data, F, wg, bg, w48, b48);
+                            rc = ctx->upload(wg, &ctx->u2_w) || ctx->upload(bg, &ctx->u2_b) ||
+                                 ctx->upload(w48, &ctx->u2_we) || ctx->upload(b48, &ctx->u2_be);
+                            ctx->fuse2 = true;
+                        }
+                    } else {
+                        rc = ctx->upload(wi, &ctx->ul_w) || ctx->upload(bi, &ctx->ul_b) ||
+                             ctx->upload(we, &ctx->ul_we) || ctx->upload(be, &ctx->ul_be);
+                    }
                 }
             }
             if (A.upsampler == S2S_PIXELSHUFFLE_AUX) {

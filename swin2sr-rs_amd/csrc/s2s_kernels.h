@@ -8,7 +8,8 @@
 enum {
     ALOAD_ROWS = 0,       // A[m*lda + k]
     ALOAD_IM2COL = 1,     // 3x3 im2col of the channel-last H x W plane A[H*W][cin]
-    ALOAD_IM2COL_UP2 = 2  // 3x3 im2col of the nearest-2x upsampling of A[(H/2)*(W/2)][cin]
+    ALOAD_IM2COL_UP2 = 2, // 3x3 im2col of the nearest-2x upsampling of A[(H/2)*(W/2)][cin]
+    ALOAD_IM2COL5 = 3     // 5x5 im2col of the channel-last H x W plane (k = tap*cin + ci)
 };
 enum {
     EPI_STORE = 0,   // out = acc + bias
@@ -139,6 +140,12 @@ dim3 up_last_grid(int oh, int ow);
 hipError_t launch_up_last(const float *in, const float *wt, const float *bias, const float *wedge,
                           const float *bedge, float *out, int H, int W, int feat, int oh, int ow,
                           float img_range, const float *mean, hipStream_t st);
+// The two-octave composition's edge outputs (input row 0 and column 0), after
+// the ALOAD_IM2COL5 / EPI_SHUFFLE_FINISH GEMM (feat = 64): weights [4][48][25][feat],
+// biases [4][48].
+hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float *bedge, float *out,
+                               int H, int W, int feat, int oh, int ow, float img_range,
+                               const float *mean, hipStream_t st);
 // torch's bicubic resize (a = -0.75, align_corners = False, edge clamp) of a
 // channel-last [h*w][4] plane to [oh*ow][4] (channel 3 stays 0).
 hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,

@@ -149,6 +149,9 @@ __device__ __forceinline__ float gelu_erf(float v) {
 template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     static_assert(WM * WN == 4, "four wavefronts");
+    // IM2COL and IM2COL5 share the loader: a (2 RAD + 1)^2 footprint
+    constexpr bool IC = ALOAD == ALOAD_IM2COL || ALOAD == ALOAD_IM2COL5;
+    constexpr int RAD = ALOAD == ALOAD_IM2COL5 ? 2 : 1;
     constexpr int WTM = MT / WM / 32;
     constexpr int WTN = NT / WN / 32;
     static_assert(WTM * WM * 32 == MT && WTN * WN * 32 == NT, "tile shape");
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // A through a resource based at the first row (pixel) this tile can
     // touch, so the offsets stay small whatever the size of the plane
     const int pb = ALOAD == ALOAD_ROWS     ? m0
-                   : ALOAD == ALOAD_IM2COL ? max(m0 - g.W - 1, 0)
+                   : IC ? max(m0 - RAD * (g.W + 1), 0)
                                            : max((m0 / g.W - 1) >> 1, 0) * (g.W >> 1);
     const int arow = ALOAD == ALOAD_ROWS ? g.lda : g.cin;
     const size_t afloats = ALOAD == ALOAD_ROWS ? (size_t)g.M * g.lda
@@ -223,24 +226,25 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         const int n = n0 + tid / KQ + KRP * i;
         bo[i] = n < g.N ? (n * g.ldb + kq) * 4 : -1;
     }
-    // IM2COL: each of the thread's rows as a byte offset from the resource
-    // base, and a mask of the 3x3 taps (bit 3(dy+1) + dx+1) that read inside
+    // IM2COL(5): each of the thread's rows as a byte offset from the resource
+    // base, and a mask of the taps (bit (2 RAD + 1)(dy + RAD) + dx + RAD) that read inside
     // the plane (none for rows past M); a chunk then costs an add, a bit test
     // and a select per row instead of the bounds checks and a multiply
     int aro[AV];
     unsigned tmask[AV];
-    if (ALOAD == ALOAD_IM2COL) {
+    if (IC) {
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
             aro[i] = (am[i] - pb) * g.cin * 4;
             unsigned msk = 0;
             if (am[i] < g.M) {
 #pragma unroll
-                for (int ty = 0; ty < 3; ++ty)
+                for (int ty = 0; ty < 2 * RAD + 1; ++ty)
 #pragma unroll
-                    for (int tx = 0; tx < 3; ++tx)
-                        if ((unsigned)(ay[i] + ty - 1) < (unsigned)g.H && (unsigned)(ax[i] + tx - 1) < (unsigned)g.W)
-                            msk |= 1u << (3 * ty + tx);
+                    for (int tx = 0; tx < 2 * RAD + 1; ++tx)
+                        if ((unsigned)(ay[i] + ty - RAD) < (unsigned)g.H &&
+                            (unsigned)(ax[i] + tx - RAD) < (unsigned)g.W)
+                            msk |= 1u << ((2 * RAD + 1) * ty + tx);
             }
             tmask[i] = msk;
         }
@@ -249,17 +253,17 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // IM2COL also tapoff = ((dy * W + dx) * cin + ci) * 4, the byte offset of
     // that element from its row's pixel (unchanged when ci wraps into the
     // next tap of the same kernel row; + (W - 3) * cin * 4 into the next row)
-    int tap = 0, ci = kq, dy = -1, dx = -1;
-    int tapoff = ALOAD == ALOAD_IM2COL ? ((-g.W - 1) * g.cin + kq) * 4 : 0;
+    int tap = 0, ci = kq, dy = -RAD, dx = -RAD;
+    int tapoff = IC ? ((-RAD * g.W - RAD) * g.cin + kq) * 4 : 0;
     auto norm_k = [&]() __attribute__((always_inline)) {
         if (ALOAD == ALOAD_ROWS) return;
         while (ci >= g.cin) {
             ci -= g.cin;
             ++tap;
-            if (++dx > 1) {
-                dx = -1;
+            if (++dx > RAD) {
+                dx = -RAD;
                 ++dy;
-                tapoff += (g.W - 3) * g.cin * 4;
+                tapoff += (g.W - 2 * RAD - 1) * g.cin * 4;
             }
         }
     };
@@ -267,14 +271,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
     auto load_chunk = [&](int k0) __attribute__((always_inline)) {
         const bool kok = k0 + kq < g.K;
-        // (tap <= 8 while k < K = 9 * cin; bit 31 of a tap mask is never set)
+        // (tap < (2 RAD + 1)^2 <= 25 while k < K; bit 31 of a tap mask is never set)
         const int tsel = kok ? tap : 31;
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
             int off;
             if (ALOAD == ALOAD_ROWS) {
                 off = (am[i] < g.M && kok) ? ((am[i] - pb) * g.lda + k0 + kq) * 4 : BUF_OOB;
-            } else if (ALOAD == ALOAD_IM2COL) {
+            } else if (IC) {
                 off = ((tmask[i] >> tsel) & 1u) ? aro[i] + tapoff : BUF_OOB;
             } else {
                 const int sy = ay[i] + dy, sx = ax[i] + dx;
@@ -2033,6 +2037,58 @@ __global__ __launch_bounds__(256) void k_up_last_edge(const float *__restrict__ 
     }
 }
 
+// The two-octave composition's (ALOAD_IM2COL5 + EPI_SHUFFLE_FINISH) outputs
+// at input row 0 and column 0, where the middle plane's and conv_last's zero
+// padding drop terms the interior composition includes: recomputed with the
+// variant for the pixel (ey = row 0, ex = column 0), weights [4][48][25][64].
+// One wave per border pixel, lane = input channel: the lane's 25 tap values
+// stay in registers, each of the 48 outputs is 25 coalesced weight loads and
+// 25 FMAs per lane, and the 64 partial sums of an output meet through LDS
+// (lane s adds up output s) rather than through 48 chains of lane shuffles.
+#define U2E_FEAT 64
+__global__ __launch_bounds__(256) void k_up2_last_edge(const float *__restrict__ in,
+                                                       const float *__restrict__ wv,
+                                                       const float *__restrict__ bv,
+                                                       float *__restrict__ out, int H, int W,
+                                                       int oh, int ow, float inv_range,
+                                                       float m0, float m1, float m2) {
+    __shared__ float part[4][48][U2E_FEAT + 1];
+    const int cw = (ow + 3) >> 2, chh = (oh + 3) >> 2;
+    const int wave = threadIdx.x >> 6;
+    const int b = blockIdx.x * 4 + wave;
+    const int lane = threadIdx.x & 63;
+    const bool live = b < cw + chh - 1;  // (whole wave; no early return: a barrier follows)
+    const int y = !live ? 0 : (b < cw ? 0 : b - cw + 1), x = !live ? 0 : (b < cw ? b : 0);
+    const int var = 2 * (y == 0) + (x == 0);
+    if (live) {
+        float xv[25];
+#pragma unroll
+        for (int tap = 0; tap < 25; ++tap) {
+            const int yy = y + tap / 5 - 2, xx = x + tap % 5 - 2;
+            const bool ok = yy >= 0 && yy < H && xx >= 0 && xx < W;
+            xv[tap] = ok ? in[((size_t)yy * W + xx) * U2E_FEAT + lane] : 0.f;
+        }
+        for (int s = 0; s < 48; ++s) {
+            const float *w = wv + (size_t)(var * 48 + s) * 25 * U2E_FEAT + lane;
+            float acc = 0.f;
+#pragma unroll
+            for (int tap = 0; tap < 25; ++tap) acc = fmaf(w[tap * U2E_FEAT], xv[tap], acc);
+            part[wave][s][lane] = acc;
+        }
+    }
+    __syncthreads();
+    if (live && lane < 48) {
+        const int s = lane;
+        float acc = 0.f;
+        for (int l = 0; l < U2E_FEAT; ++l) acc += part[wave][s][l];
+        const int kk = s >> 4, oy = 4 * y + ((s >> 2) & 3), ox = 4 * x + (s & 3);
+        if (oy < oh && ox < ow) {
+            const float mk = kk == 0 ? m0 : (kk == 1 ? m1 : m2);
+            out[((size_t)kk * oh + oy) * ow + ox] = (acc + bv[var * 48 + s]) * inv_range + mk;
+        }
+    }
+}
+
 // torch's bicubic resize, as the reference's cpu::bicubic_resize computes it
 // (src/cpu.rs:875-935: a = -0.75, align_corners = False, taps clamped to the
 // edge, the four horizontal products summed pairwise, then the vertical
@@ -2170,6 +2226,10 @@ static hipError_t run_gemm_e(const GemmArgs &g, int epi, hipStream_t st) {
         // the real-world head's conv_up1 / conv_up2 (+ LeakyReLU 0.2)
         if (epi == EPI_LRELU) return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
         return hipErrorInvalidValue;
+    } else if constexpr (ALOAD == ALOAD_IM2COL5) {
+        // the classical head's last two octaves and conv_last, composed
+        if (epi == EPI_SHUFFLE_FINISH) return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_SHUFFLE_FINISH>(g, st);
+        return hipErrorInvalidValue;
     } else {
         switch (epi) {
         case EPI_STORE: return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_STORE>(g, st);
@@ -2198,21 +2258,24 @@ static hipError_t run_gemm_v(const GemmArgs &g, int aload, int epi, hipStream_t 
     case ALOAD_ROWS: return run_gemm_e<MT, NT, WM, WN, ALOAD_ROWS>(g, epi, st);
     case ALOAD_IM2COL: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL>(g, epi, st);
     case ALOAD_IM2COL_UP2: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL_UP2>(g, epi, st);
+    case ALOAD_IM2COL5: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL5>(g, epi, st);
     default: return hipErrorInvalidValue;
     }
 }
 
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
     (void)g;
-    static const char *names[3][9] = {
+    static const char *names[4][9] = {
         {"gemm_rows_store", "gemm_rows_gelu", "gemm_rows_res", "gemm_rows_ln", "gemm_rows_ln_res",
          "gemm_rows_lrelu", "gemm_rows_shuffle", "gemm_rows_shuffle_finish", "gemm_rows_qkv_win"},
         {"conv3x3_store", "conv3x3_gelu", "conv3x3_res", "conv3x3_ln", "conv3x3_ln_res",
          "conv3x3_lrelu", "conv3x3_shuffle", "conv3x3_shuffle_finish", "conv3x3_qkv_win"},
         {"conv3x3_up2_store", "conv3x3_up2_gelu", "conv3x3_up2_res", "conv3x3_up2_ln",
          "conv3x3_up2_ln_res", "conv3x3_up2_lrelu", "conv3x3_up2_shuffle",
-         "conv3x3_up2_shuffle_finish", "conv3x3_up2_qkv_win"}};
-    if (aload < 0 || aload > 2 || epi < 0 || epi > 8) return "gemm_unknown";
+         "conv3x3_up2_shuffle_finish", "conv3x3_up2_qkv_win"},
+        {"conv5x5_store", "conv5x5_gelu", "conv5x5_res", "conv5x5_ln", "conv5x5_ln_res",
+         "conv5x5_lrelu", "conv5x5_shuffle", "conv5x5_shuffle_finish", "conv5x5_qkv_win"}};
+    if (aload < 0 || aload > 3 || epi < 0 || epi > 8) return "gemm_unknown";
     return names[aload][epi];
 }
 
@@ -2524,6 +2587,16 @@ hipError_t launch_up_last(const float *in, const float *wt, const float *bias, c
     const int n = (ow / 2 + oh / 2 - 1) * 12;  // (border pixel, output) pairs, one wave each
     hipLaunchKernelGGL(k_up_last_edge, dim3((n + 3) / 4), dim3(256), 0, st, in, wedge, bedge,
                        out, H, W, feat, oh, ow, ir, mean[0], mean[1], mean[2]);
+    return hipGetLastError();
+}
+
+hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float *bedge, float *out,
+                               int H, int W, int feat, int oh, int ow, float img_range,
+                               const float *mean, hipStream_t st) {
+    if (feat != U2E_FEAT || (oh + 3) / 4 > H || (ow + 3) / 4 > W) return hipErrorInvalidValue;
+    const int n = (ow + 3) / 4 + (oh + 3) / 4 - 1;  // border pixels, one wave each
+    hipLaunchKernelGGL(k_up2_last_edge, dim3((n + 3) / 4), dim3(256), 0, st, in, wedge, bedge, out,
+                       H, W, oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
 
