@@ -576,6 +576,9 @@ int s2s_ctx::head(int h, int w, float *d_out) {
             g = conv_gemm(fplanes[octaves - 2], H, W, feat, u2_w, u2_b, d_out, 0, 48);
             g.ldb = 25 * feat;
             g.K = 25 * feat;
+            // only the rows whose outputs survive the crop (the loader still
+            // reads the rows below them as the footprint needs)
+            g.M = std::min(H, (oh + 3) / 4) * W;
             g.scale = 4;
             g.oh = oh;
             g.ow = ow;
