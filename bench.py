@@ -61,9 +61,9 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "fc2_ln_res": ("mfma", 2 * P * C * Hd, f * P * (Hd + 2 * C)),
         # the stage close: the 3x3 conv with the 1x1 folded in, + the residual
         "conv3x3_stage": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),
-        "conv_first": ("mfma", 2 * P * C * 27, f * P * (4 + C)),
-        # patch_embed's 1x1 folded into conv_first: a K = 27 conv + LayerNorm
-        "patch_embed_ln": ("mfma", 2 * P * C * 27, f * P * (4 + C)),
+        # conv_first and patch_embed (its 1x1 folded into conv_first) + LayerNorm
+        # in one VALU pass: two K = 27 convs
+        "embed": ("valu", 2 * 2 * P * C * 27, f * P * (4 + 2 * C)),
         "conv_after_body_res": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),
         "conv_before_upsample": ("mfma", 2 * P * F * 9 * C, f * P * (C + F)),
         "layernorm": ("hbm", 10 * P * C, f * P * 2 * C),

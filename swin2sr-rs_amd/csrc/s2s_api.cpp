@@ -97,9 +97,10 @@ struct s2s_ctx {
     std::vector<void *> weight_allocs;
     uint64_t uploaded = 0;
 
-    float *cf_w = nullptr, *cf_b = nullptr;  // conv_first [C][9*4]
-    // patch_embed's 1x1 conv folded into conv_first: [C][9*4], [C]; its LayerNorm
-    float *pe_w = nullptr, *pe_b = nullptr, *pe_nw = nullptr, *pe_nb = nullptr;
+    float *cf_b = nullptr;                   // conv_first's bias [C]
+    // conv_first and patch_embed's 1x1 folded into it, for k_embed: weights
+    // [2][9][4][C], the folded bias [C], patch_embed's LayerNorm
+    float *emb_w = nullptr, *pe_b = nullptr, *pe_nw = nullptr, *pe_nb = nullptr;
     float *norm_w = nullptr, *norm_b = nullptr;
     float *cab_w = nullptr, *cab_b = nullptr;  // conv_after_body [C][9*C]
     std::vector<StageW> stages;
@@ -499,14 +500,13 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
     if (run("pad_input", dim3((P + 255) / 256), dim3(256),
             [&] { return launch_pad_input(d_in, in4, h, w, hp, wp, stream); }))
         return -1;
-    GemmArgs g = conv_gemm(in4, hp, wp, 4, cf_w, cf_b, body, c, c);
-    if (gemm("conv_first", g, ALOAD_IM2COL, EPI_STORE)) return -1;
-    // patch_embed (1x1 conv + LayerNorm) on conv_first's output, as a second
-    // conv of the padded input with the 1x1 folded into conv_first's weights
-    g = conv_gemm(in4, hp, wp, 4, pe_w, pe_b, cur, c, c);
-    g.ln_w = pe_nw;
-    g.ln_b = pe_nb;
-    if (gemm("patch_embed_ln", g, ALOAD_IM2COL, EPI_LN)) return -1;
+    // conv_first -> body, and patch_embed (1x1 conv + LayerNorm) on it -> cur,
+    // the 1x1 folded into a second set of conv_first weights: one pass
+    if (run("embed", dim3((P + 63) / 64), dim3(256), [&] {
+            return launch_embed(in4, emb_w, cf_b, pe_b, pe_nw, pe_nb, body, cur, hp, wp, c, stream);
+        }))
+        return -1;
+    GemmArgs g{};
     for (int s = 0; s < arch.n_stages; ++s)
         if (stage_fwd(s, hp, wp, cur, cur)) return -1;
     if (run("layernorm", dim3((P + 15) / 16), dim3(256),
@@ -877,14 +877,13 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
         return ctx->upload(conv_relayout(x->data, co, ci, perm), dst);
     };
 
-    rc = rc || upconv("conv_first.weight", C, 3, &ctx->cf_w, nullptr);
     rc = rc || up("conv_first.bias", {C}, &ctx->cf_b);
     {
         // patch_embed's 1x1 conv (reference src/gpu.rs:474-478) reads nothing
         // but conv_first's output, so it is uploaded folded into conv_first:
         // W[o][i][t] = sum_m P[o][m] Wcf[m][i][t], b[o] = sum_m P[o][m] bcf[m]
-        // + bpe[o] (double accumulation, rounded once), a K = 27 conv of the
-        // padded input; conv_first itself still runs for the body's skip
+        // + bpe[o] (double accumulation, rounded once); k_embed computes both
+        // convs (conv_first's output is the body's long skip) in one pass
         const s2s_tensor *wcf, *bcf, *wpe, *bpe;
         rc = rc || ts.get("conv_first.weight", {C, 3, 3, 3}, &wcf);
         rc = rc || ts.get("conv_first.bias", {C}, &bcf);
@@ -903,8 +902,15 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 for (int k = 0; k < 27; ++k) wf[(size_t)o * 27 + k] = (float)acc[k];
                 bf[o] = (float)ab;
             }
-            rc = ctx->upload(conv_relayout(wf.data(), C, 3, nullptr), &ctx->pe_w) ||
-                 ctx->upload(bf, &ctx->pe_b);
+            // k_embed's [set][tap][ci][C]: set 0 conv_first, set 1 the fold
+            std::vector<float> emb((size_t)2 * 9 * 4 * C, 0.f);
+            for (int o = 0; o < C; ++o)
+                for (int ci = 0; ci < 3; ++ci)
+                    for (int t = 0; t < 9; ++t) {
+                        emb[((size_t)t * 4 + ci) * C + o] = wcf->data[(size_t)o * 27 + ci * 9 + t];
+                        emb[((size_t)(9 + t) * 4 + ci) * C + o] = wf[(size_t)o * 27 + ci * 9 + t];
+                    }
+            rc = ctx->upload(emb, &ctx->emb_w) || ctx->upload(bf, &ctx->pe_b);
         }
     }
     rc = rc || up("patch_embed.norm.weight", {C}, &ctx->pe_nw);

@@ -126,6 +126,13 @@ hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, i
                             hipStream_t st);
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, const float *res,
                             float *out, int P, int C, hipStream_t st);
+// conv_first and the folded patch_embed + LayerNorm in one pass over the padded
+// input in4 [H*W][4] (channel 3 zero): wts [2][9][4][C] (set 0 conv_first, set
+// 1 patch_embed folded in; tap-major, then input channel, channels fastest),
+// biases b0, b1 [C], LayerNorm lnw, lnb [C]; body and cur are [H*W][C].
+hipError_t launch_embed(const float *in4, const float *wts, const float *b0, const float *b1,
+                        const float *lnw, const float *lnb, float *body, float *cur, int H, int W,
+                        int C, hipStream_t st);
 dim3 conv_last_grid(int oh, int ow);
 // `in` is the H x W x feat plane, channel-last.
 hipError_t launch_conv_last_finish(const float *in, const float *wt, const float *bias,

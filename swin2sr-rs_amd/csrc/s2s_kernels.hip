@@ -1709,6 +1709,125 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x,
     }
 }
 
+// conv_first (3 -> C, 3x3) and patch_embed (its 1x1 conv folded into a second
+// set of conv_first weights, then LayerNorm) in one pass over the padded
+// input (reference src/gpu.rs:474-478): both read the same 3x3 x 3 taps, and
+// at K = 27 neither fills an MFMA tile. VALU: a 16-lane group takes EMB_PX
+// consecutive pixels, lane l the channel float4s q = l + 16i (q < C/4); both
+// weight sets [set][tap][ci][C] sit in LDS as float4s over channels, each
+// read serving the group's EMB_PX pixels. The LayerNorm statistics sum the
+// lane's values and then the 16 lanes by DPP, as k_layernorm does.
+#define EMB_PX 4
+__global__ __launch_bounds__(256) void k_embed(const float *__restrict__ in4,
+                                               const float *__restrict__ wts,
+                                               const float *__restrict__ b0,
+                                               const float *__restrict__ b1,
+                                               const float *__restrict__ lnw,
+                                               const float *__restrict__ lnb,
+                                               float *__restrict__ body, float *__restrict__ cur,
+                                               int H, int W, int C) {
+    __shared__ float4 ws[2 * 9 * 3 * 48];  // [set][tap][ci < 3][C/4 <= 48]
+    const int nq = C >> 2;
+    for (int i = threadIdx.x; i < 2 * 9 * 3 * nq; i += 256) {
+        const int r = i / nq, q = i - r * nq;   // r = (set * 9 + tap) * 3 + ci
+        const int set = r / 27, tc = r - 27 * set;
+        ws[r * 48 + q] = *reinterpret_cast<const float4 *>(wts + ((size_t)set * 36 + tc + tc / 3) * C + 4 * q);
+    }
+    __syncthreads();
+    const int l = threadIdx.x & 15;
+    const int p0 = (blockIdx.x * 16 + (threadIdx.x >> 4)) * EMB_PX;
+    const int P = H * W;
+    int py[EMB_PX], px[EMB_PX];
+#pragma unroll
+    for (int p = 0; p < EMB_PX; ++p) {
+        py[p] = (p0 + p) / W;
+        px[p] = p0 + p - py[p] * W;
+    }
+    int qc[3];
+    float4 a0[EMB_PX][3], a1[EMB_PX][3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        qc[i] = min(l + 16 * i, nq - 1);
+        const float4 c0 = *reinterpret_cast<const float4 *>(b0 + 4 * qc[i]);
+        const float4 c1 = *reinterpret_cast<const float4 *>(b1 + 4 * qc[i]);
+#pragma unroll
+        for (int p = 0; p < EMB_PX; ++p) {
+            a0[p][i] = c0;
+            a1[p][i] = c1;
+        }
+    }
+#pragma unroll 1
+    for (int tap = 0; tap < 9; ++tap) {
+        const int dy = tap / 3 - 1, dx = tap - 3 * (tap / 3) - 1;
+        float4 xv[EMB_PX];
+#pragma unroll
+        for (int p = 0; p < EMB_PX; ++p) {
+            const int yy = py[p] + dy, xx = px[p] + dx;
+            const bool ok = p0 + p < P && yy >= 0 && yy < H && xx >= 0 && xx < W;
+            xv[p] = ok ? *reinterpret_cast<const float4 *>(in4 + ((size_t)yy * W + xx) * 4)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int ci = 0; ci < 3; ++ci)
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const float4 w0 = ws[(tap * 3 + ci) * 48 + qc[i]];
+                const float4 w1 = ws[((9 + tap) * 3 + ci) * 48 + qc[i]];
+#pragma unroll
+                for (int p = 0; p < EMB_PX; ++p) {
+                    const float xc = ci == 0 ? xv[p].x : (ci == 1 ? xv[p].y : xv[p].z);
+                    a0[p][i].x = fmaf(w0.x, xc, a0[p][i].x);
+                    a0[p][i].y = fmaf(w0.y, xc, a0[p][i].y);
+                    a0[p][i].z = fmaf(w0.z, xc, a0[p][i].z);
+                    a0[p][i].w = fmaf(w0.w, xc, a0[p][i].w);
+                    a1[p][i].x = fmaf(w1.x, xc, a1[p][i].x);
+                    a1[p][i].y = fmaf(w1.y, xc, a1[p][i].y);
+                    a1[p][i].z = fmaf(w1.z, xc, a1[p][i].z);
+                    a1[p][i].w = fmaf(w1.w, xc, a1[p][i].w);
+                }
+            }
+    }
+    float4 gw[3], gb[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        gw[i] = *reinterpret_cast<const float4 *>(lnw + 4 * qc[i]);
+        gb[i] = *reinterpret_cast<const float4 *>(lnb + 4 * qc[i]);
+    }
+    const float invc = 1.0f / (float)C;
+#pragma unroll
+    for (int p = 0; p < EMB_PX; ++p) {
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            if (l + 16 * i >= nq) continue;
+            const float4 v = a1[p][i];
+            s1 += (v.x + v.y) + (v.z + v.w);
+            s2 += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+        s1 = row16_sum(s1);
+        s2 = row16_sum(s2);
+        const int pix = p0 + p;
+        if (pix >= P) continue;
+        const float mean = s1 * invc;
+        float var = s2 * invc - mean * mean;
+        var = var > 0.f ? var : 0.f;
+        const float rstd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int q = l + 16 * i;
+            if (q >= nq) continue;
+            *reinterpret_cast<float4 *>(body + (size_t)pix * C + 4 * q) = a0[p][i];
+            const float4 v = a1[p][i];
+            float4 y;
+            y.x = (v.x - mean) * rstd * gw[i].x + gb[i].x;
+            y.y = (v.y - mean) * rstd * gw[i].y + gb[i].y;
+            y.z = (v.z - mean) * rstd * gw[i].z + gb[i].z;
+            y.w = (v.w - mean) * rstd * gw[i].w + gb[i].w;
+            *reinterpret_cast<float4 *>(cur + (size_t)pix * C + 4 * q) = y;
+        }
+    }
+}
+
 // conv_last (feat -> 3, 3x3, zero pad) fused with the reference's host
 // epilogue cpu::finish (src/cpu.rs:1925-1941): y/img_range + mean, cropped to
 // the unpadded output, written planar [3][oh][ow].
@@ -2597,6 +2716,16 @@ hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float
     const int n = (ow + 3) / 4 + (oh + 3) / 4 - 1;  // border pixels, one wave each
     hipLaunchKernelGGL(k_up2_last_edge, dim3((n + 3) / 4), dim3(256), 0, st, in, wedge, bedge, out,
                        H, W, oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const float *in4, const float *wts, const float *b0, const float *b1,
+                        const float *lnw, const float *lnb, float *body, float *cur, int H, int W,
+                        int C, hipStream_t st) {
+    if (C % 4 || C > 192) return hipErrorInvalidValue;
+    const int P = H * W;
+    hipLaunchKernelGGL(k_embed, dim3((P + 16 * EMB_PX - 1) / (16 * EMB_PX)), dim3(256), 0, st, in4,
+                       wts, b0, b1, lnw, lnb, body, cur, H, W, C);
     return hipGetLastError();
 }
 
