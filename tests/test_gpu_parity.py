@@ -235,6 +235,25 @@ def test_forward_small_model(pkg, orc, h, w):
     assert d8 <= 1
 
 
+@pytest.mark.parametrize("scale,h,w", [(2, 13, 21), (4, 9, 11), (8, 9, 11)])
+def test_pixelshuffle_head_compositions(pkg, orc, scale, h, w):
+    """The classical head's composed last stage at every octave count: x2 runs
+    the last octave and conv_last composed (k_up_last), x4 the last two octaves
+    (the 5x5 conv GEMM through pixel_shuffle(4)), x8 one ordinary octave before
+    those two; each with its top-row / left-column edge pass, on images small
+    enough that the edges are a large part of the output."""
+    M = pkg.model
+    arch = M.Arch(upsampler="pixelshuffle", scale=scale, embed=24, heads=2, depths=[1])
+    want, got, got2 = _forward_pair(pkg, orc, arch, 5 + scale, h, w, perturb=True)
+    assert got.shape == want.shape == (3, h * scale, w * scale)
+    assert np.array_equal(got, got2)
+    err = np.abs(got - want).max()
+    assert err < 1e-4, err
+    # the edge rows and columns on their own
+    assert np.abs(got[:, :scale, :] - want[:, :scale, :]).max() < 1e-4
+    assert np.abs(got[:, :, :scale] - want[:, :, :scale]).max() < 1e-4
+
+
 def test_forward_stage_without_blocks(pkg, orc):
     """A stage with no Swin blocks: its close (the folded 3x3 + 1x1 conv and the
     stage residual) reads the plane it must write, so it goes through scratch."""
