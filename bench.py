@@ -75,8 +75,9 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "up_last": ("valu", 2 * (h * s // 2) * (w * s // 2) * 12 * 25 * F,
                     f * ((hp * s // 2) * (wp * s // 2) * F + 3 * h * s * w * s)),
         # the last two octaves and conv_last composed: a 5x5 conv GEMM to 48
-        # outputs per pixel of the plane before them (scale 4)
-        "up2_last": ("mfma", 2 * (hp * s // 4) * (wp * s // 4) * 48 * 25 * F,
+        # outputs per pixel of the plane before them (scale 4), over the rows
+        # whose outputs survive the crop (ceil(oh / 4) of them)
+        "up2_last": ("mfma", 2 * min(hp * s // 4, -(-h * s // 4)) * (wp * s // 4) * 48 * 25 * F,
                      f * ((hp * s // 4) * (wp * s // 4) * F + 3 * h * s * w * s)),
     }
     px = P
@@ -94,6 +95,17 @@ def traffic_from_profiles(kernel):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
     return float(m.group(1)) if m else None
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(M, orc, arch, weights, sample, passes):
@@ -116,6 +128,8 @@ def cpu_baseline(M, orc, arch, weights, sample, passes):
         "value": round(out_px / dt / 1e6, 5),
         "unit": "Mpix/s",
         "cores": int(orc.lib().orc_threads()),
+        "nproc": len(os.sched_getaffinity(0)),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"median of {passes} classical-x4 {sample}x{sample}->{sample * arch.scale}x"
                    f"{sample * arch.scale} whole-image forwards (same weights and input), after a"

@@ -95,6 +95,32 @@ const char *s2s_name(void);
  * context holds on the device for the weights. */
 uint64_t s2s_uploaded_bytes(const s2s_ctx *ctx);
 
+/* `gpu::uploaded_bytes(&Weights)` (reference src/gpu.rs:792-799) as the crate
+ * calls it: from the checkpoint alone, before any backend exists
+ * (`memory_budget`, reference src/main.rs:459-471). `*bytes` is exactly what
+ * `s2s_create` will upload for this architecture and tensor set (the weights
+ * as the kernels read them - re-laid-out, folded, composed - and the CPB
+ * tables), so `s2s_uploaded_bytes` of the context it makes equals it. */
+int s2s_uploaded_bytes_for(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors,
+                           uint64_t *bytes);
+
+/* The device bytes a forward of an h x w image allocates in this context
+ * (the body plan and the image plan, the host path's device copies of the
+ * input and output included): this backend's exact counterpart of the figure
+ * the crate models as `activation_bytes` / `per_pixel_floats(gpu = true)`
+ * (reference src/backend.rs:205-212, 300-383), which it never exceeds. */
+int s2s_plan_bytes(s2s_ctx *ctx, int h, int w, uint64_t *bytes);
+
+/* A cap on the bytes of the per-image plans (`s2s_plan_bytes`); 0 = none, the
+ * default, or the value of SWIN2SR_HIP_ALLOC_LIMIT (bytes) at `s2s_create`. A
+ * forward whose plan would pass it fails like a failed allocation, with
+ * "out of memory" in the message - the error the crate's tile-halving retry
+ * keys on (`run_with_fallback` / `is_out_of_memory`, reference
+ * src/main.rs:579-662). No counterpart in the reference (the CUDA driver's
+ * own limit is the only one there): it lets a caller reserve device memory,
+ * and a test drive that retry. */
+int s2s_set_alloc_limit(s2s_ctx *ctx, uint64_t bytes);
+
 /* ---- the forward pass ---------------------------------------------------- */
 
 /* `Backend::forward` for the device (reference src/gpu.rs:741-754 and
@@ -169,6 +195,20 @@ int s2s_profile_only(s2s_ctx *ctx, const char *kernel);
  * Reference: the stage loop of src/gpu.rs:481-529 / src/cpu.rs:1516-1581. */
 int s2s_rstb_device(s2s_ctx *ctx, int stage, int hp, int wp, const float *d_in, float *d_out);
 
+/* ---- self-test ------------------------------------------------------------ */
+
+/* `gpu::selftest(&Weights)` behind `--cuda-selftest` (reference
+ * src/gpu.rs:889-1265, src/main.rs:180-192): every kernel of the forward on a
+ * small deterministic input (x[i] = sin(0.7 i + phase), the reference's
+ * generator) against the operation's definition evaluated on the host in
+ * double precision, at the reference selftest's shapes and at the
+ * checkpoint's own width and head shape; plus the checkpoint's CPB tables
+ * (the device MLP against `cpb_pre`, where the set carries both). Prints
+ * "hip selftest: N kernel/shape pairs checked ..." to stdout on success;
+ * otherwise fails naming the check, the worst element and both values.
+ * `tensors` may be NULL (no CPB check). */
+int s2s_selftest(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors);
+
 /* ---- per-op test entry points -------------------------------------------- */
 /* The device half of `gpu::selftest` (reference src/gpu.rs:889-1265): each runs
  * one kernel on host buffers (uploads, launches, downloads, synchronises) so a
@@ -181,6 +221,28 @@ int s2s_rstb_device(s2s_ctx *ctx, int stage, int hp, int wp, const float *d_in, 
  * `yx[(wi*n+t)*2+{0,1}]` = plane (y, x) read at `shift`, and
  * `reg[(wi*n+t)*2+{0,1}]` = the mask band (row, column). */
 int s2s_test_window_map(int hp, int wp, int win, int shift, int32_t *yx, uint8_t *reg);
+
+/* The production shifted-window gather (`Plan::index`, reference
+ * src/plan.rs:72-78; the CUDA build's `ss_window_gather`, cuda/swin2sr.cu:
+ * 99-135): a block's qkv GEMM exactly as the forward launches it, whose A rows
+ * are read window by window in the shifted order and stored in the window
+ * attention's unit layout - one unit per (window, head pair), 64 token rows of
+ * 6*head_dim + 2 floats: [q_h0 | q_h1 | k_h0 | k_h1 | v_h0 | v_h1 | 2 pad].
+ * `x` is `[hp*wp][c]`, `wqkv` `[3c][c]`, `bqkv` `[3c]`; `unit` receives the raw
+ * buffer (`unit_cap` >= its size in floats; unwritten padding reads NaN).
+ * Only for the head shapes that use the unit layout. */
+int s2s_test_qkv_windows(int hp, int wp, int heads, int head_dim, int shift, const float *x,
+                         const float *wqkv, const float *bqkv, float *unit, size_t unit_cap);
+
+/* The production attention half of a block: the qkv GEMM above, then the
+ * window attention with the shift mask (`Plan::region`, reference
+ * src/plan.rs:84-108) and the scatter back to the plane (`cpu::scatter`,
+ * src/cpu.rs:1200-1222), exactly as the forward launches them. `x` is
+ * `[hp*wp][c]`, `cpb` `[n*n][heads]` (the checkpoint's cpb_pre layout), `out`
+ * `[hp*wp][c]`. */
+int s2s_test_block_attention(int hp, int wp, int heads, int head_dim, int shift, const float *x,
+                             const float *wqkv, const float *bqkv, const float *logit_scale,
+                             const float *cpb, float *out);
 
 /* Window attention (reference cpu::attention, src/cpu.rs:1244-1402): `qkv` is
  * `[hp*wp][3*c]` in plane order (q | k | v per pixel), `cpb` the `[n*n][heads]`

@@ -49,6 +49,11 @@ EXPORTS = {
     "s2s_destroy": (None, [C.c_void_p]),
     "s2s_name": (C.c_char_p, []),
     "s2s_uploaded_bytes": (C.c_uint64, [C.c_void_p]),
+    "s2s_uploaded_bytes_for": (C.c_int, [C.POINTER(Arch_), C.POINTER(Tensor_), C.c_size_t,
+                                         C.POINTER(C.c_uint64)]),
+    "s2s_plan_bytes": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_uint64)]),
+    "s2s_set_alloc_limit": (C.c_int, [C.c_void_p, C.c_uint64]),
+    "s2s_selftest": (C.c_int, [C.POINTER(Arch_), C.POINTER(Tensor_), C.c_size_t]),
     "s2s_forward": (C.c_int, [C.c_void_p, C.c_int, C.c_int, FP, FP]),
     "s2s_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "s2s_aux": (C.c_int, [C.c_void_p, C.POINTER(FP), C.POINTER(C.c_size_t)]),
@@ -65,6 +70,10 @@ EXPORTS = {
     "s2s_rstb_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "s2s_test_window_map": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int32),
                                       C.POINTER(C.c_uint8)]),
+    "s2s_test_qkv_windows": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP,
+                                       FP, C.c_size_t]),
+    "s2s_test_block_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, FP, FP,
+                                           FP, FP, FP, FP]),
     "s2s_test_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, FP]),
     "s2s_test_cpb_table": (C.c_int, [C.c_int, C.c_int, FP, FP, FP, FP]),
     "s2s_test_linear": (C.c_int, [C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_int, FP, FP, FP,
@@ -173,6 +182,17 @@ class HipBackend:
     def uploaded_bytes(self) -> int:
         return int(self._lib.s2s_uploaded_bytes(self._ctx))
 
+    def plan_bytes(self, h: int, w: int) -> int:
+        """Device bytes a forward of an h x w image allocates (s2s_plan_bytes)."""
+        b = C.c_uint64()
+        check(self._lib.s2s_plan_bytes(self._ctx, h, w, C.byref(b)), "s2s_plan_bytes")
+        return int(b.value)
+
+    def set_alloc_limit(self, nbytes: int):
+        """Cap the per-image plans at `nbytes` (0 = none): past it a forward
+        fails with "out of memory"."""
+        check(self._lib.s2s_set_alloc_limit(self._ctx, int(nbytes)), "s2s_set_alloc_limit")
+
     def forward(self, h: int, w: int, input_adjusted: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(input_adjusted, dtype=np.float32)
         assert x.shape == (3, h, w), x.shape
@@ -230,7 +250,63 @@ def device_info() -> Tuple[str, str]:
     return name.value.decode(), arch.value.decode()
 
 
+def uploaded_bytes_for(arch: M.Arch, weights: Dict[str, np.ndarray]) -> int:
+    """`gpu::uploaded_bytes(&Weights)`: what s2s_create will upload, no context."""
+    lib = load_library()
+    a = arch_struct(arch)
+    tabs, keep = tensor_table(weights)
+    b = C.c_uint64()
+    check(lib.s2s_uploaded_bytes_for(C.byref(a), tabs, len(weights), C.byref(b)),
+          "s2s_uploaded_bytes_for")
+    del keep
+    return int(b.value)
+
+
+def selftest(arch: M.Arch, weights: Optional[Dict[str, np.ndarray]] = None):
+    """`gpu::selftest` (the crate's --cuda-selftest): raises S2SError naming the
+    failing check; prints the count of checks on success."""
+    lib = load_library()
+    a = arch_struct(arch)
+    if weights:
+        tabs, keep = tensor_table(weights)
+        rc = lib.s2s_selftest(C.byref(a), tabs, len(weights))
+        del keep
+    else:
+        rc = lib.s2s_selftest(C.byref(a), None, 0)
+    check(rc, "s2s_selftest")
+
+
 # ---- per-op test entry points ------------------------------------------------
+
+def unit_floats(hp, wp, heads, head_dim):
+    """Floats of the window attention's unit layout of qkv for a plane."""
+    return (hp // 8) * (wp // 8) * ((heads + 1) // 2) * 64 * (6 * head_dim + 2)
+
+
+def test_qkv_windows(hp, wp, heads, head_dim, shift, x, wqkv, bqkv):
+    """The production qkv GEMM's raw unit-layout output, shape
+    [windows][head pairs][64][6*head_dim + 2] (unwritten padding is NaN)."""
+    lib = load_library()
+    n = unit_floats(hp, wp, heads, head_dim)
+    out = np.empty(n, np.float32)
+    c32 = lambda a: np.ascontiguousarray(a, np.float32)
+    check(lib.s2s_test_qkv_windows(hp, wp, heads, head_dim, shift, fptr(c32(x)), fptr(c32(wqkv)),
+                                   fptr(c32(bqkv)), fptr(out), n), "s2s_test_qkv_windows")
+    return out.reshape((hp // 8) * (wp // 8), (heads + 1) // 2, 64, 6 * head_dim + 2)
+
+
+def test_block_attention(hp, wp, heads, head_dim, shift, x, wqkv, bqkv, logit_scale, cpb):
+    """The production qkv GEMM + window attention; the plane [hp*wp][c]."""
+    lib = load_library()
+    c = heads * head_dim
+    out = np.empty((hp * wp, c), np.float32)
+    c32 = lambda a: np.ascontiguousarray(a, np.float32)
+    check(lib.s2s_test_block_attention(hp, wp, heads, head_dim, shift, fptr(c32(x)),
+                                       fptr(c32(wqkv)), fptr(c32(bqkv)),
+                                       fptr(c32(logit_scale).reshape(-1)), fptr(c32(cpb)),
+                                       fptr(out)), "s2s_test_block_attention")
+    return out
+
 
 def test_window_map(hp, wp, shift, win=8):
     lib = load_library()

@@ -89,12 +89,30 @@ struct Pending {
 
 int s2s_fail(const char *msg) { return fail(msg ? msg : "unknown error"); }
 
+// One device buffer of a forward's plan: where its pointer goes, its size in
+// floats, its name (for error messages) and whether the kernels reach it only
+// through per-task resources or 64-bit pointers ("wide": any size), as opposed
+// to a 32-bit offset from its base (below the 2 GiB resource limit).
+struct BufSpec {
+    float **dst;
+    size_t floats;
+    const char *what;
+    bool wide;
+};
+
+// Device allocations of one lifetime (weights, body plan, image plan) and
+// their total size.
+struct AllocList {
+    std::vector<void *> ptrs;
+    uint64_t bytes = 0;
+};
+
 struct s2s_ctx {
     s2s_arch arch{};
     int c = 0, hd = 0, hidden = 0, feat = 0, octaves = 0;
     int device = 0;
     hipStream_t stream = nullptr;
-    std::vector<void *> weight_allocs;
+    AllocList weight_allocs;
     uint64_t uploaded = 0;
 
     float *cf_b = nullptr;                   // conv_first's bias [C]
@@ -118,7 +136,9 @@ struct s2s_ctx {
     bool fuse2 = false;
     float *u2_w = nullptr, *u2_b = nullptr, *u2_we = nullptr, *u2_be = nullptr;
     int fused_octaves() const { return fuse2 ? 2 : (fuse_last ? 1 : 0); }
-    // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [3][9*F], conv_after_aux [F][9*4]
+    // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [4][9*F] (its fourth
+    // output row zero, so the conv writes channel 3 of the aux plane as 0),
+    // conv_after_aux [F][9*4]
     float *bc_w = nullptr, *bc_b = nullptr, *ax_w = nullptr, *ax_b = nullptr;
     float *caa_w = nullptr, *caa_b = nullptr;
     // pixelshuffledirect: upsample.0 [3*s*s][9*C]
@@ -129,17 +149,23 @@ struct s2s_ctx {
 
     // buffers planned for one padded plane (hp, wp)
     int bhp = 0, bwp = 0;
-    std::vector<void *> body_allocs;
+    AllocList body_allocs;
     float *cur = nullptr, *wk = nullptr, *tmp = nullptr, *body = nullptr;
     float *qkv = nullptr, *o = nullptr, *hid = nullptr;
     // head / io buffers planned for one image (h, w)
     int ih = 0, iw = 0;
-    std::vector<void *> head_allocs;
+    AllocList head_allocs;
     float *in_dev = nullptr, *in4 = nullptr, *out_dev = nullptr;
     std::vector<float *> fplanes;  // the head's feature planes
     // pixelshuffle_aux: aux conv output [P][4], its planar image [3][P], the
     // bicubic input [(hp*s)*(wp*s)][4] and its conv (= the last head plane)
     float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr, *bicf = nullptr;
+    // the host path's pinned staging copies of the input and output images
+    float *pin_in = nullptr, *pin_out = nullptr;
+    int pin_h = 0, pin_w = 0;
+    // a cap on the bytes of the body and image plans together (0 = none):
+    // SWIN2SR_HIP_ALLOC_LIMIT at s2s_create, or s2s_set_alloc_limit
+    uint64_t alloc_limit = 0;
 
     bool prof = false;
     std::string prof_only;  // bracket only launches of this name ("" = all)
@@ -151,9 +177,8 @@ struct s2s_ctx {
 
     ~s2s_ctx();
     int upload(const std::vector<float> &host, float **dev);
-    int alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what,
-              bool wide = false);
-    int plan_body(int hp, int wp);
+    int alloc(AllocList &list, size_t floats, float **dev, const char *what, bool wide = false,
+              bool planned = false);
     // qkv buffer floats: the plane layout, or the attention unit layout
     size_t qkv_floats(int hp, int wp) const {
         const size_t plane = (size_t)hp * wp * 3 * c;
@@ -161,7 +186,14 @@ struct s2s_ctx {
                    ? std::max(plane, attn_unit_floats(hp, wp, arch.heads, hd))
                    : plane;
     }
+    // The buffers of a padded plane's body, and of an image's head (with the
+    // host path's device copies of the input and output when `io`); `bind`
+    // points the specs at the context's members (else dst is null).
+    void body_specs(int hp, int wp, bool bind, std::vector<BufSpec> &v);
+    void image_specs(int h, int w, bool io, bool bind, std::vector<BufSpec> &v);
+    int plan_body(int hp, int wp);
     int plan_image(int h, int w);
+    int stage_buffers(int h, int w);
     hipEvent_t event();
     int drain();
     template <typename F>
@@ -175,9 +207,10 @@ struct s2s_ctx {
 
 namespace {
 
-void free_list(std::vector<void *> &l) {
-    for (void *p : l) (void)hipFree(p);
-    l.clear();
+void free_list(AllocList &l) {
+    for (void *p : l.ptrs) (void)hipFree(p);
+    l.ptrs.clear();
+    l.bytes = 0;
 }
 
 }  // namespace
@@ -192,13 +225,15 @@ s2s_ctx::~s2s_ctx() {
     free_list(head_allocs);
     free_list(body_allocs);
     free_list(weight_allocs);
+    if (pin_in) (void)hipHostFree(pin_in);
+    if (pin_out) (void)hipHostFree(pin_out);
     if (stream) (void)hipStreamDestroy(stream);
 }
 
 int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
     float *p = nullptr;
     HIPCHK("hipMalloc(weights)", hipMalloc(&p, std::max<size_t>(host.size(), 1) * sizeof(float)));
-    weight_allocs.push_back(p);
+    weight_allocs.ptrs.push_back(p);
     HIPCHK("hipMemcpy(weights)",
            hipMemcpy(p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice));
     uploaded += host.size() * sizeof(float);
@@ -216,46 +251,98 @@ int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
 // the crate's GPU_MAX_PLANE_PIXELS (65535 x 16, src/backend.rs:230). A plane
 // that would pass it is refused like an allocation failure: the message says
 // "out of memory", which is what the crate's tile-halving retry keys on
-// (src/main.rs:655-662), and a smaller tile then fits.
+// (src/main.rs:655-662), and a smaller tile then fits. `planned` buffers (the
+// body and image plans) also count against the context's allocation limit.
 static constexpr size_t kMaxBufferBytes = 0x7fff0000u;  // BUF_MAX_BYTES of the kernels
 
-int s2s_ctx::alloc(std::vector<void *> &list, size_t floats, float **dev, const char *what,
-                   bool wide) {
+int s2s_ctx::alloc(AllocList &list, size_t floats, float **dev, const char *what, bool wide,
+                   bool planned) {
+    const size_t bytes = std::max<size_t>(floats, 1) * sizeof(float);
     if (!wide && floats > kMaxBufferBytes / sizeof(float))
         return fail(std::string("hipMalloc(") + what + ", " + std::to_string(floats * sizeof(float)) +
                     " bytes) refused: above the 2 GiB limit of the kernels' 32-bit offsets into "
                     "this buffer (out of memory for one pass; tile the image)");
+    if (planned && alloc_limit &&
+        body_allocs.bytes + head_allocs.bytes + bytes > alloc_limit)
+        return fail(std::string("hipMalloc(") + what + ", " + std::to_string(bytes) +
+                    " bytes) refused: the context's allocation limit of " +
+                    std::to_string(alloc_limit) + " bytes would be passed (" +
+                    std::to_string(body_allocs.bytes + head_allocs.bytes) +
+                    " already planned): out of memory");
     float *p = nullptr;
-    hipError_t e = hipMalloc(&p, std::max<size_t>(floats, 1) * sizeof(float));
+    hipError_t e = hipMalloc(&p, bytes);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return fail(std::string("hipMalloc(") + what + ", " +
                     std::to_string(floats * sizeof(float)) + " bytes) failed: " +
                     hipGetErrorString(e) + (e == hipErrorOutOfMemory ? " (out of memory)" : ""));
     }
-    list.push_back(p);
+    list.ptrs.push_back(p);
+    list.bytes += bytes;
     *dev = p;
     return 0;
 }
 
 // Body buffers for a padded plane: the activation, the in-stage working copy,
 // the conv scratch, conv_first's output (the body skip), qkv, the attention
-// output and the MLP hidden layer. Reused while the plane size repeats
-// (reference Gpu::forward rebuilds Acts only on a size change, src/gpu.rs:741-750).
+// output and the MLP hidden layer.
+void s2s_ctx::body_specs(int hp, int wp, bool bind, std::vector<BufSpec> &v) {
+    const size_t P = (size_t)hp * wp;
+    auto d = [&](float **p) { return bind ? p : nullptr; };
+    v.push_back({d(&cur), P * c, "cur", false});
+    v.push_back({d(&wk), P * c, "work", false});
+    v.push_back({d(&tmp), P * c, "tmp", false});
+    v.push_back({d(&body), P * c, "body", false});
+    v.push_back({d(&qkv), qkv_floats(hp, wp), "qkv", true});
+    v.push_back({d(&o), P * c, "attn", false});
+    v.push_back({d(&hid), P * hidden, "mlp", false});
+}
+
+// Image buffers: the padded input (and, for the host path, device copies of
+// the input and the output), the head's feature planes - one per octave that
+// is not composed away for the pixel-shuffle heads, P, 4P, 16P, 16P for
+// nearest+conv, none for pixelshuffledirect - and the compressed head's aux
+// and bicubic planes.
+void s2s_ctx::image_specs(int h, int w, bool io, bool bind, std::vector<BufSpec> &v) {
+    const int win = arch.window, s = arch.scale;
+    const size_t P = (size_t)((h / win + 1) * win) * ((w / win + 1) * win);
+    auto d = [&](float **p) { return bind ? p : nullptr; };
+    if (io) {
+        v.push_back({d(&in_dev), (size_t)3 * h * w, "input", false});
+        v.push_back({d(&out_dev), (size_t)3 * h * s * w * s, "output", true});
+    }
+    v.push_back({d(&in4), P * 4, "padded input", false});
+    std::vector<size_t> planes;
+    if (arch.upsampler == S2S_PIXELSHUFFLE || arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
+        size_t px = P;
+        for (int o_ = 0; o_ <= octaves - fused_octaves(); ++o_, px *= 4) planes.push_back(px);
+    } else if (arch.upsampler == S2S_NEAREST_CONV) {
+        planes = {P, 4 * P, 16 * P, 16 * P};
+    }
+    if (bind) fplanes.assign(planes.size(), nullptr);
+    for (size_t i = 0; i < planes.size(); ++i)
+        v.push_back({bind ? &fplanes[i] : nullptr, planes[i] * feat, "head plane", true});
+    if (arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
+        v.push_back({d(&aux4), P * 4, "aux conv", false});
+        v.push_back({d(&auxp), P * 3, "aux image", false});
+        v.push_back({d(&bic4), P * s * s * 4, "bicubic input", true});
+    }
+}
+
+// Reused while the plane size repeats (reference Gpu::forward rebuilds Acts
+// only on a size change, src/gpu.rs:741-750).
 int s2s_ctx::plan_body(int hp, int wp) {
     if (hp == bhp && wp == bwp) return 0;
     if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
     free_list(body_allocs);
     bhp = bwp = 0;
-    const size_t P = (size_t)hp * wp;
-    if (alloc(body_allocs, P * c, &cur, "cur") || alloc(body_allocs, P * c, &wk, "work") ||
-        alloc(body_allocs, P * c, &tmp, "tmp") || alloc(body_allocs, P * c, &body, "body") ||
-        alloc(body_allocs, qkv_floats(hp, wp), &qkv, "qkv", true) ||
-        alloc(body_allocs, P * c, &o, "attn") ||
-        alloc(body_allocs, P * hidden, &hid, "mlp")) {
-        free_list(body_allocs);
-        return -1;
-    }
+    std::vector<BufSpec> v;
+    body_specs(hp, wp, true, v);
+    for (const BufSpec &b : v)
+        if (alloc(body_allocs, b.floats, b.dst, b.what, b.wide, true)) {
+            free_list(body_allocs);
+            return -1;
+        }
     bhp = hp;
     bwp = wp;
     return 0;
@@ -264,51 +351,51 @@ int s2s_ctx::plan_body(int hp, int wp) {
 int s2s_ctx::plan_image(int h, int w) {
     const int win = arch.window;
     const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
-    if (plan_body(hp, wp)) return -1;
-    if (h == ih && w == iw) return 0;
+    if (h == ih && w == iw && hp == bhp && wp == bwp) return 0;
     if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
+    // the image's buffers go first, so a size change never holds the old
+    // image plan and the new body plan at once
     free_list(head_allocs);
     fplanes.clear();
     ih = iw = 0;
-    const size_t P = (size_t)hp * wp;
-    const int s = arch.scale;
-    int rc = alloc(head_allocs, (size_t)3 * h * w, &in_dev, "input") ||
-             alloc(head_allocs, P * 4, &in4, "padded input") ||
-             alloc(head_allocs, (size_t)3 * h * s * w * s, &out_dev, "output", true);
-    // the head's feature planes: one per octave for the pixel-shuffle heads,
-    // P, 4P, 16P, 16P for nearest+conv, none for pixelshuffledirect
-    std::vector<size_t> planes;
-    if (arch.upsampler == S2S_PIXELSHUFFLE || arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
-        size_t px = P;
-        for (int o_ = 0; o_ <= octaves - fused_octaves(); ++o_, px *= 4) planes.push_back(px);
-    } else if (arch.upsampler == S2S_NEAREST_CONV) {
-        planes = {P, 4 * P, 16 * P, 16 * P};
-    }
-    for (size_t i = 0; rc == 0 && i < planes.size(); ++i) {
-        float *f = nullptr;
-        rc = alloc(head_allocs, planes[i] * feat, &f, "head plane", true);
-        fplanes.push_back(f);
-    }
-    if (rc == 0 && arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
-        const size_t Q = P * s * s;
-        rc = alloc(head_allocs, P * 4, &aux4, "aux conv") ||
-             alloc(head_allocs, P * 3, &auxp, "aux image") ||
-             alloc(head_allocs, Q * 4, &bic4, "bicubic input", true);
+    if (plan_body(hp, wp)) return -1;
+    std::vector<BufSpec> v;
+    image_specs(h, w, true, true, v);
+    for (const BufSpec &b : v)
+        if (alloc(head_allocs, b.floats, b.dst, b.what, b.wide, true)) {
+            free_list(head_allocs);
+            fplanes.clear();
+            return -1;
+        }
+    if (arch.upsampler == S2S_PIXELSHUFFLE_AUX)
         // the bicubic branch's conv lands in the last octave's plane, which the
         // last shuffle then updates in place (each element read, added, written
         // by one thread)
         bicf = fplanes[octaves];
-        // channel 3 of aux4 is never written and must read zero
-        if (rc == 0 && hipMemset(aux4, 0, P * 4 * sizeof(float)) != hipSuccess)
-            rc = fail("hipMemset(aux conv) failed");
-    }
-    if (rc) {
-        free_list(head_allocs);
-        fplanes.clear();
-        return -1;
-    }
     ih = h;
     iw = w;
+    return 0;
+}
+
+// The host path's pinned staging images for an h x w image (page-locked, so
+// the copies run as DMA at the link's rate and the host-side copies overlap
+// them). Only s2s_forward uses them.
+int s2s_ctx::stage_buffers(int h, int w) {
+    if (h == pin_h && w == pin_w) return 0;
+    if (pin_in) (void)hipHostFree(pin_in);
+    if (pin_out) (void)hipHostFree(pin_out);
+    pin_in = pin_out = nullptr;
+    pin_h = pin_w = 0;
+    const int s = arch.scale;
+    hipError_t e = hipHostMalloc((void **)&pin_in, (size_t)3 * h * w * sizeof(float));
+    if (e == hipSuccess)
+        e = hipHostMalloc((void **)&pin_out, (size_t)3 * h * s * w * s * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(hip_msg("hipHostMalloc(staging)", e));
+    }
+    pin_h = h;
+    pin_w = w;
     return 0;
 }
 
@@ -413,29 +500,10 @@ int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *
     const int P = hp * wp;
     // qkv straight into the window attention's unit layout where its kernel
     // takes the head shape, else the plane layout [P][3c]
-    const bool unit = qkv_unit_layout(arch.heads, hd, c);
-    GemmArgs g = rows_gemm(x_in, c, b.wqkv, c, b.bqkv, qkv, 3 * c, P, 3 * c, c);
-    g.H = hp;
-    g.W = wp;
-    g.shift = shift;
-    g.heads = arch.heads;
-    g.hd = hd;
-    if (gemm("qkv", g, ALOAD_ROWS, unit ? EPI_QKV_WIN : EPI_STORE)) return -1;
-
-    AttnArgs a{};
-    a.qkv = qkv;
-    a.unit = unit;
-    a.cpbt = b.cpbt;
-    a.logit_scale = b.ls;
-    a.out = o;
-    a.hp = hp;
-    a.wp = wp;
-    a.nww = wp / arch.window;
-    a.nw = (hp / arch.window) * a.nww;
-    a.heads = arch.heads;
-    a.head_dim = hd;
-    a.c = c;
-    a.shift = shift;
+    GemmArgs g;
+    const int epi = qkv_gemm_args(x_in, b.wqkv, b.bqkv, qkv, hp, wp, shift, arch.heads, hd, &g);
+    if (gemm("qkv", g, ALOAD_ROWS, epi)) return -1;
+    const AttnArgs a = window_attn_args(qkv, b.cpbt, b.ls, o, hp, wp, shift, arch.heads, hd);
     const unsigned ag = attention_grid(a);
     if (run("window_attention", dim3(ag), dim3(256),
             [&] { return launch_attention(a, stream, nullptr); }))
@@ -549,7 +617,9 @@ int s2s_ctx::head(int h, int w, float *d_out) {
                 return -1;
             g = conv_gemm(bic4, qh, qw, 4, bc_w, bc_b, bicf, feat, feat);
             if (gemm("conv_bicubic", g, ALOAD_IM2COL, EPI_STORE)) return -1;
-            g = conv_gemm(fplanes[0], hp, wp, feat, ax_w, ax_b, aux4, 4, 3);
+            // four output channels, the fourth with zero weights and bias: the
+            // aux plane's channel 3, which conv_after_aux reads as zero padding
+            g = conv_gemm(fplanes[0], hp, wp, feat, ax_w, ax_b, aux4, 4, 4);
             if (gemm("conv_aux", g, ALOAD_IM2COL, EPI_STORE)) return -1;
             g = conv_gemm(aux4, hp, wp, 4, caa_w, caa_b, fplanes[0], feat, feat);
             g.slope = 0.01f;
@@ -811,6 +881,75 @@ void compose_up2_last(const std::vector<float> &ue, const std::vector<float> &ub
     b48.assign(B.begin(), B.end());
 }
 
+// The head's feature width: conv_before_upsample's output channels.
+int head_feat_of(const TensorSet &ts, int C, int *F) {
+    const s2s_tensor *cb = ts.find("conv_before_upsample.0.weight");
+    if (!cb || cb->ndim != 4 || cb->shape[0] <= 0 || cb->shape[0] % 32 != 0)
+        return fail("weight `conv_before_upsample.0.weight` is missing or not [feat][C][3][3] "
+                    "with feat a multiple of 32");
+    if (ts.get("conv_before_upsample.0.weight", {cb->shape[0], C, 3, 3}, &cb)) return -1;
+    *F = (int)cb->shape[0];
+    return 0;
+}
+
+int octaves_of(int scale) {
+    int oct = 0;
+    while ((1 << oct) < scale) ++oct;
+    return oct;
+}
+
+// The bytes s2s_create uploads for an architecture and tensor set: the
+// weights as the kernels read them (re-laid-out, padded to 4 input channels,
+// folded and composed) and one CPB table per block. Written out term by term
+// from s2s_create's uploads; s2s_create checks its own count against it, so
+// the two cannot drift apart.
+int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes) {
+    const uint64_t C = A.embed, C4 = round4(A.embed), H2 = (uint64_t)A.mlp_ratio * A.embed;
+    const uint64_t NH = A.heads, n = (uint64_t)A.window * A.window;
+    uint64_t f = 0;
+    f += C;                     // conv_first's bias (the body skip)
+    f += 2 * 9 * 4 * C + C;     // k_embed's two weight sets, the folded bias
+    f += 4 * C;                 // patch_embed's LayerNorm, the final LayerNorm
+    f += C * 9 * C4 + C;        // conv_after_body
+    for (int s = 0; s < A.n_stages; ++s) {
+        f += C * 9 * C4 + C;    // the stage close (3x3 with the 1x1 folded in)
+        const uint64_t per_block = 3 * C * C + 3 * C  // fused qkv and its bias
+                                   + NH               // logit scale
+                                   + C * C + C        // proj
+                                   + 4 * C            // norm1, norm2
+                                   + H2 * C + H2 + C * H2 + C  // fc1, fc2
+                                   + NH * n * n;      // the CPB table
+        f += per_block * (uint64_t)A.depths[s];
+    }
+    const int up = A.upsampler;
+    if (up == S2S_PIXELSHUFFLE || up == S2S_PIXELSHUFFLE_AUX || up == S2S_NEAREST_CONV) {
+        int F = 0;
+        if (head_feat_of(ts, A.embed, &F)) return -1;
+        const uint64_t F_ = F, F4 = round4(F);
+        f += F_ * 9 * C4 + F_;          // conv_before_upsample
+        f += 9 * F_ * 3 + 3;            // conv_last
+        if (up == S2S_NEAREST_CONV) {
+            f += 3 * (F_ * 9 * F4 + F_);  // conv_up1, conv_up2, conv_hr
+        } else {
+            const int oct = octaves_of(A.scale);
+            f += (uint64_t)oct * (4 * F_ * 9 * F4 + 4 * F_);  // the octave convs
+            if (up == S2S_PIXELSHUFFLE && F % 8 == 0) {
+                if (oct >= 2 && F == 64)
+                    f += 5 * 48 * 25 * F_ + 5 * 48;  // two octaves and conv_last composed
+                else
+                    f += 5 * 12 * 25 * F_ + 5 * 12;  // the last octave and conv_last composed
+            }
+            if (up == S2S_PIXELSHUFFLE_AUX)
+                f += (F_ * 9 * 4 + F_) + (4 * 9 * F4 + 4) + (F_ * 9 * 4 + F_);  // bicubic, aux, after_aux
+        }
+    } else if (up == S2S_PIXELSHUFFLE_DIRECT) {
+        const uint64_t n3 = 3 * (uint64_t)A.scale * A.scale;
+        f += n3 * 9 * C4 + n3;
+    }
+    *bytes = f * sizeof(float);
+    return 0;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -996,21 +1135,35 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             rc = rc || up(p + "mlp.fc2.weight", {C, H2}, &bw.w2);
             rc = rc || up(p + "mlp.fc2.bias", {C}, &bw.b2);
             if (rc) break;
-            // The bias table. From the MLP when the set carries it (computed on
-            // the device: 16*sigmoid of Linear-ReLU-Linear on the log-spaced
-            // coordinates, gathered); otherwise from the converter's cpb_pre.
+            // The bias table, stored [head][query][key] and scaled by log2(e)
+            // for the base-2 softmax. From the converter's cpb_pre when the
+            // set carries it - the table the crate itself reads
+            // (src/gpu.rs:780-790, src/cpu.rs:1276-1284) - otherwise from the
+            // MLP (16*sigmoid of Linear-ReLU-Linear on the log-spaced
+            // coordinates, gathered, computed on the device).
             rc = ctx->alloc(ctx->weight_allocs, (size_t)NH * n * n, &bw.cpbt, "cpb");
             if (rc) break;
             ctx->uploaded += (uint64_t)NH * n * n * sizeof(float);
-            const s2s_tensor *m0 = ts.find(p + "attn.cpb_mlp.0.weight");
-            if (m0) {
+            if (ts.find(p + "attn.cpb_pre")) {
+                const s2s_tensor *cp;
+                rc = ts.get(p + "attn.cpb_pre", {(int64_t)n * n, NH}, &cp);
+                if (rc) break;
+                std::vector<float> t((size_t)NH * n * n);
+                for (int q = 0; q < n; ++q)
+                    for (int k = 0; k < n; ++k)
+                        for (int hh = 0; hh < NH; ++hh)
+                            t[((size_t)hh * n + q) * n + k] =
+                                ATTN_LOG2E * cp->data[((size_t)q * n + k) * NH + hh];
+                if (hipMemcpy(bw.cpbt, t.data(), t.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+                    rc = fail("hipMemcpy(cpb) failed");
+            } else {
                 const s2s_tensor *w0, *b0, *w2;
                 rc = rc || ts.get(p + "attn.cpb_mlp.0.weight", {512, 2}, &w0);
                 rc = rc || ts.get(p + "attn.cpb_mlp.0.bias", {512}, &b0);
                 rc = rc || ts.get(p + "attn.cpb_mlp.2.weight", {NH, 512}, &w2);
                 if (rc) break;
                 float *dw0, *db0, *dw2;
-                std::vector<void *> tmpl;
+                AllocList tmpl;
                 rc = ctx->alloc(tmpl, 1024, &dw0, "cpb w0") || ctx->alloc(tmpl, 512, &db0, "cpb b0") ||
                      ctx->alloc(tmpl, (size_t)NH * 512, &dw2, "cpb w2");
                 if (!rc) {
@@ -1025,31 +1178,12 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                     if (le != hipSuccess) rc = fail(hip_msg("cpb table", le));
                 }
                 free_list(tmpl);
-            } else {
-                const s2s_tensor *cp;
-                rc = ts.get(p + "attn.cpb_pre", {(int64_t)n * n, NH}, &cp);
-                if (rc) break;
-                std::vector<float> t((size_t)NH * n * n);
-                for (int q = 0; q < n; ++q)
-                    for (int k = 0; k < n; ++k)
-                        for (int hh = 0; hh < NH; ++hh)
-                            t[((size_t)hh * n + q) * n + k] = cp->data[((size_t)q * n + k) * NH + hh];
-                if (hipMemcpy(bw.cpbt, t.data(), t.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
-                    rc = fail("hipMemcpy(cpb) failed");
             }
         }
     }
 
     // ---- the reconstruction head (reference src/gpu.rs:801-872, network_swin2sr.py:790-860)
-    auto head_feat = [&]() -> int {
-        const s2s_tensor *cb = ts.find("conv_before_upsample.0.weight");
-        if (!cb || cb->ndim != 4 || cb->shape[0] <= 0 || cb->shape[0] % 32 != 0)
-            return fail("weight `conv_before_upsample.0.weight` is missing or not [feat][C][3][3] "
-                        "with feat a multiple of 32");
-        if (ts.get("conv_before_upsample.0.weight", {cb->shape[0], C, 3, 3}, &cb)) return -1;
-        ctx->feat = (int)cb->shape[0];
-        return 0;
-    };
+    auto head_feat = [&]() -> int { return head_feat_of(ts, C, &ctx->feat); };
     auto conv_last = [&](int F) -> int {
         const s2s_tensor *lw;
         if (ts.get("conv_last.weight", {3, F, 3, 3}, &lw)) return -1;
@@ -1066,8 +1200,7 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
         rc = rc || head_feat();
         if (!rc) {
             const int F = ctx->feat;
-            int oct = 0;
-            while ((1 << oct) < A.scale) ++oct;
+            const int oct = octaves_of(A.scale);
             ctx->octaves = oct;
             rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
@@ -1120,8 +1253,18 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             if (A.upsampler == S2S_PIXELSHUFFLE_AUX) {
                 rc = rc || upconv("conv_bicubic.weight", F, 3, &ctx->bc_w, nullptr);
                 rc = rc || up("conv_bicubic.bias", {F}, &ctx->bc_b);
-                rc = rc || upconv("conv_aux.weight", 3, F, &ctx->ax_w, nullptr);
-                rc = rc || up("conv_aux.bias", {3}, &ctx->ax_b);
+                // conv_aux with a fourth, zero output row (it writes the aux
+                // plane's zero channel 3 itself)
+                const s2s_tensor *aw, *ab;
+                rc = rc || ts.get("conv_aux.weight", {3, F, 3, 3}, &aw);
+                rc = rc || ts.get("conv_aux.bias", {3}, &ab);
+                if (!rc) {
+                    std::vector<float> w4 = conv_relayout(aw->data, 3, F, nullptr);
+                    w4.resize((size_t)4 * 9 * round4(F), 0.f);
+                    std::vector<float> b4(ab->data, ab->data + 3);
+                    b4.push_back(0.f);
+                    rc = ctx->upload(w4, &ctx->ax_w) || ctx->upload(b4, &ctx->ax_b);
+                }
                 rc = rc || upconv("conv_after_aux.0.weight", F, 3, &ctx->caa_w, nullptr);
                 rc = rc || up("conv_after_aux.0.bias", {F}, &ctx->caa_b);
             }
@@ -1148,6 +1291,17 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             rc = rc || conv_last(F);
         }
     }
+    uint64_t planned = 0;
+    if (!rc && weights_device_bytes(A, ts, &planned)) rc = -1;
+    if (!rc && planned != ctx->uploaded)
+        rc = fail("internal: s2s_create uploaded " + std::to_string(ctx->uploaded) +
+                  " bytes where s2s_uploaded_bytes_for plans " + std::to_string(planned));
+    if (!rc) {
+        // an allocation cap on the per-image plans, for callers (and tests)
+        // that reserve device memory: "out of memory" past it
+        const char *lim = getenv("SWIN2SR_HIP_ALLOC_LIMIT");
+        if (lim && *lim) ctx->alloc_limit = strtoull(lim, nullptr, 10);
+    }
     if (rc) {
         std::string keep = g_err;
         delete ctx;
@@ -1155,6 +1309,35 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
         return -1;
     }
     *out = ctx;
+    return 0;
+}
+
+int s2s_uploaded_bytes_for(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors,
+                           uint64_t *bytes) {
+    if (!arch || !tensors || !bytes) return fail("s2s_uploaded_bytes_for: null argument");
+    if (arch->embed <= 0 || arch->heads <= 0 || arch->n_stages < 0 ||
+        arch->n_stages > S2S_MAX_STAGES)
+        return fail("s2s_uploaded_bytes_for: bad architecture");
+    TensorSet ts{tensors, n_tensors};
+    return weights_device_bytes(*arch, ts, bytes);
+}
+
+int s2s_plan_bytes(s2s_ctx *ctx, int h, int w, uint64_t *bytes) {
+    if (!ctx || !bytes) return fail("s2s_plan_bytes: null argument");
+    if (h < ctx->arch.window || w < ctx->arch.window) return fail("image smaller than one window");
+    const int win = ctx->arch.window;
+    std::vector<BufSpec> v;
+    ctx->body_specs((h / win + 1) * win, (w / win + 1) * win, false, v);
+    ctx->image_specs(h, w, true, false, v);
+    uint64_t b = 0;
+    for (const BufSpec &x : v) b += std::max<size_t>(x.floats, 1) * sizeof(float);
+    *bytes = b;
+    return 0;
+}
+
+int s2s_set_alloc_limit(s2s_ctx *ctx, uint64_t bytes) {
+    if (!ctx) return fail("null context");
+    ctx->alloc_limit = bytes;
     return 0;
 }
 
@@ -1168,18 +1351,47 @@ int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_o
     return ctx->forward_device(h, w, d_in, d_out);
 }
 
+// The host path: the caller's pageable input is copied into the context's
+// pinned staging image and uploaded as one DMA; the output comes back in
+// chunks, each copied out of the pinned image while the next is still in
+// flight, so the host copy overlaps the link.
 int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out) {
     if (!ctx || !in_adjusted || !out) return fail("s2s_forward: null argument");
     HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
     if (h < ctx->arch.window || w < ctx->arch.window) return ctx->forward_device(h, w, nullptr, nullptr);
-    if (ctx->plan_image(h, w)) return -1;
+    if (ctx->plan_image(h, w) || ctx->stage_buffers(h, w)) return -1;
     const int s = ctx->arch.scale;
     const size_t nin = (size_t)3 * h * w, nout = (size_t)3 * h * s * w * s;
-    HIPCHK("hipMemcpyAsync(input)", hipMemcpyAsync(ctx->in_dev, in_adjusted, nin * 4,
+    std::memcpy(ctx->pin_in, in_adjusted, nin * 4);
+    HIPCHK("hipMemcpyAsync(input)", hipMemcpyAsync(ctx->in_dev, ctx->pin_in, nin * 4,
                                                    hipMemcpyHostToDevice, ctx->stream));
     if (ctx->forward_device(h, w, ctx->in_dev, ctx->out_dev)) return -1;
-    HIPCHK("hipMemcpyAsync(output)", hipMemcpyAsync(out, ctx->out_dev, nout * 4,
-                                                    hipMemcpyDeviceToHost, ctx->stream));
+    constexpr size_t kChunk = (size_t)1 << 19;  // floats per download chunk (2 MiB)
+    const size_t nchunks = (nout + kChunk - 1) / kChunk;
+    std::vector<hipEvent_t> done(nchunks, nullptr);
+    int rc = 0;
+    for (size_t i = 0; i < nchunks && rc == 0; ++i) {
+        const size_t off = i * kChunk, len = std::min(kChunk, nout - off);
+        hipError_t e = hipMemcpyAsync(ctx->pin_out + off, ctx->out_dev + off, len * 4,
+                                      hipMemcpyDeviceToHost, ctx->stream);
+        if (e == hipSuccess) e = (done[i] = ctx->event()) ? hipSuccess : hipErrorOutOfMemory;
+        if (e == hipSuccess) e = hipEventRecord(done[i], ctx->stream);
+        if (e != hipSuccess) rc = fail(hip_msg("hipMemcpyAsync(output)", e));
+    }
+    for (size_t i = 0; i < nchunks; ++i) {
+        if (!done[i]) continue;
+        if (rc == 0) {
+            const hipError_t e = hipEventSynchronize(done[i]);
+            if (e != hipSuccess) {
+                rc = fail(hip_msg("hipEventSynchronize(output)", e));
+            } else {
+                const size_t off = i * kChunk, len = std::min(kChunk, nout - off);
+                std::memcpy(out + off, ctx->pin_out + off, len * 4);
+            }
+        }
+        ctx->free_events.push_back(done[i]);
+    }
+    if (rc) return rc;
     ctx->aux_host.clear();
     if (ctx->arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
         // the compressed head's second image, at the padded geometry

@@ -109,6 +109,54 @@ struct AttnArgs {
     int nws;                   // k_wattn: window lanes per XCD (set by launch_attention)
 };
 
+// A block's qkv projection as the forward launches it: x [hp*wp][c] times
+// the fused [3c][c] weight plus [q_bias | 0 | v_bias], written in the window
+// attention's unit layout (EPI_QKV_WIN; A rows read in the block's
+// shifted-window order) when the head shape takes it, else in the plane
+// layout [hp*wp][3c] (EPI_STORE). Returns the epilogue to launch with.
+inline int qkv_gemm_args(const float *x, const float *wqkv, const float *bqkv, float *qkv,
+                         int hp, int wp, int shift, int heads, int hd, GemmArgs *g) {
+    const int c = heads * hd;
+    *g = GemmArgs{};
+    g->A = x;
+    g->lda = c;
+    g->B = wqkv;
+    g->ldb = c;
+    g->bias = bqkv;
+    g->out = qkv;
+    g->ldo = 3 * c;
+    g->M = hp * wp;
+    g->N = 3 * c;
+    g->K = c;
+    g->H = hp;
+    g->W = wp;
+    g->shift = shift;
+    g->heads = heads;
+    g->hd = hd;
+    return qkv_unit_layout(heads, hd, c) ? EPI_QKV_WIN : EPI_STORE;
+}
+
+// The window attention over that qkv buffer, output scattered back to the
+// plane [hp*wp][c] (cpbt [heads][64][64] x log2(e), logit_scale [heads]).
+inline AttnArgs window_attn_args(const float *qkv, const float *cpbt, const float *logit_scale,
+                                 float *out, int hp, int wp, int shift, int heads, int hd) {
+    AttnArgs a{};
+    a.qkv = qkv;
+    a.unit = qkv_unit_layout(heads, hd, heads * hd);
+    a.cpbt = cpbt;
+    a.logit_scale = logit_scale;
+    a.out = out;
+    a.hp = hp;
+    a.wp = wp;
+    a.nww = wp / 8;
+    a.nw = (hp / 8) * a.nww;
+    a.heads = heads;
+    a.head_dim = hd;
+    a.c = heads * hd;
+    a.shift = shift;
+    return a;
+}
+
 #define GEMM_NVARIANTS 6
 hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st);
 hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int variant,

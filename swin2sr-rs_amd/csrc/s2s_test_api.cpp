@@ -149,6 +149,72 @@ int s2s_test_attention(int hp, int wp, int win, int heads, int head_dim, int shi
     return 0;
 }
 
+// The block's qkv GEMM exactly as the forward launches it (qkv_gemm_args:
+// the shifted-window gather into the unit layout), its raw output buffer
+// downloaded. Unwritten floats (the padding) read back as NaN.
+int s2s_test_qkv_windows(int hp, int wp, int heads, int head_dim, int shift, const float *x,
+                         const float *wqkv, const float *bqkv, float *unit, size_t unit_cap) {
+    const int c = heads * head_dim;
+    if (!qkv_unit_layout(heads, head_dim, c))
+        return fail("this head shape keeps qkv in the plane layout (no unit layout to probe)");
+    if (hp % 8 || wp % 8 || hp <= 0 || wp <= 0) return fail("plane must be a multiple of 8");
+    if (shift < 0 || shift >= 8) return fail("shift must be in [0, 8)");
+    const size_t P = (size_t)hp * wp, nu = attn_unit_floats(hp, wp, heads, head_dim);
+    if (unit_cap < nu) return fail("unit buffer too small: " + std::to_string(nu) + " floats needed");
+    Dev d;
+    const float *dx = d.up(x, P * c), *dw = d.up(wqkv, (size_t)3 * c * c);
+    const float *db = d.up(bqkv, (size_t)3 * c);
+    float *dq = d.alloc<float>(nu);
+    if (!dx || !dw || !db || !dq) return fail("hipMalloc failed: out of memory");
+    if (hipMemset(dq, 0xff, nu * 4) != hipSuccess) return fail("hipMemset failed");
+    GemmArgs g;
+    const int epi = qkv_gemm_args(dx, dw, db, dq, hp, wp, shift, heads, head_dim, &g);
+    hipError_t e = launch_gemm(g, ALOAD_ROWS, epi, 0);
+    if (int rc = finish(e, "k_bsgemm(qkv)")) return rc;
+    if (hipMemcpy(unit, dq, nu * 4, hipMemcpyDeviceToHost) != hipSuccess) return fail("hipMemcpy failed");
+    return 0;
+}
+
+// The block's attention half exactly as the forward launches it: the qkv
+// GEMM (unit or plane layout by head shape), then the window attention whose
+// output is scattered back to the plane [hp*wp][c]. `cpb` is [n*n][heads] in
+// the checkpoint's (cpb_pre) layout.
+int s2s_test_block_attention(int hp, int wp, int heads, int head_dim, int shift, const float *x,
+                             const float *wqkv, const float *bqkv, const float *logit_scale,
+                             const float *cpb, float *out) {
+    const int c = heads * head_dim;
+    if (head_dim > 32 || head_dim <= 0 || c % 4) return fail("unsupported head shape");
+    if (hp % 8 || wp % 8 || hp <= 0 || wp <= 0) return fail("plane must be a multiple of 8");
+    if (shift < 0 || shift >= 8) return fail("shift must be in [0, 8)");
+    const size_t P = (size_t)hp * wp;
+    const int n = 64;
+    std::vector<float> cpbt((size_t)heads * n * n);
+    for (int q = 0; q < n; ++q)
+        for (int k = 0; k < n; ++k)
+            for (int h = 0; h < heads; ++h)
+                cpbt[((size_t)h * n + q) * n + k] = ATTN_LOG2E * cpb[((size_t)q * n + k) * heads + h];
+    const size_t nq = qkv_unit_layout(heads, head_dim, c)
+                          ? std::max(P * 3 * c, attn_unit_floats(hp, wp, heads, head_dim))
+                          : P * 3 * c;
+    Dev d;
+    const float *dx = d.up(x, P * c), *dw = d.up(wqkv, (size_t)3 * c * c);
+    const float *db = d.up(bqkv, (size_t)3 * c), *dls = d.up(logit_scale, heads);
+    const float *dcp = d.up(cpbt.data(), cpbt.size());
+    float *dq = d.alloc<float>(nq), *dout = d.alloc<float>(P * c);
+    if (!dx || !dw || !db || !dls || !dcp || !dq || !dout)
+        return fail("hipMalloc failed: out of memory");
+    GemmArgs g;
+    const int epi = qkv_gemm_args(dx, dw, db, dq, hp, wp, shift, heads, head_dim, &g);
+    hipError_t e = launch_gemm(g, ALOAD_ROWS, epi, 0);
+    if (e == hipSuccess)
+        e = launch_attention(window_attn_args(dq, dcp, dls, dout, hp, wp, shift, heads, head_dim), 0,
+                             nullptr);
+    if (int rc = finish(e, "qkv + window attention")) return rc;
+    if (hipMemcpy(out, dout, P * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
 int s2s_test_cpb_table(int win, int heads, const float *w0, const float *b0, const float *w2,
                        float *out) {
     if (win < 2) return fail("window must be >= 2");

@@ -1,4 +1,5 @@
-"""The crate's tiling and memory policy, host side (reference src/backend.rs:88-383).
+"""The crate's tiling and memory policy, host side (reference src/backend.rs:88-383,
+src/main.rs:579-662).
 
 `north_star` keeps this logic in the crate's Rust host unchanged; this module is
 its mirror over the `Backend` interface, so the tiled path (config 4: 256-pixel
@@ -10,15 +11,23 @@ would drive it:
     mean-adjusted (`Pre::adjust`), run through `backend.forward`, and its
     interior copied to the output on the OUTPUT grid; `tile == 0` is one exact
     pass over the whole image;
+  - `run_with_fallback`: `run_tiled`, retried with the tile halved (the whole
+    image's first retry at half its longer side) while the backend reports
+    "out of memory", announced on stderr;
   - `crop_side`: the padded plane a crop runs on, `(n // win + 1) * win`;
-  - `per_pixel_floats`: this backend's device floats per padded pixel (its
-    buffer plan, `s2s_ctx::plan_body` / `plan_image`), which stays at or below
-    the figure the crate models for its device (`src/backend.rs:300-383`), so a
-    budget computed with the crate's model never under-counts this backend;
+  - `crate_per_pixel_floats`: the crate's own model of its device's floats per
+    padded pixel (`per_pixel_floats(wt, gpu = true)`), which `auto_tile` and
+    `activation_bytes` budget with - the policy is the crate's, unchanged;
+  - `plan_floats` / `per_pixel_floats`: this backend's exact buffer plan for an
+    image (what `s2s_plan_bytes` reports) and its bound per padded pixel, which
+    stays below the crate's model, so a budget computed with that model never
+    under-counts this backend;
   - `auto_tile`: the largest window-multiple tile (from 1024, halving) whose
     crop fits a byte budget and the launch ceiling.
 """
 from __future__ import annotations
+
+import sys
 
 import numpy as np
 
@@ -45,29 +54,93 @@ def crop_side(h: int, w: int, tile: int, pad: int, win: int) -> int:
     return max((th // win + 1) * win, (tw // win + 1) * win)
 
 
-def per_pixel_floats(arch: M.Arch) -> int:
-    """Device floats per padded pixel of this backend's buffer plan."""
-    c = arch.embed
-    hidden = arch.mlp_ratio * c
-    s = arch.scale
-    body = 4 * c + 3 * c + c + hidden          # cur, work, tmp, body skip; qkv; attn out; mlp
-    f = arch.feat
+def crate_per_pixel_floats(arch: M.Arch) -> int:
+    """reference src/backend.rs:300-383 with `gpu = true`: the crate's device
+    inventory per padded pixel (activations, the head's peak, the io images)."""
+    c, mlp, r2, f = arch.embed, arch.embed * arch.mlp_ratio, arch.scale ** 2, arch.feat
+    acts = 5 * c + 3 * c + 3 * c + mlp
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
-        head = sum(f * 4 ** o for o in range(arch.octaves + 1))
+        prev, peak = f, 0
+        for o in range(arch.octaves):
+            shuf = 4 * f * 4 ** o
+            peak, prev = max(peak, prev + shuf), shuf
+        head = max(peak, prev + 3 * r2)
+    elif arch.upsampler == "nearest+conv":
+        head = max(max(4 * f * 4 ** s + f * 4 ** (s + 1) for s in range(2)), 4 * f + 3 * r2)
+    else:
+        head = 2 * 3 * r2
+    return acts + head + 3 + 3 * r2
+
+
+def _unit_layout(arch: M.Arch) -> bool:
+    """Whether the forward keeps qkv in the window attention's unit layout
+    (the library's qkv_unit_layout)."""
+    hd, heads, c = arch.head_dim, arch.heads, arch.embed
+    if hd not in (2, 10, 30, 32) or c != heads * hd or c % 4:
+        return False
+    if heads % 2 and hd % 4:
+        return False
+    return c in (180, 60, 360, 120)
+
+
+def _fused_octaves(arch: M.Arch) -> int:
+    """Octaves of the pixel-shuffle head composed into its last kernel."""
+    if arch.upsampler != "pixelshuffle" or arch.feat % 8:
+        return 0
+    return 2 if arch.octaves >= 2 and arch.feat == 64 else 1
+
+
+def _plan_terms(arch: M.Arch, h: int, w: int):
+    """(floats per buffer) of the library's plan for an h x w image, in
+    s2s_ctx::body_specs + image_specs order (host-path copies included)."""
+    win, c, s, f = arch.window, arch.embed, arch.scale, arch.feat
+    hp, wp = (h // win + 1) * win, (w // win + 1) * win
+    P = hp * wp
+    qkv = P * 3 * c
+    if _unit_layout(arch):
+        qkv = max(qkv, P * ((arch.heads + 1) // 2) * (6 * arch.head_dim + 2))
+    terms = [P * c] * 4 + [qkv, P * c, P * arch.mlp_ratio * c]
+    terms += [3 * h * w, 3 * h * s * w * s, P * 4]
+    if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
+        terms += [P * 4 ** o * f for o in range(arch.octaves - _fused_octaves(arch) + 1)]
         if arch.upsampler == "pixelshuffle_aux":
-            head += 4 + 3 + 4 * s * s            # aux conv, aux image, bicubic input
+            terms += [P * 4, P * 3, P * s * s * 4]
+    elif arch.upsampler == "nearest+conv":
+        terms += [P * f, 4 * P * f, 16 * P * f, 16 * P * f]
+    return terms
+
+
+def plan_floats(arch: M.Arch, h: int, w: int) -> int:
+    """This backend's device floats for an h x w image: exactly what
+    `s2s_plan_bytes` reports, / 4."""
+    return sum(max(t, 1) for t in _plan_terms(arch, h, w))
+
+
+def per_pixel_floats(arch: M.Arch) -> int:
+    """This backend's device floats per padded pixel: `plan_floats` divided by
+    the padded plane, bounded over image sizes (the io images counted at the
+    padded size)."""
+    c, s, f = arch.embed, arch.scale, arch.feat
+    qkv = 3 * c
+    if _unit_layout(arch):
+        qkv = max(qkv, ((arch.heads + 1) // 2) * (6 * arch.head_dim + 2))
+    body = 4 * c + qkv + c + arch.mlp_ratio * c
+    if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
+        head = sum(f * 4 ** o for o in range(arch.octaves - _fused_octaves(arch) + 1))
+        if arch.upsampler == "pixelshuffle_aux":
+            head += 4 + 3 + 4 * s * s
     elif arch.upsampler == "nearest+conv":
         head = f * (1 + 4 + 16 + 16)
     else:
         head = 0
-    io = 3 + 4 + 3 * s * s                      # input, padded input, output
+    io = 3 + 3 * s * s + 4
     return body + head + io
 
 
 def auto_tile(arch: M.Arch, budget: int, h: int, w: int, pad: int) -> int:
-    """reference src/backend.rs:169-189 with this backend's per-pixel figure."""
+    """reference src/backend.rs:169-189, with the crate's own device model."""
     win = arch.window
-    per_px = per_pixel_floats(arch)
+    per_px = crate_per_pixel_floats(arch)
     pad = _round_pad(pad, win)
 
     def fits(side):
@@ -80,6 +153,46 @@ def auto_tile(arch: M.Arch, budget: int, h: int, w: int, pad: int) -> int:
         if fits(crop_side(h, w, t, pad, win)) or t == win:
             return t
         t = max(t // 2 // win, 1) * win
+
+
+def is_out_of_memory(err: str) -> bool:
+    """reference src/main.rs:660-662: the one failure a smaller tile can fix."""
+    return "OUT_OF_MEMORY" in err or "out of memory" in err
+
+
+def run_with_fallback(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: int,
+                      quiet: bool = False, log=None):
+    """reference src/main.rs:579-662: `run_tiled`, and while the backend fails
+    with an out-of-memory error, again with the tile halved - a failed
+    whole-image pass (`tile == 0`) falls back to half the image's longer side -
+    down to one window. Only out-of-memory errors are retried; a retry out of
+    `tile == 0` (the only exact mode) is announced even when `quiet`.
+    Returns (image, tile used)."""
+    log = log or (lambda m: print(m, file=sys.stderr, flush=True))
+    win = arch.window
+    _, h, w = img.shape
+    for _ in range(64):
+        try:
+            return run_tiled(arch, backend, img, tile, pad), tile
+        except Exception as e:  # the backend's error type carries the message
+            msg = str(e)
+            if not (is_out_of_memory(msg) and (tile > win or tile == 0)):
+                raise
+            nxt = (max(h, w) // 2 // win if tile == 0 else tile // 2 // win)
+            nxt = max(nxt, 1) * win
+            shrinking = nxt != 0 if tile == 0 else nxt < tile
+            if not shrinking or nxt == 0:
+                raise type(e)(f"{msg}\n(a {win}-pixel tile is the smallest this engine will "
+                              "run, and it did not fit either)") from e
+            note = msg.rstrip(".")
+            if tile == 0:
+                log(f"note: {note} - retrying with a {nxt}x{nxt} tile (--tile 0 is the only "
+                    "exact mode; this run is now tiled, and tiled results differ slightly from "
+                    "one pass - see README)")
+            elif not quiet:
+                log(f"note: {note} - retrying with a {nxt}x{nxt} tile")
+            tile = nxt
+    raise RuntimeError(f"gave up after 64 tile reductions at tile {tile}")
 
 
 def run_tiled(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: int) -> np.ndarray:

@@ -41,35 +41,45 @@ def test_crop_side_is_the_reference_rule(pkg):
     assert T.crop_side(1024, 1024, 256, 9, 8) == T.crop_side(1024, 1024, 256, 16, 8)
 
 
+def test_crate_device_model_is_the_references(pkg):
+    """reference src/backend.rs:300-383 (gpu = true), checked against the
+    figures its own comments quote: 3671 floats a padded pixel for the
+    180-wide classical x4, 819 for the lightweight x2."""
+    M, T = pkg.model, pkg.tiling
+    assert T.crate_per_pixel_floats(M.classical(4)) == 3671
+    assert T.crate_per_pixel_floats(M.lightweight(2)) == 819
+
+
 def test_per_pixel_floats_stays_within_the_crates_device_model(pkg):
     """The crate budgets with its own device inventory (src/backend.rs:300-383);
-    this backend must not allocate more per padded pixel than that model says."""
-    M = pkg.model
-    T = pkg.tiling
-
-    def crate_model(a):
-        c, mlp, r2, f = a.embed, a.embed * a.mlp_ratio, a.scale ** 2, a.feat
-        acts = 5 * c + 3 * c + 3 * c + mlp
-        if a.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
-            prev, peak = f, 0
-            for o in range(a.octaves):
-                shuf = 4 * f * 4 ** o
-                peak, prev = max(peak, prev + shuf), shuf
-            head = max(peak, prev + 3 * r2)
-        elif a.upsampler == "nearest+conv":
-            head = max(max(4 * f * 4 ** s + f * 4 ** (s + 1) for s in range(2)), 4 * f + 3 * r2)
-        else:
-            head = 2 * 3 * r2
-        return acts + head + 3 + 3 * r2
-
+    this backend must not allocate more per padded pixel than that model says,
+    and its exact plan must stay within its own per-pixel bound."""
+    M, T = pkg.model, pkg.tiling
     for a in (M.classical(4), M.classical(2), M.lightweight(2), M.realworld(), M.compressed()):
-        assert T.per_pixel_floats(a) <= crate_model(a), a.upsampler
+        assert T.per_pixel_floats(a) <= T.crate_per_pixel_floats(a), a.upsampler
+        for h, w in [(8, 8), (37, 29), (256, 256), (480, 640)]:
+            P = (h // 8 + 1) * 8 * ((w // 8 + 1) * 8)
+            assert T.plan_floats(a, h, w) <= T.per_pixel_floats(a) * P
+
+
+def test_plan_floats_counts_the_unit_layout_and_the_composed_octaves(pkg):
+    """The terms the advisor found the old figure missing: the attention's
+    unit layout of qkv ((heads+1)/2 x (6 hd + 2) floats a pixel, 546 at
+    hd = 30) and the head planes the composed octaves never allocate."""
+    M, T = pkg.model, pkg.tiling
+    a = M.classical(4)
+    P = 264 * 264
+    terms = T._plan_terms(a, 256, 256)
+    assert terms[4] == P * 546                  # qkv, unit layout
+    assert terms[-1] == P * 64                  # one head plane: both octaves composed
+    assert T.plan_floats(M.classical(2), 256, 256) - T.plan_floats(a, 256, 256) == \
+        3 * 256 * 256 * (4 - 16)                # x2: one composed octave, plane 0 only
 
 
 def test_auto_tile(pkg):
     T = pkg.tiling
     a = pkg.model.classical(4)
-    per = T.per_pixel_floats(a)
+    per = T.crate_per_pixel_floats(a)
     # a budget the whole image fits: one pass
     assert T.auto_tile(a, per * 264 * 264 * 4, 256, 256, 32) == 0
     # a budget a 256 tile with 32 of context fits but the image does not
@@ -79,6 +89,62 @@ def test_auto_tile(pkg):
     # the launch ceiling tiles even an unlimited budget
     big = T.auto_tile(a, 1 << 62, 2000, 2000, 32)
     assert big != 0 and T.crop_side(2000, 2000, big, 32, 8) ** 2 <= T.GPU_MAX_PLANE_PIXELS
+
+
+class CappedBackend:
+    """A backend that fails like a device out of memory above a crop size, or
+    with another error when asked (test code only)."""
+
+    def __init__(self, inner, max_side, error="hipMalloc(qkv) failed: out of memory"):
+        self.inner, self.max_side, self.error, self.sizes = inner, max_side, error, []
+
+    def forward(self, h, w, x):
+        self.sizes.append((h, w))
+        if max(h, w) > self.max_side:
+            raise RuntimeError(self.error)
+        return self.inner.forward(h, w, x)
+
+
+def test_run_with_fallback_halves_until_the_tile_fits(pkg, orc):
+    """reference src/main.rs:579-662: tile 0 falls back to half the image's
+    longer side, then halves; each retry is announced; the result is
+    run_tiled's at the tile that fitted."""
+    M, T = pkg.model, pkg.tiling
+    a = tiny(pkg)
+    inner = OracleBackend(orc, a, M.make_weights(a, seed=8, perturb=True))
+    img = M.to_unit(M.input_uniform(64, 48, seed=9))
+    be = CappedBackend(inner, 32)
+    notes = []
+    got, tile = T.run_with_fallback(a, be, img, 0, 8, log=notes.append)
+    assert tile == 16
+    assert be.sizes[:2] == [(64, 48), (40, 40)]
+    assert len(notes) == 2 and "--tile 0 is the only exact mode" in notes[0]
+    assert "retrying with a 32x32 tile" in notes[0] and "retrying with a 16x16 tile" in notes[1]
+    assert np.array_equal(got, T.run_tiled(a, inner, img, 16, 8))
+    # quiet silences the note for a tile the user chose, never the one out of tile 0
+    notes.clear()
+    T.run_with_fallback(a, CappedBackend(inner, 32), img, 32, 8, quiet=True, log=notes.append)
+    assert notes == []
+
+
+def test_run_with_fallback_retries_only_out_of_memory(pkg, orc):
+    M, T = pkg.model, pkg.tiling
+    a = tiny(pkg)
+    inner = OracleBackend(orc, a, M.make_weights(a, seed=8, perturb=True))
+    img = M.to_unit(M.input_uniform(32, 32, seed=9))
+    be = CappedBackend(inner, 8, error="k_gemm failed: hipErrorIllegalAddress")
+    with pytest.raises(RuntimeError, match="IllegalAddress"):
+        T.run_with_fallback(a, be, img, 0, 8, log=lambda m: None)
+    assert len(be.sizes) == 1
+    # a one-window tile that still does not fit is not retried: the device's
+    # own error ends the run (the guard is tile > win or tile == 0)
+    be = CappedBackend(inner, 4)
+    notes = []
+    with pytest.raises(RuntimeError, match="out of memory"):
+        T.run_with_fallback(a, be, img, 0, 8, log=notes.append)
+    assert len(notes) == 2 and "retrying with a 8x8 tile" in notes[1]
+    assert T.is_out_of_memory("cuMemAlloc failed: CUDA_ERROR_OUT_OF_MEMORY")
+    assert not T.is_out_of_memory("launch failed")
 
 
 def test_tile_covering_the_image_is_one_exact_pass(pkg, orc):
