@@ -138,6 +138,22 @@ int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out
  * inputs already in HBM (the throughput harness) uses. */
 int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
 
+/* `s2s_forward_device` without allocating anything: every intermediate
+ * buffer is carved out of a static device workspace of 256 MiB per GPU
+ * (a file-scope array the library holds on each GPU it runs on until the
+ * process ends), and the call makes no hipMalloc, hipFree or other allocating
+ * call (no profiler events either). No counterpart in the reference: it is
+ * for callers that cannot allocate - code under HIP graph capture, tight
+ * serving loops, harnesses that forbid it. The caller passes the device input
+ * and output as for `s2s_forward_device`; enqueued on the context's stream,
+ * not synchronised. Planes whose buffers do not fit the workspace are refused
+ * with an error (classical x4 at C = 180: padded planes up to ~35,800 pixels,
+ * i.e. images up to 183 x 183; `s2s_plan_bytes` less the two host-path copies
+ * is the figure). Every call on one GPU shares that GPU's workspace, which
+ * keeps the last call's contents: calls that overlap on one GPU (other
+ * contexts or streams) race. */
+int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
+
 /* `Backend::aux` (reference src/gpu.rs:756-758): the last forward's secondary
  * image, denormalised, at the PADDED plane's geometry `[3][hp][wp]`. `*n` is 0
  * (and `*ptr` NULL) when the head makes none. Valid until the next forward. */

@@ -56,6 +56,8 @@ EXPORTS = {
     "s2s_selftest": (C.c_int, [C.POINTER(Arch_), C.POINTER(Tensor_), C.c_size_t]),
     "s2s_forward": (C.c_int, [C.c_void_p, C.c_int, C.c_int, FP, FP]),
     "s2s_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "s2s_forward_device_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                             C.c_void_p]),
     "s2s_aux": (C.c_int, [C.c_void_p, C.POINTER(FP), C.POINTER(C.c_size_t)]),
     "s2s_last_error": (C.c_char_p, []),
     "s2s_device_info": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t]),
@@ -204,6 +206,12 @@ class HipBackend:
     def forward_device(self, h: int, w: int, d_in: int, d_out: int):
         check(self._lib.s2s_forward_device(self._ctx, h, w, C.c_void_p(d_in), C.c_void_p(d_out)),
               "s2s_forward_device")
+
+    def forward_device_noalloc(self, h: int, w: int, d_in: int, d_out: int):
+        """The forward on the library's static per-GPU workspace (no allocation)."""
+        check(self._lib.s2s_forward_device_noalloc(self._ctx, h, w, C.c_void_p(d_in),
+                                                   C.c_void_p(d_out)),
+              "s2s_forward_device_noalloc")
 
     def rstb_device(self, stage: int, hp: int, wp: int, d_in: int, d_out: int):
         check(self._lib.s2s_rstb_device(self._ctx, stage, hp, wp, C.c_void_p(d_in),

@@ -21,6 +21,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -254,6 +255,34 @@ int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
 // (src/main.rs:655-662), and a smaller tile then fits. `planned` buffers (the
 // body and image plans) also count against the context's allocation limit.
 static constexpr size_t kMaxBufferBytes = 0x7fff0000u;  // BUF_MAX_BYTES of the kernels
+
+// The workspace of the allocation-free forward (s2s_forward_device_noalloc):
+// one static array per GPU, S2S_NOALLOC_SCRATCH_BYTES long, which every
+// process that loads the library holds on each GPU it runs on until it ends.
+// Host code never uses the name `scratch` as an address (on the host it is a
+// stand-in for the device symbol): each device's address comes from
+// hipGetSymbolAddress at s2s_create, with that device current, and is kept in
+// g_scratch[device].
+#define S2S_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+static __device__ __align__(256) unsigned char scratch[S2S_NOALLOC_SCRATCH_BYTES];
+static constexpr int kMaxDevices = 64;
+static void *g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Looks up the current device's address of `scratch`, once per device.
+static int scratch_init(int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (dev < 0 || dev >= kMaxDevices) return fail("device index out of range for the workspace table");
+    if (g_scratch[dev]) return 0;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return fail(hip_msg("hipGetSymbolAddress(scratch)", e == hipSuccess ? hipErrorInvalidSymbol : e));
+    }
+    g_scratch[dev] = p;
+    return 0;
+}
 
 int s2s_ctx::alloc(AllocList &list, size_t floats, float **dev, const char *what, bool wide,
                    bool planned) {
@@ -988,6 +1017,7 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
 
     int dev = 0;
     HIPCHK("hipGetDevice", hipGetDevice(&dev));
+    if (scratch_init(dev)) return -1;
     s2s_ctx *ctx = new s2s_ctx();
     ctx->arch = A;
     ctx->c = A.embed;
@@ -1348,6 +1378,65 @@ uint64_t s2s_uploaded_bytes(const s2s_ctx *ctx) { return ctx ? ctx->uploaded : 0
 int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out) {
     if (!ctx) return fail("null context");
     HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    return ctx->forward_device(h, w, d_in, d_out);
+}
+
+// The forward with every intermediate buffer carved out of this GPU's static
+// workspace instead of the context's planned allocations: no hipMalloc,
+// hipFree or other allocating call (and no profiler events). The context's
+// own plan is left as it was. Calls that overlap on one GPU (other contexts,
+// other streams) share the one workspace and race.
+int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out) {
+    if (!ctx || !d_in || !d_out) return fail("s2s_forward_device_noalloc: null argument");
+    const int win = ctx->arch.window;
+    if (h < win || w < win) return ctx->forward_device(h, w, d_in, d_out);  // its error message
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    char *base = ctx->device >= 0 && ctx->device < kMaxDevices ? (char *)g_scratch[ctx->device] : nullptr;
+    if (!base) return fail("s2s_forward_device_noalloc: no workspace address for this device");
+    const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
+
+    // the context's plan, restored on every return
+    struct Saved {
+        s2s_ctx *c;
+        int bhp, bwp, ih, iw;
+        bool prof;
+        float *cur, *wk, *tmp, *body, *qkv, *o, *hid, *in_dev, *in4, *out_dev;
+        float *aux4, *auxp, *bic4, *bicf;
+        std::vector<float *> fplanes;
+        ~Saved() {
+            c->bhp = bhp; c->bwp = bwp; c->ih = ih; c->iw = iw; c->prof = prof;
+            c->cur = cur; c->wk = wk; c->tmp = tmp; c->body = body; c->qkv = qkv; c->o = o;
+            c->hid = hid; c->in_dev = in_dev; c->in4 = in4; c->out_dev = out_dev;
+            c->aux4 = aux4; c->auxp = auxp; c->bic4 = bic4; c->bicf = bicf;
+            c->fplanes.swap(fplanes);
+        }
+    } saved{ctx, ctx->bhp, ctx->bwp, ctx->ih, ctx->iw, ctx->prof, ctx->cur, ctx->wk, ctx->tmp,
+            ctx->body, ctx->qkv, ctx->o, ctx->hid, ctx->in_dev, ctx->in4, ctx->out_dev,
+            ctx->aux4, ctx->auxp, ctx->bic4, ctx->bicf, {}};
+    saved.fplanes.swap(ctx->fplanes);
+
+    std::vector<BufSpec> v;
+    ctx->body_specs(hp, wp, true, v);
+    ctx->image_specs(h, w, false, true, v);
+    size_t off = 0;
+    for (const BufSpec &b : v) off += (std::max<size_t>(b.floats, 1) * sizeof(float) + 255) / 256 * 256;
+    if (off > S2S_NOALLOC_SCRATCH_BYTES)
+        return fail("s2s_forward_device_noalloc: a " + std::to_string(h) + "x" + std::to_string(w) +
+                    " image needs " + std::to_string(off) + " bytes of workspace, above this "
+                    "entry's maximum of " + std::to_string(S2S_NOALLOC_SCRATCH_BYTES) +
+                    " bytes (use s2s_forward_device, or a smaller tile)");
+    off = 0;
+    for (const BufSpec &b : v) {
+        *b.dst = (float *)(base + off);
+        off += (std::max<size_t>(b.floats, 1) * sizeof(float) + 255) / 256 * 256;
+    }
+    if (ctx->arch.upsampler == S2S_PIXELSHUFFLE_AUX) ctx->bicf = ctx->fplanes[ctx->octaves];
+    // the carved plan is the current one for this call (plan_image keeps it)
+    ctx->bhp = hp;
+    ctx->bwp = wp;
+    ctx->ih = h;
+    ctx->iw = w;
+    ctx->prof = false;
     return ctx->forward_device(h, w, d_in, d_out);
 }
 

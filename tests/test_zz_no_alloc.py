@@ -1,0 +1,62 @@
+"""The allocation-free forward (s2s_forward_device_noalloc) against the
+allocating one (s2s_forward_device) through the C ABI: the same kernels on a
+static per-GPU workspace, so the outputs must agree bit for bit - on two calls
+in a row, the second on a smaller image (the workspace keeps the first call's
+contents), and for a head that writes the compressed model's aux planes. A
+plane past the workspace is refused with an error and the context still runs."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(pkg, be, arch, h, w, seed):
+    M, hip = pkg.model, pkg.hip
+    s = arch.scale
+    x = M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=seed)))
+    din = hip.DeviceBuffer.from_array(x)
+    want_buf = hip.DeviceBuffer(3 * h * s * w * s)
+    got_buf = hip.DeviceBuffer(3 * h * s * w * s)
+    be.forward_device(h, w, din.ptr, want_buf.ptr)
+    be.forward_device_noalloc(h, w, din.ptr, got_buf.ptr)
+    hip.stream_synchronize(be.stream())
+    want = want_buf.download((3, h * s, w * s))
+    got = got_buf.download((3, h * s, w * s))
+    for b in (din, want_buf, got_buf):
+        b.free()
+    return got, want
+
+
+@pytest.mark.parametrize("which", ["classical-x4", "compressed-x4"])
+def test_noalloc_forward_matches_the_allocating_one(pkg, which):
+    M = pkg.model
+    if which == "classical-x4":
+        arch = M.classical(4)
+    else:
+        arch = M.Arch(upsampler="pixelshuffle_aux", scale=4, embed=180, heads=6, depths=[2, 2])
+    be = pkg.HipBackend(arch, M.make_weights(arch, seed=7, perturb=True))
+    try:
+        for h, w, seed in [(120, 96, 1), (40, 56, 2)]:
+            got, want = _pair(pkg, be, arch, h, w, seed)
+            assert np.isfinite(got).all()
+            assert np.array_equal(got, want), (h, w)
+    finally:
+        be.close()
+
+
+def test_noalloc_refuses_a_plane_past_the_workspace(pkg):
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    be = pkg.HipBackend(arch, M.make_weights(arch, seed=1))
+    try:
+        h = w = 256
+        din = hip.DeviceBuffer(3 * h * w)
+        dout = hip.DeviceBuffer(3 * h * 4 * w * 4)
+        with pytest.raises(pkg.abi.S2SError, match="bytes of workspace, above this entry's maximum"):
+            be.forward_device_noalloc(h, w, din.ptr, dout.ptr)
+        din.free()
+        dout.free()
+        got, want = _pair(pkg, be, arch, 64, 64, 3)
+        assert np.array_equal(got, want)
+    finally:
+        be.close()
