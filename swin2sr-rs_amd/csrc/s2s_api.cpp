@@ -26,7 +26,7 @@
 #include <tuple>
 #include <vector>
 
-#include "../../include/swin2sr_hip.h"
+#include "swin2sr_hip.h"
 #include "s2s_kernels.h"
 
 namespace {

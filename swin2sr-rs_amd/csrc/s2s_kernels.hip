@@ -606,6 +606,26 @@ __device__ __forceinline__ float xrow_sum2(float a, float b) {
     return c + d;
 }
 
+// The two 32-lane halves of a wave exchanged on the VALU (gfx950
+// v_permlane32_swap with both operands a copy of x): `lo` gets lanes 0-31 of x
+// in both halves, `hi` lanes 32-63, so lo + hi (or max(lo, hi)) combines lane
+// l with lane l ^ 32 in every lane. Inline assembly for the reason above.
+__device__ __forceinline__ void halves(float x, float &lo, float &hi) {
+    lo = x;
+    hi = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+}
+__device__ __forceinline__ float half_sum(float x) {
+    float lo, hi;
+    halves(x, lo, hi);
+    return lo + hi;
+}
+__device__ __forceinline__ float half_max(float x) {
+    float lo, hi;
+    halves(x, lo, hi);
+    return fmaxf(lo, hi);
+}
+
 template <int KPW, int KS, int RB, int EPI>
 __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int NT = 256 * KS;
@@ -1482,7 +1502,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                 float qs = 0.f;
 #pragma unroll
                 for (int j = 0; j < NS; ++j) qs += qop[j] * qop[j];
-                qs += __shfl_xor(qs, 32, 64);
+                qs = half_sum(qs);
                 // ls / max(|q|, 1e-12) = ls * rsq(max(|q|^2, 1e-24)), one
                 // hardware reciprocal square root (1 ulp) instead of the
                 // correctly rounded sqrt and division sequences
@@ -1504,7 +1524,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                 float ks = 0.f;
 #pragma unroll
                 for (int j = 0; j < NS; ++j) ks += kop[kt][j] * kop[kt][j];
-                ks += __shfl_xor(ks, 32, 64);
+                ks = half_sum(ks);
                 const float ksc = __builtin_amdgcn_rsqf(fmaxf(ks, 1e-24f));
 #pragma unroll
                 for (int j = 0; j < NS; ++j) kop[kt][j] *= ksc;
@@ -1540,7 +1560,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = half_max(mx);
             float sum = 0.f;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
@@ -1551,7 +1571,7 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
                     if (!MSUM) sum += p;
                 }
             if (!MSUM) {
-                sum += __shfl_xor(sum, 32, 64);
+                sum = half_sum(sum);
                 inv = 1.0f / sum;
             }
 
@@ -1574,7 +1594,9 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
             if (MSUM) {
                 // row HD of O^T is the sum of the query's probabilities: lane
                 // half SUM_HH, register SUM_E
-                const float sum = __shfl(o[SUM_E], r + 32 * SUM_HH, 64);
+                float lo, hi;
+                halves(o[SUM_E], lo, hi);
+                const float sum = SUM_HH ? hi : lo;
                 inv = 1.0f / sum;
             }
         }

@@ -10,7 +10,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/swin2sr_hip.h"
+#include "swin2sr_hip.h"
 #include "s2s_kernels.h"
 
 namespace {

@@ -74,3 +74,54 @@ def test_benchmark_init_rules(pkg):
     assert 0.018 < s < 0.022
     bound = 1 / np.sqrt(180 * 9)
     assert np.abs(w["layers.0.conv.weight"]).max() <= bound
+
+
+def _rust_externs(text):
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    return re.findall(r"pub fn (s2s_[a-z0-9_]+)\(", block)
+
+
+def _rust_struct(text, name):
+    body = re.search(r"pub struct %s \{(.*?)\n\}" % name, text, re.S).group(1)
+    return re.findall(r"pub (\w+): ([^,\n]+),", body)
+
+
+def _c_struct(text, name):
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        m = re.match(r"(.+?)\s*(\*?)\s*(\w+)(\[[^\]]+\])?$", decl)
+        fields.append((m.group(3), (m.group(1) + m.group(2)).replace(" ", ""), m.group(4)))
+    return fields
+
+
+def test_rust_ffi_matches_the_header(pkg):
+    """The Rust binding a maintainer adds (swin2sr-rs_amd/rust/src/hip.rs) cannot be
+    compiled in this image: hold it against the header instead - every function it
+    declares is declared in include/swin2sr_hip.h and exported by the library, and
+    its #[repr(C)] structs have the C structs' fields in the same order and types."""
+    rs = (ROOT / "swin2sr-rs_amd" / "rust" / "src" / "hip.rs").read_text()
+    lib = pkg.load_library()
+    syms = declared_symbols()
+    fns = _rust_externs(rs)
+    assert len(fns) >= 15
+    for f in fns:
+        assert f in syms and hasattr(lib, f), f
+    ctype = {"int": "c_int", "float": "f32", "constchar*": "*const c_char",
+             "constfloat*": "*const f32", "int64_t": "i64"}
+    h = HEADER.read_text()
+    for rname, cname in (("S2sArch", "s2s_arch"), ("S2sTensor", "s2s_tensor")):
+        r = _rust_struct(rs, rname)
+        c = _c_struct(h, cname)
+        assert [n for n, _ in r] == [n for n, _, _ in c], (rname, r, c)
+        for (rn, rt), (cn, ct, arr) in zip(r, c):
+            want = ctype[ct]
+            if arr:
+                n = arr.strip("[]").replace("S2S_MAX_STAGES", "16")
+                want = f"[{want}; {n}]"
+            assert rt.strip() == want, (rn, rt, want)
