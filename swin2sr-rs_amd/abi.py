@@ -195,11 +195,17 @@ class HipBackend:
         fails with "out of memory"."""
         check(self._lib.s2s_set_alloc_limit(self._ctx, int(nbytes)), "s2s_set_alloc_limit")
 
-    def forward(self, h: int, w: int, input_adjusted: np.ndarray) -> np.ndarray:
+    def forward(self, h: int, w: int, input_adjusted: np.ndarray,
+                out: Optional[np.ndarray] = None) -> np.ndarray:
+        """`Backend::forward`: a new output image per call, as the crate's
+        backend returns a new Vec (or into `out`, a caller-owned float32
+        [3][h*s][w*s] array)."""
         x = np.ascontiguousarray(input_adjusted, dtype=np.float32)
         assert x.shape == (3, h, w), x.shape
         s = self.arch.scale
-        out = np.empty((3, h * s, w * s), np.float32)
+        if out is None:
+            out = np.empty((3, h * s, w * s), np.float32)
+        assert out.shape == (3, h * s, w * s) and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
         check(self._lib.s2s_forward(self._ctx, h, w, fptr(x), fptr(out)), "s2s_forward")
         return out
 

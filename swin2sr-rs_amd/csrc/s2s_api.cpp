@@ -14,6 +14,7 @@
 //   classical head (:601-623):   conv+lrelu(0.01), (conv3x3 + shuffle2) per
 //                                octave, conv_last + finish (denormalise, crop)
 #include <hip/hip_runtime.h>
+#include <immintrin.h>
 
 #include <algorithm>
 #include <cmath>
@@ -1440,6 +1441,37 @@ int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, fl
     return ctx->forward_device(h, w, d_in, d_out);
 }
 
+// Host copy out of the pinned staging image into the caller's buffer with
+// streaming (non-temporal) stores: the destination lines are written whole
+// without first being read into the cache, which roughly halves the memory
+// traffic of a plain copy of a buffer this size. AVX2 where the CPU has it,
+// memcpy otherwise.
+__attribute__((target("avx2"))) static void stream_copy_avx2(float *dst, const float *src, size_t n) {
+    size_t i = 0;
+    while (i < n && ((uintptr_t)(dst + i) & 31)) {
+        dst[i] = src[i];
+        ++i;
+    }
+    for (; i + 32 <= n; i += 32) {
+        const __m256 a = _mm256_loadu_ps(src + i), b = _mm256_loadu_ps(src + i + 8);
+        const __m256 c = _mm256_loadu_ps(src + i + 16), d = _mm256_loadu_ps(src + i + 24);
+        _mm256_stream_ps(dst + i, a);
+        _mm256_stream_ps(dst + i + 8, b);
+        _mm256_stream_ps(dst + i + 16, c);
+        _mm256_stream_ps(dst + i + 24, d);
+    }
+    for (; i < n; ++i) dst[i] = src[i];
+    _mm_sfence();
+}
+
+static void copy_out(float *dst, const float *src, size_t n) {
+    static const bool avx2 = __builtin_cpu_supports("avx2");
+    if (avx2 && n >= 1024)
+        stream_copy_avx2(dst, src, n);
+    else
+        std::memcpy(dst, src, n * sizeof(float));
+}
+
 // The host path: the caller's pageable input is copied into the context's
 // pinned staging image and uploaded as one DMA; the output comes back in
 // chunks, each copied out of the pinned image while the next is still in
@@ -1475,7 +1507,7 @@ int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out
                 rc = fail(hip_msg("hipEventSynchronize(output)", e));
             } else {
                 const size_t off = i * kChunk, len = std::min(kChunk, nout - off);
-                std::memcpy(out + off, ctx->pin_out + off, len * 4);
+                copy_out(out + off, ctx->pin_out + off, len);
             }
         }
         ctx->free_events.push_back(done[i]);
