@@ -59,12 +59,22 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "proj_ln_res": ("mfma", 2 * P * C * C, f * P * 3 * C),
         "fc1_gelu": ("mfma", 2 * P * Hd * C, f * P * (C + Hd)),
         "fc2_ln_res": ("mfma", 2 * P * C * Hd, f * P * (Hd + 2 * C)),
-        # the stage close: the 3x3 conv with the 1x1 folded in, + the residual
-        "conv3x3_stage": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),
+        # the body's 3x3 convs (the stage close with the 1x1 folded in, and
+        # conv_after_body) as Winograd F(2x2,3x3): the input transform (the
+        # plane in, 16 transform planes of P/4 tiles = 4 P C floats out), the
+        # 16 transform-position GEMMs (P/4 tiles x C x C multiply-adds each:
+        # 8 P C^2 FLOPs, the direct conv's 18 P C^2 / 2.25; M over V in place),
+        # then the output transform + bias + residual (M and the residual in,
+        # the plane out)
+        "conv3x3_stage_in": ("hbm", 0, f * P * 5 * C),
+        "conv3x3_stage": ("mfma", 8 * P * C * C, f * P * 8 * C),
+        "conv3x3_stage_out": ("hbm", 0, f * P * 6 * C),
+        "conv_after_body_in": ("hbm", 0, f * P * 5 * C),
+        "conv_after_body": ("mfma", 8 * P * C * C, f * P * 8 * C),
+        "conv_after_body_out": ("hbm", 0, f * P * 6 * C),
         # conv_first and patch_embed (its 1x1 folded into conv_first) + LayerNorm
         # in one VALU pass: two K = 27 convs
         "embed": ("valu", 2 * 2 * P * C * 27, f * P * (4 + 2 * C)),
-        "conv_after_body_res": ("mfma", 2 * P * C * 9 * C, f * P * 3 * C),
         "conv_before_upsample": ("mfma", 2 * P * F * 9 * C, f * P * (C + F)),
         "layernorm": ("hbm", 10 * P * C, f * P * 2 * C),
         "pad_input": ("hbm", 0, f * (3 * h * w + 4 * P)),

@@ -295,6 +295,19 @@ int s2s_test_ln_residual(int hw, int c, const float *x, const float *ln_w, const
 int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
                      const float *bias, int epilogue, const float *res, float slope, float *out);
 
+/* The body's C -> C 3x3 convs as the forward runs them for the released
+ * widths (the stage close, conv_after_body): Winograd F(2x2,3x3) - the
+ * weights transformed as at upload, the input transform, the 16
+ * transform-position GEMMs on the weight-stationary kernel, the output
+ * transform with the bias and the epilogue (0 store, 2 += res, 5
+ * LeakyReLU(slope)) - against the reference's direct cpu::conv3x3
+ * (src/cpu.rs:400-414; the reference's own CUDA backend runs these convs as
+ * Winograd F(4,3), src/gpu.rs:161-181). Channel-last `[h*w][C]` in and out;
+ * h and w even, c_in == c_out == C in {60, 120, 180}. */
+int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
+                              const float *bias, int epilogue, const float *res, float slope,
+                              float *out);
+
 /* The head's fused conv3x3 + pixel_shuffle(2) (reference cpu::conv3x3_shuffle2,
  * src/cpu.rs:502-542): weights `[4*feat][c_in][3][3]`, output channel-last
  * `[(2h)*(2w)][feat]`. */

@@ -83,6 +83,8 @@ EXPORTS = {
     "s2s_test_ln_residual": (C.c_int, [C.c_int, C.c_int, FP, FP, FP, FP, FP]),
     "s2s_test_conv3x3": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_int, FP,
                                    C.c_float, FP]),
+    "s2s_test_conv3x3_winograd": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP,
+                                            C.c_int, FP, C.c_float, FP]),
     "s2s_test_conv3x3_shuffle2": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, FP]),
 }
 
@@ -384,6 +386,18 @@ def test_conv3x3(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
     c32 = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
     check(lib.s2s_test_conv3x3(h, w, cin, cout, fptr(c32(x_hwc)), fptr(c32(wgt)), fptr(c32(bias)),
                                epilogue, fptr(c32(res)), slope, fptr(out)), "s2s_test_conv3x3")
+    return out
+
+
+def test_conv3x3_winograd(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
+    """The body's Winograd conv path (even planes, c_out % 4 == 0)."""
+    lib = load_library()
+    cout, cin = wgt.shape[0], wgt.shape[1]
+    out = np.empty((h * w, cout), np.float32)
+    c32 = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
+    check(lib.s2s_test_conv3x3_winograd(h, w, cin, cout, fptr(c32(x_hwc)), fptr(c32(wgt)),
+                                        fptr(c32(bias)), epilogue, fptr(c32(res)), slope, fptr(out)),
+          "s2s_test_conv3x3_winograd")
     return out
 
 

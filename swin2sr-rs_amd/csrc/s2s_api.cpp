@@ -122,7 +122,7 @@ struct s2s_ctx {
     // [2][9][4][C], the folded bias [C], patch_embed's LayerNorm
     float *emb_w = nullptr, *pe_b = nullptr, *pe_nw = nullptr, *pe_nb = nullptr;
     float *norm_w = nullptr, *norm_b = nullptr;
-    float *cab_w = nullptr, *cab_b = nullptr;  // conv_after_body [C][9*C]
+    float *cab_w = nullptr, *cab_b = nullptr;  // conv_after_body (body_conv_weights)
     std::vector<StageW> stages;
     float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C]
     std::vector<float *> up_w, up_b;           // octave convs, shuffle-permuted [4F][9*F]
@@ -152,7 +152,7 @@ struct s2s_ctx {
     // buffers planned for one padded plane (hp, wp)
     int bhp = 0, bwp = 0;
     AllocList body_allocs;
-    float *cur = nullptr, *wk = nullptr, *tmp = nullptr, *body = nullptr;
+    float *cur = nullptr, *wk = nullptr, *body = nullptr;
     float *qkv = nullptr, *o = nullptr, *hid = nullptr;
     // head / io buffers planned for one image (h, w)
     int ih = 0, iw = 0;
@@ -181,12 +181,15 @@ struct s2s_ctx {
     int upload(const std::vector<float> &host, float **dev);
     int alloc(AllocList &list, size_t floats, float **dev, const char *what, bool wide = false,
               bool planned = false);
-    // qkv buffer floats: the plane layout, or the attention unit layout
+    // qkv buffer floats: the plane layout, or the attention unit layout; it
+    // also holds the body's Winograd convs' transform-domain products (16
+    // planes of (hp/2)(wp/2) tiles x C) between blocks
     size_t qkv_floats(int hp, int wp) const {
         const size_t plane = (size_t)hp * wp * 3 * c;
-        return qkv_unit_layout(arch.heads, hd, c)
-                   ? std::max(plane, attn_unit_floats(hp, wp, arch.heads, hd))
-                   : plane;
+        const size_t q = qkv_unit_layout(arch.heads, hd, c)
+                             ? std::max(plane, attn_unit_floats(hp, wp, arch.heads, hd))
+                             : plane;
+        return wino_body(c) ? std::max(q, (size_t)4 * hp * wp * c) : q;
     }
     // The buffers of a padded plane's body, and of an image's head (with the
     // host path's device copies of the input and output when `io`); `bind`
@@ -203,6 +206,8 @@ struct s2s_ctx {
     int gemm(const char *name, const GemmArgs &g, int aload, int epi);
     int block_fwd(const BlockW &b, int hp, int wp, int shift, const float *x_in, float *x_out);
     int stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out);
+    int conv_body(const char *name, const float *in, int H, int W, const float *u,
+                  const float *bias, const float *res, float *out);
     int forward_device(int h, int w, const float *d_in, float *d_out);
     int head(int h, int w, float *d_out);
 };
@@ -314,14 +319,14 @@ int s2s_ctx::alloc(AllocList &list, size_t floats, float **dev, const char *what
 }
 
 // Body buffers for a padded plane: the activation, the in-stage working copy,
-// the conv scratch, conv_first's output (the body skip), qkv, the attention
-// output and the MLP hidden layer.
+// conv_first's output (the body skip), qkv (also the Winograd convs'
+// transform-domain products), the attention output (also the final norm's
+// output) and the MLP hidden layer.
 void s2s_ctx::body_specs(int hp, int wp, bool bind, std::vector<BufSpec> &v) {
     const size_t P = (size_t)hp * wp;
     auto d = [&](float **p) { return bind ? p : nullptr; };
     v.push_back({d(&cur), P * c, "cur", false});
     v.push_back({d(&wk), P * c, "work", false});
-    v.push_back({d(&tmp), P * c, "tmp", false});
     v.push_back({d(&body), P * c, "body", false});
     v.push_back({d(&qkv), qkv_floats(hp, wp), "qkv", true});
     v.push_back({d(&o), P * c, "attn", false});
@@ -560,7 +565,6 @@ int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *
 // One RSTB stage (reference src/gpu.rs:481-529): blocks, conv3x3, 1x1, + x_in.
 int s2s_ctx::stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out) {
     const StageW &st = stages[s];
-    const int P = hp * wp;
     const float *src = x_in;
     for (size_t bi = 0; bi < st.blocks.size(); ++bi) {
         const int shift = (bi % 2 == 1) ? arch.window / 2 : 0;
@@ -568,20 +572,53 @@ int s2s_ctx::stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out) {
         src = wk;
     }
     // The stage close (reference src/gpu.rs:526-528: the 3x3 conv, the 1x1
-    // patch_embed conv, the stage's residual) as one conv launch: the two
-    // convolutions are folded into one at upload, and the residual is its
-    // epilogue, element by element, so it may write over x_in; it goes through
-    // tmp only when the conv would read the plane it writes (no blocks).
-    float *dst = src == x_out ? tmp : x_out;
-    GemmArgs g = conv_gemm(src, hp, wp, c, st.conv_w, st.conv_b, dst, c, c);
-    g.res = x_in;
-    g.ldr = c;
-    if (gemm("conv3x3_stage", g, ALOAD_IM2COL, EPI_RES)) return -1;
-    if (dst != x_out) {
-        const hipError_t e = hipMemcpyAsync(x_out, dst, (size_t)P * c * 4, hipMemcpyDeviceToDevice, stream);
-        if (e != hipSuccess) return fail(hip_msg("hipMemcpyAsync(stage)", e));
+    // patch_embed conv, the stage's residual) as one conv: the two
+    // convolutions are folded into one at upload, and the residual is added
+    // by the output transform element by element, so it may write over x_in
+    // (the transform-domain GEMM has read all of its input before that).
+    return conv_body("conv3x3_stage", src, hp, wp, st.conv_w, st.conv_b, x_in, x_out);
+}
+
+// A C -> C 3x3 conv of the body (the stage close, conv_after_body), + bias +
+// residual. For the released widths (wino_body) as Winograd F(2x2,3x3): the
+// input transform V of every 2x2 output tile into the qkv buffer (free
+// between blocks), the 16 transform-position GEMMs M = V U^T on the
+// weight-stationary kernel (M over V in place), then the output transform
+// with the bias and the residual: 2.25x fewer multiplies than the direct conv,
+// the same result to fp32 rounding (the reference's own CUDA backend runs
+// these convs as Winograd F(4,3), src/gpu.rs:161-181). Other widths: the
+// direct implicit-GEMM conv with the residual as its epilogue.
+int s2s_ctx::conv_body(const char *name, const float *in, int H, int W, const float *u,
+                       const float *bias, const float *res, float *out) {
+    if (!wino_body(c)) {
+        // the epilogue adds the residual element by element; only a conv that
+        // reads the plane it writes (a stage with no blocks) goes through
+        // `o` (free between blocks)
+        float *dst = in == out ? o : out;
+        GemmArgs g = conv_gemm(in, H, W, c, u, bias, dst, c, c);
+        g.res = res;
+        g.ldr = c;
+        if (gemm(name, g, ALOAD_IM2COL, EPI_RES)) return -1;
+        if (dst != out) {
+            const hipError_t e = hipMemcpyAsync(out, dst, (size_t)H * W * c * 4, hipMemcpyDeviceToDevice, stream);
+            if (e != hipSuccess) return fail(hip_msg("hipMemcpyAsync(stage)", e));
+        }
+        return 0;
     }
-    return 0;
+    const int T = (H / 2) * (W / 2);
+    const long long n = (long long)T * (c / 4);
+    const dim3 tg((unsigned)((n + 255) / 256));
+    const std::string in_name = std::string(name) + "_in", out_name = std::string(name) + "_out";
+    if (run(in_name.c_str(), tg, dim3(256), [&] { return launch_wino_in(in, c, qkv, H, W, c, stream); }))
+        return -1;
+    GemmArgs g = rows_gemm(qkv, c, u, c, nullptr, qkv, c, T, c, c);
+    g.nb = 16;
+    g.a_bstride = g.o_bstride = (size_t)T * c;
+    g.b_bstride = (size_t)c * c;
+    if (gemm(name, g, ALOAD_ROWS, EPI_STORE)) return -1;
+    return run(out_name.c_str(), tg, dim3(256), [&] {
+        return launch_wino_out(qkv, bias, res, c, out, c, H, W, c, 0, 0.f, stream);
+    });
 }
 
 int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
@@ -604,16 +641,13 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out) {
             return launch_embed(in4, emb_w, cf_b, pe_b, pe_nw, pe_nb, body, cur, hp, wp, c, stream);
         }))
         return -1;
-    GemmArgs g{};
     for (int s = 0; s < arch.n_stages; ++s)
         if (stage_fwd(s, hp, wp, cur, cur)) return -1;
     if (run("layernorm", dim3((P + 15) / 16), dim3(256),
-            [&] { return launch_layernorm(cur, norm_w, norm_b, nullptr, tmp, P, c, stream); }))
+            [&] { return launch_layernorm(cur, norm_w, norm_b, nullptr, o, P, c, stream); }))
         return -1;
-    g = conv_gemm(tmp, hp, wp, c, cab_w, cab_b, cur, c, c);
-    g.res = body;
-    g.ldr = c;
-    if (gemm("conv_after_body_res", g, ALOAD_IM2COL, EPI_RES)) return -1;
+    // (the final norm lands in the attention output's plane, free after the blocks)
+    if (conv_body("conv_after_body", o, hp, wp, cab_w, cab_b, body, cur)) return -1;
     return head(h, w, d_out);
 }
 
@@ -784,6 +818,16 @@ std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vect
     return out;
 }
 
+// A body C -> C conv's weights [co][ci][3][3] as its kernels read them: the
+// Winograd transform [16][C][C] for the released widths, else the implicit
+// GEMM's [co][tap][ci_pad4].
+std::vector<float> body_conv_weights(const float *w, int C) {
+    if (!wino_body(C)) return conv_relayout(w, C, C, nullptr);
+    std::vector<float> u((size_t)16 * C * C);
+    wino_weights(w, C, C, u.data());
+    return u;
+}
+
 // co = 4ch + 2dy + dx  ->  row (2dy+dx)*feat + ch, so a 32-column tile of the
 // GEMM is 32 consecutive output channels of one sub-pixel (coalesced stores).
 std::vector<int> shuffle_perm(int feat) {
@@ -940,9 +984,11 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
     f += C;                     // conv_first's bias (the body skip)
     f += 2 * 9 * 4 * C + C;     // k_embed's two weight sets, the folded bias
     f += 4 * C;                 // patch_embed's LayerNorm, the final LayerNorm
-    f += C * 9 * C4 + C;        // conv_after_body
+    // the body's C -> C convs: Winograd weights [16][C][C] or direct [C][9][C4]
+    const uint64_t body_conv = wino_body(A.embed) ? 16 * C * C : C * 9 * C4;
+    f += body_conv + C;         // conv_after_body
     for (int s = 0; s < A.n_stages; ++s) {
-        f += C * 9 * C4 + C;    // the stage close (3x3 with the 1x1 folded in)
+        f += body_conv + C;     // the stage close (3x3 with the 1x1 folded in)
         const uint64_t per_block = 3 * C * C + 3 * C  // fused qkv and its bias
                                    + NH               // logit scale
                                    + C * C + C        // proj
@@ -1087,7 +1133,11 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
     rc = rc || up("patch_embed.norm.bias", {C}, &ctx->pe_nb);
     rc = rc || up("norm.weight", {C}, &ctx->norm_w);
     rc = rc || up("norm.bias", {C}, &ctx->norm_b);
-    rc = rc || upconv("conv_after_body.weight", C, C, &ctx->cab_w, nullptr);
+    {
+        const s2s_tensor *cw;
+        rc = rc || ts.get("conv_after_body.weight", {C, C, 3, 3}, &cw);
+        if (!rc) rc = ctx->upload(body_conv_weights(cw->data, C), &ctx->cab_w);
+    }
     rc = rc || up("conv_after_body.bias", {C}, &ctx->cab_b);
 
     // cpb scratch: the [heads][(2w-1)^2] MLP output before the gather
@@ -1128,7 +1178,7 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 for (size_t k = 0; k < kk; ++k) wf[(size_t)o * kk + k] = (float)acc[k];
                 bf[o] = (float)ab;
             }
-            rc = rc || ctx->upload(conv_relayout(wf.data(), C, C, nullptr), &st.conv_w);
+            rc = rc || ctx->upload(body_conv_weights(wf.data(), C), &st.conv_w);
             rc = rc || ctx->upload(bf, &st.conv_b);
         }
         st.blocks.resize(A.depths[s]);
@@ -1401,17 +1451,17 @@ int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, fl
         s2s_ctx *c;
         int bhp, bwp, ih, iw;
         bool prof;
-        float *cur, *wk, *tmp, *body, *qkv, *o, *hid, *in_dev, *in4, *out_dev;
+        float *cur, *wk, *body, *qkv, *o, *hid, *in_dev, *in4, *out_dev;
         float *aux4, *auxp, *bic4, *bicf;
         std::vector<float *> fplanes;
         ~Saved() {
             c->bhp = bhp; c->bwp = bwp; c->ih = ih; c->iw = iw; c->prof = prof;
-            c->cur = cur; c->wk = wk; c->tmp = tmp; c->body = body; c->qkv = qkv; c->o = o;
+            c->cur = cur; c->wk = wk; c->body = body; c->qkv = qkv; c->o = o;
             c->hid = hid; c->in_dev = in_dev; c->in4 = in4; c->out_dev = out_dev;
             c->aux4 = aux4; c->auxp = auxp; c->bic4 = bic4; c->bicf = bicf;
             c->fplanes.swap(fplanes);
         }
-    } saved{ctx, ctx->bhp, ctx->bwp, ctx->ih, ctx->iw, ctx->prof, ctx->cur, ctx->wk, ctx->tmp,
+    } saved{ctx, ctx->bhp, ctx->bwp, ctx->ih, ctx->iw, ctx->prof, ctx->cur, ctx->wk,
             ctx->body, ctx->qkv, ctx->o, ctx->hid, ctx->in_dev, ctx->in4, ctx->out_dev,
             ctx->aux4, ctx->auxp, ctx->bic4, ctx->bicf, {}};
     saved.fplanes.swap(ctx->fplanes);

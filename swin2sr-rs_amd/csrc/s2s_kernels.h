@@ -67,6 +67,12 @@ struct GemmArgs {
     int scale, oh, ow;
     float img_range, mean[3];
     int M, N, K;
+    // A batch of nb independent row GEMMs (0 or 1 = one; ALOAD_ROWS, store
+    // epilogue, no bias): A, B and out advance by a_bstride, b_bstride and
+    // o_bstride floats per batch (out may be A: each row's output is stored
+    // after that row has been read)
+    int nb;
+    size_t a_bstride, b_bstride, o_bstride;
 };
 
 // The weight-stationary token GEMM (k_bsgemm): out = epi(A B^T + bias) with A
@@ -88,6 +94,9 @@ struct BsArgs {
     int P, ngw;
     // EPI_QKV_WIN: plane hp x wp (nww windows per row), shift, head shape
     int hp, wp, nww, shift, heads, hd;
+    // batches (nb >= 1) and their strides in floats
+    int nb;
+    size_t a_bs, b_bs, o_bs;
 };
 
 // The attention kernels run the softmax in base 2: logits scaled by log2(e)
@@ -169,6 +178,24 @@ const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi);
 // profiler's rows), and the kernel family name it picks.
 void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block);
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out);
+// Winograd F(2x2,3x3) for a 3x3 stride-1 zero-pad-1 conv on a channel-last
+// H x W plane (H, W even, C % 4 == 0): wino_weights transforms the
+// [co][ci][3][3] weights to U = G g G^T, the GEMM's B [16][co][round4(ci)]
+// (double accumulation, rounded once); launch_wino_in writes V = B^T d B of
+// every 2x2 output tile's 4x4 input patch (zero outside the plane) as
+// [16][T][C] for the T = (H/2)(W/2) tiles; a batch of 16 row GEMMs M[b] =
+// V[b] U[b]^T (over M's own buffer); launch_wino_out transforms M back
+// (Y = A^T M A), adds the bias, then the residual `res` [H*W][ldr] if set,
+// then LeakyReLU(slope) if `lrelu`, into out [H*W][ldo].
+void wino_weights(const float *w, int co, int ci, float *out);
+// The body's C -> C convs take the Winograd path when the batched GEMM runs on
+// the weight-stationary kernel with every column in one workgroup (so it may
+// write M over V in place): C in {60, 120, 180}, every released width.
+inline bool wino_body(int c) { return c == 60 || c == 120 || c == 180; }
+hipError_t launch_wino_in(const float *in, int ldi, float *v, int H, int W, int C, hipStream_t st);
+hipError_t launch_wino_out(const float *m, const float *bias, const float *res, int ldr,
+                           float *out, int ldo, int H, int W, int C, int lrelu, float slope,
+                           hipStream_t st);
 unsigned attention_grid(const AttnArgs &g);
 hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,
                             hipStream_t st);

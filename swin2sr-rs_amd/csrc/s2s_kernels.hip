@@ -682,8 +682,18 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const int kq = KS == 1 ? 0 : wave >> 2;
     const int j = lane & 15;
     const int q = lane >> 4;
-    const int ng = blockIdx.x / g.P;
-    const int p = blockIdx.x - ng * g.P;
+    // workgroup (batch bt, column group ng, slot p); a batch's A, B and out
+    // start bt strides in
+    const int ngc = (g.N + g.ngw - 1) / g.ngw;
+    const int grp = blockIdx.x / g.P;
+    const int p = blockIdx.x - grp * g.P;
+    const int bt = grp / ngc;
+    const int ng = grp - bt * ngc;
+    if (g.nb > 1) {
+        g.A += bt * g.a_bs;
+        g.B += bt * g.b_bs;
+        g.out += bt * g.o_bs;
+    }
     const int gc0 = ng * g.ngw;
     const int gw = min(gc0 + g.ngw, g.N) - gc0;  // columns in this group
     const int kbase = kq * KPW;
@@ -2480,6 +2490,7 @@ static int cu_count() {
 // over two wave sets).
 static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks) {
     if (aload != ALOAD_ROWS || epi == EPI_SHUFFLE) return false;
+    if (g.nb > 1 && (epi != EPI_STORE || g.bias)) return false;
     if (g.lda % 4 || g.ldb % 4 || g.M <= 0 || g.N <= 0) return false;
     // each lane stores runs of 4 (2) consecutive columns as one float4 (float2):
     // the column groups and the row strides are multiples of 4
@@ -2525,11 +2536,12 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     }
     const int ng = (g.N + 191) / 192;
     const int ngw = (g.N + ng - 1) / ng;
+    const int nb = std::max(g.nb, 1);
     const int ntask = (g.M + 16 * RB - 1) / (16 * RB);
-    int P = per_cu * cu_count() / ng;
+    int P = per_cu * cu_count() / (ng * nb);
     if (P >= 8) P -= P % 8;
     P = std::max(1, std::min(P, ntask));
-    const dim3 grid((unsigned)(P * ng));
+    const dim3 grid((unsigned)(P * ng * nb));
     if (grid_out) *grid_out = grid;
     if (!launch) return hipSuccess;
     BsArgs a{};
@@ -2556,6 +2568,10 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     a.shift = g.shift;
     a.heads = g.heads;
     a.hd = g.hd;
+    a.nb = nb;
+    a.a_bs = g.a_bstride;
+    a.b_bs = g.b_bstride;
+    a.o_bs = g.o_bstride;
     hipLaunchKernelGGL((k_bsgemm<KPW, KS, RB, EPI>), grid, dim3(256 * KS), 0, st, a);
     return hipGetLastError();
 }
@@ -2583,10 +2599,11 @@ static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool laun
 
 // Rows per task: 32 (twice the MFMA work per task for the same per-task
 // overhead) where the task count still divides well over the workgroups
-// (several column groups) and the epilogue leaves room in the register file;
+// (several column groups, or batches) and the epilogue leaves room in the
+// register file;
 // 16 otherwise.
 static int bs_rb(const GemmArgs &g, int ks, int epi) {
-    const int ng = (g.N + 191) / 192;
+    const int ng = (g.N + 191) / 192 * std::max(g.nb, 1);  // column groups x batches
     const bool simple = epi == EPI_STORE || epi == EPI_GELU || epi == EPI_LRELU || epi == EPI_QKV_WIN;
     (void)ks;
     return (ng >= 2 && simple) ? 2 : 1;
@@ -2623,6 +2640,7 @@ void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *bloc
 hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
     int kpw, ks;
     if (bs_eligible(g, aload, epi, &kpw, &ks)) return run_bs_any(g, kpw, ks, epi, st, true, nullptr);
+    if (g.nb > 1) return hipErrorInvalidValue;  // batches run on k_bsgemm only
     return launch_gemm_variant(g, aload, epi, gemm_pick(g, aload, epi), st);
 }
 
@@ -2764,6 +2782,154 @@ hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *
     hipLaunchKernelGGL(k_cpb_gather, dim3((total + 255) / 256), dim3(256), 0, st, tab, cpbt, win,
                        heads);
     return hipGetLastError();
+}
+
+// Winograd F(2x2,3x3) input transform: tile (ty, tx), channels 4c4..4c4+3.
+// The tile's 4x4 input patch d (rows 2ty-1 .. 2ty+2, columns 2tx-1 ..
+// 2tx+2, zero outside the plane) to V = B^T d B with
+// B^T = [1 0 -1 0; 0 1 1 0; 0 -1 1 0; 0 1 0 -1], rows then columns, stored as
+// V[4 xi + nu][tile][c]. One thread per (tile, float4 of channels);
+// consecutive threads read and write consecutive float4s.
+__global__ void k_wino_in(const float *__restrict__ in, int ldi, float *__restrict__ v, int H,
+                          int W, int C, int T) {
+    const int c4n = C >> 2;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)T * c4n) return;
+    const int tile = (int)(i / c4n);
+    const int c = 4 * (int)(i - (long long)tile * c4n);
+    const int tw = W >> 1;
+    const int ty = tile / tw, tx = tile - (tile / tw) * tw;
+    float4 d[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int y = 2 * ty - 1 + r, x = 2 * tx - 1 + q;
+            d[r][q] = ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W)
+                          ? *reinterpret_cast<const float4 *>(in + ((size_t)y * W + x) * ldi + c)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    const size_t plane = (size_t)T * C;
+    float *out = v + (size_t)tile * C + c;
+    auto add = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
+    auto sub = [](float4 x, float4 y) { return make_float4(x.x - y.x, x.y - y.y, x.z - y.z, x.w - y.w); };
+#pragma unroll
+    for (int xi = 0; xi < 4; ++xi) {
+        // row xi of B^T d, then its four columns times B
+        float4 t[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            t[q] = xi == 0 ? sub(d[0][q], d[2][q])
+                 : xi == 1 ? add(d[1][q], d[2][q])
+                 : xi == 2 ? sub(d[2][q], d[1][q])
+                           : sub(d[1][q], d[3][q]);
+        *reinterpret_cast<float4 *>(out + (4 * xi + 0) * plane) = sub(t[0], t[2]);
+        *reinterpret_cast<float4 *>(out + (4 * xi + 1) * plane) = add(t[1], t[2]);
+        *reinterpret_cast<float4 *>(out + (4 * xi + 2) * plane) = sub(t[2], t[1]);
+        *reinterpret_cast<float4 *>(out + (4 * xi + 3) * plane) = sub(t[1], t[3]);
+    }
+}
+
+hipError_t launch_wino_in(const float *in, int ldi, float *v, int H, int W, int C, hipStream_t st) {
+    if (H % 2 || W % 2 || C % 4 || ldi % 4) return hipErrorInvalidValue;
+    const int T = (H / 2) * (W / 2);
+    const long long n = (long long)T * (C / 4);
+    hipLaunchKernelGGL(k_wino_in, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, ldi, v,
+                       H, W, C, T);
+    return hipGetLastError();
+}
+
+// Winograd F(2x2,3x3) output transform: tile (ty, tx), channels 4c4..4c4+3:
+// M[b][tile][c] for the 16 positions b = 4 xi + nu, Y = A^T M A with
+// A^T = [1 1 1 0; 0 1 -1 -1] (rows, then columns), + bias, + the residual,
+// then LeakyReLU when asked, into the 2x2 output pixels (2ty + r, 2tx + c).
+// One thread per (tile, float4 of channels); M's 16 planes are read with
+// consecutive threads on consecutive float4s.
+__global__ void k_wino_out(const float *__restrict__ m, const float *__restrict__ bias,
+                           const float *__restrict__ res, int ldr, float *__restrict__ out,
+                           int ldo, int W, int C, int T, int lrelu, float slope) {
+    const int c4n = C >> 2;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)T * c4n) return;
+    const int tile = (int)(i / c4n);
+    const int c = 4 * (int)(i - (long long)tile * c4n);
+    const size_t plane = (size_t)T * C;
+    float4 mv[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b)
+        mv[b] = *reinterpret_cast<const float4 *>(m + b * plane + (size_t)tile * C + c);
+    const float4 bv = bias ? *reinterpret_cast<const float4 *>(bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int tw = W >> 1;
+    const int ty = tile / tw, tx = tile - (tile / tw) * tw;
+    auto comp = [&](int e, float *y) __attribute__((always_inline)) {
+        float t0[4], t1[4];
+#pragma unroll
+        for (int nu = 0; nu < 4; ++nu) {
+            const float m0 = (&mv[0 * 4 + nu].x)[e], m1 = (&mv[1 * 4 + nu].x)[e];
+            const float m2 = (&mv[2 * 4 + nu].x)[e], m3 = (&mv[3 * 4 + nu].x)[e];
+            t0[nu] = m0 + m1 + m2;
+            t1[nu] = m1 - m2 - m3;
+        }
+        y[0] = t0[0] + t0[1] + t0[2];
+        y[1] = t0[1] - t0[2] - t0[3];
+        y[2] = t1[0] + t1[1] + t1[2];
+        y[3] = t1[1] - t1[2] - t1[3];
+    };
+    float yx[4], yy[4], yz[4], yw[4];
+    comp(0, yx);
+    comp(1, yy);
+    comp(2, yz);
+    comp(3, yw);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const size_t px = (size_t)(2 * ty + (q >> 1)) * W + 2 * tx + (q & 1);
+        float4 v = make_float4(yx[q] + bv.x, yy[q] + bv.y, yz[q] + bv.z, yw[q] + bv.w);
+        if (res) {
+            const float4 r = *reinterpret_cast<const float4 *>(res + px * ldr + c);
+            v.x += r.x;
+            v.y += r.y;
+            v.z += r.z;
+            v.w += r.w;
+        }
+        if (lrelu) {
+            v.x = v.x < 0.f ? v.x * slope : v.x;
+            v.y = v.y < 0.f ? v.y * slope : v.y;
+            v.z = v.z < 0.f ? v.z * slope : v.z;
+            v.w = v.w < 0.f ? v.w * slope : v.w;
+        }
+        *reinterpret_cast<float4 *>(out + px * ldo + c) = v;
+    }
+}
+
+hipError_t launch_wino_out(const float *m, const float *bias, const float *res, int ldr,
+                           float *out, int ldo, int H, int W, int C, int lrelu, float slope,
+                           hipStream_t st) {
+    if (H % 2 || W % 2 || C % 4 || ldo % 4 || (res && ldr % 4)) return hipErrorInvalidValue;
+    const int T = (H / 2) * (W / 2);
+    const long long n = (long long)T * (C / 4);
+    hipLaunchKernelGGL(k_wino_out, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, bias,
+                       res, ldr, out, ldo, W, C, T, lrelu, slope);
+    return hipGetLastError();
+}
+
+// U = G g G^T per (co, ci), G = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1],
+// accumulated in double and rounded once, as the GEMM's B: [16][co][round4(ci)]
+// with batch b = 4 xi + nu.
+void wino_weights(const float *w, int co, int ci, float *out) {
+    static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    const int cp = (ci + 3) / 4 * 4;
+    for (size_t i = 0; i < (size_t)16 * co * cp; ++i) out[i] = 0.f;
+    for (int o = 0; o < co; ++o)
+        for (int i = 0; i < ci; ++i) {
+            const float *g = w + ((size_t)o * ci + i) * 9;
+            for (int xi = 0; xi < 4; ++xi)
+                for (int nu = 0; nu < 4; ++nu) {
+                    double u = 0.0;
+                    for (int a = 0; a < 3; ++a)
+                        for (int b = 0; b < 3; ++b) u += G[xi][a] * (double)g[3 * a + b] * G[nu][b];
+                    out[((size_t)(4 * xi + nu) * co + o) * cp + i] = (float)u;
+                }
+        }
 }
 
 hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,

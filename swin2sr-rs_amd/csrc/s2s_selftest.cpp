@@ -178,6 +178,27 @@ extern "C" int s2s_selftest(const s2s_arch *arch, const s2s_tensor *tensors, siz
         }
     }
 
+    // the body's Winograd F(2x2,3x3) conv (the stage close, conv_after_body)
+    // at the released widths and the checkpoint's own, on even planes (one
+    // that is all border, and planes wider than one 64-lane wavefront)
+    {
+        const int shapes[4][3] = {{2, 4, 60}, {34, 40, 120}, {16, 70, 180}, {8, 10, arch->embed}};
+        for (auto &sh : shapes) {
+            const int h = sh[0], w = sh[1], c = sh[2];
+            if (!wino_body(c)) continue;
+            std::vector<float> x = seq((size_t)h * w * c, 0.3f), wgt = seq((size_t)c * c * 9, 1.1f),
+                               b = seq(c, 2.2f), res = seq((size_t)h * w * c, 0.9f), got((size_t)h * w * c);
+            for (float &v : wgt) v /= std::sqrt(9.0f * c);
+            CHECK(s2s_test_conv3x3_winograd(h, w, c, c, x.data(), wgt.data(), b.data(), 2, res.data(),
+                                            0.f, got.data()));
+            std::vector<double> want = conv3x3(x, h, w, c, c, wgt, b);
+            for (size_t i = 0; i < want.size(); ++i) want[i] += res[i];
+            CHECK(cnt.ok(close("winograd conv3x3 " + std::to_string(c) + "->" + std::to_string(c) +
+                                   " + residual at " + std::to_string(h) + "x" + std::to_string(w),
+                               want, got, tol)));
+        }
+    }
+
     // conv3x3 + pixel_shuffle(2) (the head's octave) at the reference's shapes
     {
         const int shapes[5][4] = {{4, 3, 5, 7}, {4, 3, 1, 6}, {6, 24, 4, 5}, {2, 2, 3, 61}, {2, 2, 1, 1025}};

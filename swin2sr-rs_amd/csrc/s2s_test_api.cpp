@@ -327,6 +327,50 @@ int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const fl
     return 0;
 }
 
+int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
+                              const float *bias, int epilogue, const float *res, float slope,
+                              float *out) {
+    if (epilogue != 0 && epilogue != 2 && epilogue != 5) return fail("winograd epilogue must be 0, 2 or 5");
+    if (epilogue == 2 && !res) return fail("residual epilogue needs res");
+    if (h <= 0 || w <= 0 || h % 2 || w % 2) return fail("the Winograd conv needs an even plane");
+    if (!wino_body(c_in) || c_out != c_in)
+        return fail("the Winograd conv is the body's C -> C conv, C in {60, 120, 180}");
+    const size_t P = (size_t)h * w, T = P / 4;
+    std::vector<float> u((size_t)16 * c_out * c_in);
+    wino_weights(wgt, c_out, c_in, u.data());
+    Dev d;
+    const float *dx = d.up(x, P * c_in), *du = d.up(u.data(), u.size());
+    const float *db = bias ? d.up(bias, c_out) : nullptr;
+    const float *dr = res ? d.up(res, P * c_out) : nullptr;
+    // V [16][T][C], then M [16][T][C] over it row for row, as the forward does
+    float *dv = d.alloc<float>(16 * T * c_in), *dout = d.alloc<float>(P * c_out);
+    if (!dx || !du || !dv || !dout || (bias && !db) || (res && !dr))
+        return fail("hipMalloc failed: out of memory");
+    GemmArgs g{};
+    g.A = dv;
+    g.lda = c_in;
+    g.B = du;
+    g.ldb = c_in;
+    g.out = dv;
+    g.ldo = c_out;
+    g.M = (int)T;
+    g.N = c_out;
+    g.K = c_in;
+    g.nb = 16;
+    g.a_bstride = T * c_in;
+    g.o_bstride = T * c_out;
+    g.b_bstride = (size_t)c_out * c_in;
+    hipError_t e = launch_wino_in(dx, c_in, dv, h, w, c_in, 0);
+    if (e == hipSuccess) e = launch_gemm(g, ALOAD_ROWS, EPI_STORE, 0);
+    if (e == hipSuccess)
+        e = launch_wino_out(dv, db, epilogue == 2 ? dr : nullptr, c_out, dout, c_out, h, w, c_out,
+                            epilogue == 5, slope, 0);
+    if (int rc = finish(e, "winograd conv3x3")) return rc;
+    if (hipMemcpy(out, dout, P * c_out * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
 int s2s_test_conv3x3_shuffle2(int h, int w, int c_in, int feat, const float *x,
                               const float *wgt, const float *bias, float *out) {
     const int cp = round4(c_in);

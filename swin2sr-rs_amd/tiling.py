@@ -99,7 +99,9 @@ def _plan_terms(arch: M.Arch, h: int, w: int):
     qkv = P * 3 * c
     if _unit_layout(arch):
         qkv = max(qkv, P * ((arch.heads + 1) // 2) * (6 * arch.head_dim + 2))
-    terms = [P * c] * 4 + [qkv, P * c, P * arch.mlp_ratio * c]
+    if c in (60, 120, 180):
+        qkv = max(qkv, 4 * P * c)  # the Winograd convs' 16 transform planes of P/4 tiles
+    terms = [P * c] * 3 + [qkv, P * c, P * arch.mlp_ratio * c]
     terms += [3 * h * w, 3 * h * s * w * s, P * 4]
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
         terms += [P * 4 ** o * f for o in range(arch.octaves - _fused_octaves(arch) + 1)]
@@ -124,7 +126,9 @@ def per_pixel_floats(arch: M.Arch) -> int:
     qkv = 3 * c
     if _unit_layout(arch):
         qkv = max(qkv, ((arch.heads + 1) // 2) * (6 * arch.head_dim + 2))
-    body = 4 * c + qkv + c + arch.mlp_ratio * c
+    if c in (60, 120, 180):
+        qkv = max(qkv, 4 * c)
+    body = 3 * c + qkv + c + arch.mlp_ratio * c
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
         head = sum(f * 4 ** o for o in range(arch.octaves - _fused_octaves(arch) + 1))
         if arch.upsampler == "pixelshuffle_aux":

@@ -194,6 +194,34 @@ def test_conv3x3(pkg, orc, h, w, cin, cout, epi):
     assert err < 5e-5, err
 
 
+@pytest.mark.parametrize("h,w,c", [(2, 2, 180), (6, 10, 60), (34, 40, 120), (20, 70, 180),
+                                   (72, 80, 180), (264, 264, 180), (72, 72, 60)])
+@pytest.mark.parametrize("epi", [0, 2, 5])
+def test_conv3x3_winograd(pkg, orc, h, w, c, epi):
+    """The body's C -> C convs (the stage close, conv_after_body) run as
+    Winograd F(2x2,3x3) at the released widths: against the oracle's direct
+    conv, at the same bar as the direct kernel, up to the headline plane
+    (264 x 264 x 180, the borders' zero padding included); a 2x2 plane is
+    all border."""
+    cin = cout = c
+    r = rng(h * w + cin + cout + epi + 7)
+    x = r.standard_normal((cin, h, w), dtype=np.float32)
+    wt = (r.standard_normal((cout, cin, 3, 3), dtype=np.float32) / np.sqrt(9 * cin)).astype(np.float32)
+    b = r.standard_normal(cout, dtype=np.float32)
+    res = r.standard_normal((cout, h, w), dtype=np.float32)
+    base = orc.conv3x3(x, wt, b)
+    if epi == 0:
+        want = base
+    elif epi == 2:
+        want = base + res
+    else:
+        want = np.where(base < 0, base * np.float32(0.01), base)
+    got = pkg.abi.test_conv3x3_winograd(nchw_to_hwc(x), h, w, wt, b, epilogue=epi,
+                                        res=nchw_to_hwc(res) if epi == 2 else None, slope=0.01)
+    err = np.abs(hwc_to_nchw(got, h, w) - want).max()
+    assert err < 5e-5, err
+
+
 @pytest.mark.parametrize("cin,feat,h,w", [(4, 3, 5, 7), (4, 4, 1, 6), (6, 24, 4, 5), (64, 64, 9, 70),
                                           (8, 8, 3, 61)])
 def test_conv3x3_shuffle2(pkg, orc, cin, feat, h, w):
