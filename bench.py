@@ -51,6 +51,7 @@ def kernel_work(arch, h, w, hp=None, wp=None):
     if hp is None:
         hp, wp = (h // win + 1) * win, (w // win + 1) * win
     P = hp * wp
+    VT = 36 * ((hp + 3) // 4) * ((wp + 3) // 4)  # rows of the 36 Winograd GEMMs
     Hd = arch.mlp_ratio * C
     f = 4
     work = {
@@ -60,18 +61,18 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "fc1_gelu": ("mfma", 2 * P * Hd * C, f * P * (C + Hd)),
         "fc2_ln_res": ("mfma", 2 * P * C * Hd, f * P * (Hd + 2 * C)),
         # the body's 3x3 convs (the stage close with the 1x1 folded in, and
-        # conv_after_body) as Winograd F(2x2,3x3): the input transform (the
-        # plane in, 16 transform planes of P/4 tiles = 4 P C floats out), the
-        # 16 transform-position GEMMs (P/4 tiles x C x C multiply-adds each:
-        # 8 P C^2 FLOPs, the direct conv's 18 P C^2 / 2.25; M over V in place),
-        # then the output transform + bias + residual (M and the residual in,
-        # the plane out)
-        "conv3x3_stage_in": ("hbm", 0, f * P * 5 * C),
-        "conv3x3_stage": ("mfma", 8 * P * C * C, f * P * 8 * C),
-        "conv3x3_stage_out": ("hbm", 0, f * P * 6 * C),
-        "conv_after_body_in": ("hbm", 0, f * P * 5 * C),
-        "conv_after_body": ("mfma", 8 * P * C * C, f * P * 8 * C),
-        "conv_after_body_out": ("hbm", 0, f * P * 6 * C),
+        # conv_after_body) as Winograd F(4x4,3x3) over T = ceil(hp/4) ceil(wp/4)
+        # tiles: the input transform (the plane in, 36 transform planes of T
+        # tiles out), the 36 transform-position GEMMs (T x C x C multiply-adds
+        # each: 72 T C^2 FLOPs, the direct conv's 18 P C^2 / 4 when 4 divides
+        # the plane; M over V in place), then the output transform + bias +
+        # residual (M and the residual in, the plane out)
+        "conv3x3_stage_in": ("hbm", 0, f * (P * C + VT * C)),
+        "conv3x3_stage": ("mfma", 2 * VT * C * C, f * (2 * VT * C + 36 * C * C)),
+        "conv3x3_stage_out": ("hbm", 0, f * (VT * C + 2 * P * C)),
+        "conv_after_body_in": ("hbm", 0, f * (P * C + VT * C)),
+        "conv_after_body": ("mfma", 2 * VT * C * C, f * (2 * VT * C + 36 * C * C)),
+        "conv_after_body_out": ("hbm", 0, f * (VT * C + 2 * P * C)),
         # conv_first and patch_embed (its 1x1 folded into conv_first) + LayerNorm
         # in one VALU pass: two K = 27 convs
         "embed": ("valu", 2 * 2 * P * C * 27, f * P * (4 + 2 * C)),

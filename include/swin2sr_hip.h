@@ -296,14 +296,14 @@ int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const fl
                      const float *bias, int epilogue, const float *res, float slope, float *out);
 
 /* The body's C -> C 3x3 convs as the forward runs them for the released
- * widths (the stage close, conv_after_body): Winograd F(2x2,3x3) - the
- * weights transformed as at upload, the input transform, the 16
+ * widths (the stage close, conv_after_body): Winograd F(4x4,3x3) - the
+ * weights transformed as at upload, the input transform, the 36
  * transform-position GEMMs on the weight-stationary kernel, the output
  * transform with the bias and the epilogue (0 store, 2 += res, 5
  * LeakyReLU(slope)) - against the reference's direct cpu::conv3x3
  * (src/cpu.rs:400-414; the reference's own CUDA backend runs these convs as
- * Winograd F(4,3), src/gpu.rs:161-181). Channel-last `[h*w][C]` in and out;
- * h and w even, c_in == c_out == C in {60, 120, 180}. */
+ * Winograd with 6x6 tiles, src/gpu.rs:161-181). Channel-last `[h*w][C]` in
+ * and out; any h, w >= 1, c_in == c_out == C in {60, 120, 180}. */
 int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
                               const float *bias, int epilogue, const float *res, float slope,
                               float *out);

@@ -390,7 +390,7 @@ def test_conv3x3(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
 
 
 def test_conv3x3_winograd(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
-    """The body's Winograd conv path (even planes, c_out % 4 == 0)."""
+    """The body's Winograd F(4x4,3x3) conv path (c_in == c_out in {60, 120, 180})."""
     lib = load_library()
     cout, cin = wgt.shape[0], wgt.shape[1]
     out = np.empty((h * w, cout), np.float32)

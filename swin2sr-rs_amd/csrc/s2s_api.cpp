@@ -182,14 +182,14 @@ struct s2s_ctx {
     int alloc(AllocList &list, size_t floats, float **dev, const char *what, bool wide = false,
               bool planned = false);
     // qkv buffer floats: the plane layout, or the attention unit layout; it
-    // also holds the body's Winograd convs' transform-domain products (16
-    // planes of (hp/2)(wp/2) tiles x C) between blocks
+    // also holds the body's Winograd convs' transform-domain products (36
+    // planes of wino_tiles(hp, wp) tiles x C) between blocks
     size_t qkv_floats(int hp, int wp) const {
         const size_t plane = (size_t)hp * wp * 3 * c;
         const size_t q = qkv_unit_layout(arch.heads, hd, c)
                              ? std::max(plane, attn_unit_floats(hp, wp, arch.heads, hd))
                              : plane;
-        return wino_body(c) ? std::max(q, (size_t)4 * hp * wp * c) : q;
+        return wino_body(c) ? std::max(q, WINO_POS * wino_tiles(hp, wp) * c) : q;
     }
     // The buffers of a padded plane's body, and of an image's head (with the
     // host path's device copies of the input and output when `io`); `bind`
@@ -580,14 +580,14 @@ int s2s_ctx::stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out) {
 }
 
 // A C -> C 3x3 conv of the body (the stage close, conv_after_body), + bias +
-// residual. For the released widths (wino_body) as Winograd F(2x2,3x3): the
-// input transform V of every 2x2 output tile into the qkv buffer (free
-// between blocks), the 16 transform-position GEMMs M = V U^T on the
-// weight-stationary kernel (M over V in place), then the output transform
-// with the bias and the residual: 2.25x fewer multiplies than the direct conv,
-// the same result to fp32 rounding (the reference's own CUDA backend runs
-// these convs as Winograd F(4,3), src/gpu.rs:161-181). Other widths: the
-// direct implicit-GEMM conv with the residual as its epilogue.
+// residual. For the released widths (wino_body) as Winograd F(4x4,3x3): the
+// input transform V of every 4x4 output tile into the qkv buffer (free
+// between blocks), the 36 transform-position GEMMs M = V U^T as one batched
+// launch of the weight-stationary kernel (M over V in place), then the output
+// transform with the bias and the residual: 4x fewer multiplies than the
+// direct conv, the same map to fp32 rounding (the reference's own CUDA backend
+// runs these convs as Winograd with 6x6 tiles, src/gpu.rs:161-181). Other
+// widths: the direct implicit-GEMM conv with the residual as its epilogue.
 int s2s_ctx::conv_body(const char *name, const float *in, int H, int W, const float *u,
                        const float *bias, const float *res, float *out) {
     if (!wino_body(c)) {
@@ -605,18 +605,17 @@ int s2s_ctx::conv_body(const char *name, const float *in, int H, int W, const fl
         }
         return 0;
     }
-    const int T = (H / 2) * (W / 2);
-    const long long n = (long long)T * (c / 4);
-    const dim3 tg((unsigned)((n + 255) / 256));
+    const int T = (int)wino_tiles(H, W);
     const std::string in_name = std::string(name) + "_in", out_name = std::string(name) + "_out";
-    if (run(in_name.c_str(), tg, dim3(256), [&] { return launch_wino_in(in, c, qkv, H, W, c, stream); }))
+    if (run(in_name.c_str(), dim3(wino_in_grid(H, W, c)), dim3(256),
+            [&] { return launch_wino_in(in, c, qkv, H, W, c, stream); }))
         return -1;
     GemmArgs g = rows_gemm(qkv, c, u, c, nullptr, qkv, c, T, c, c);
-    g.nb = 16;
+    g.nb = WINO_POS;
     g.a_bstride = g.o_bstride = (size_t)T * c;
     g.b_bstride = (size_t)c * c;
     if (gemm(name, g, ALOAD_ROWS, EPI_STORE)) return -1;
-    return run(out_name.c_str(), tg, dim3(256), [&] {
+    return run(out_name.c_str(), dim3(wino_out_grid(H, W, c)), dim3(256), [&] {
         return launch_wino_out(qkv, bias, res, c, out, c, H, W, c, 0, 0.f, stream);
     });
 }
@@ -819,11 +818,11 @@ std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vect
 }
 
 // A body C -> C conv's weights [co][ci][3][3] as its kernels read them: the
-// Winograd transform [16][C][C] for the released widths, else the implicit
+// Winograd transform [36][C][C] for the released widths, else the implicit
 // GEMM's [co][tap][ci_pad4].
 std::vector<float> body_conv_weights(const float *w, int C) {
     if (!wino_body(C)) return conv_relayout(w, C, C, nullptr);
-    std::vector<float> u((size_t)16 * C * C);
+    std::vector<float> u((size_t)WINO_POS * C * C);
     wino_weights(w, C, C, u.data());
     return u;
 }
@@ -984,8 +983,8 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
     f += C;                     // conv_first's bias (the body skip)
     f += 2 * 9 * 4 * C + C;     // k_embed's two weight sets, the folded bias
     f += 4 * C;                 // patch_embed's LayerNorm, the final LayerNorm
-    // the body's C -> C convs: Winograd weights [16][C][C] or direct [C][9][C4]
-    const uint64_t body_conv = wino_body(A.embed) ? 16 * C * C : C * 9 * C4;
+    // the body's C -> C convs: Winograd weights [36][C][C] or direct [C][9][C4]
+    const uint64_t body_conv = wino_body(A.embed) ? WINO_POS * C * C : C * 9 * C4;
     f += body_conv + C;         // conv_after_body
     for (int s = 0; s < A.n_stages; ++s) {
         f += body_conv + C;     // the stage close (3x3 with the 1x1 folded in)

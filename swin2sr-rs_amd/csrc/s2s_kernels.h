@@ -178,21 +178,25 @@ const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi);
 // profiler's rows), and the kernel family name it picks.
 void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block);
 hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_out);
-// Winograd F(2x2,3x3) for a 3x3 stride-1 zero-pad-1 conv on a channel-last
-// H x W plane (H, W even, C % 4 == 0): wino_weights transforms the
-// [co][ci][3][3] weights to U = G g G^T, the GEMM's B [16][co][round4(ci)]
-// (double accumulation, rounded once); launch_wino_in writes V = B^T d B of
-// every 2x2 output tile's 4x4 input patch (zero outside the plane) as
-// [16][T][C] for the T = (H/2)(W/2) tiles; a batch of 16 row GEMMs M[b] =
-// V[b] U[b]^T (over M's own buffer); launch_wino_out transforms M back
-// (Y = A^T M A), adds the bias, then the residual `res` [H*W][ldr] if set,
-// then LeakyReLU(slope) if `lrelu`, into out [H*W][ldo].
+// Winograd F(4x4,3x3) for a 3x3 stride-1 zero-pad-1 conv on a channel-last
+// H x W plane (C % 4 == 0): wino_weights transforms the [co][ci][3][3]
+// weights to U = G g G^T, the GEMM's B [36][co][round4(ci)] (double
+// accumulation, rounded once); launch_wino_in writes V = B^T d B of every 4x4
+// output tile's 6x6 input patch (zero outside the plane) as [36][T][C] for the
+// T = wino_tiles(H, W) tiles; a batch of 36 row GEMMs M[b] = V[b] U[b]^T (over
+// M's own buffer); launch_wino_out transforms M back (Y = A^T M A), adds the
+// bias, then the residual `res` [H*W][ldr] if set, then LeakyReLU(slope) if
+// `lrelu`, into out [H*W][ldo] (the tiles' pixels inside the plane).
+constexpr int WINO_POS = 36;
+inline size_t wino_tiles(int H, int W) { return (size_t)((H + 3) / 4) * ((W + 3) / 4); }
 void wino_weights(const float *w, int co, int ci, float *out);
 // The body's C -> C convs take the Winograd path when the batched GEMM runs on
 // the weight-stationary kernel with every column in one workgroup (so it may
 // write M over V in place): C in {60, 120, 180}, every released width.
 inline bool wino_body(int c) { return c == 60 || c == 120 || c == 180; }
 hipError_t launch_wino_in(const float *in, int ldi, float *v, int H, int W, int C, hipStream_t st);
+unsigned wino_in_grid(int H, int W, int C);   // the launches' 1-D grids of 256 threads
+unsigned wino_out_grid(int H, int W, int C);
 hipError_t launch_wino_out(const float *m, const float *bias, const float *res, int ldr,
                            float *out, int ldo, int H, int W, int C, int lrelu, float slope,
                            hipStream_t st);

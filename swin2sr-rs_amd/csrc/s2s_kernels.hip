@@ -525,8 +525,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 //     K halves) meet in LDS;
 //   - the whole row is inside the workgroup, so LayerNorm (+ residual) is an
 //     epilogue.
-// Blocks are numbered ng*P + p with P a multiple of 8, so the column groups
-// that read the same A tile run on the same XCD and share its L2.
+// Blocks are numbered (batch*ngc + ng)*P + p; with several column groups P
+// is a multiple of 8, so the groups that read the same A tile run on the same
+// XCD and share its L2.
 //
 // MFMA 16x16x4 f32 lane layout: lane l supplies A[l%16][k] and B[k][l%16] for
 // its k (above); accumulator register r of lane l holds D[4*(l/16) + r][l%16].
@@ -2539,7 +2540,9 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     const int nb = std::max(g.nb, 1);
     const int ntask = (g.M + 16 * RB - 1) / (16 * RB);
     int P = per_cu * cu_count() / (ng * nb);
-    if (P >= 8) P -= P % 8;
+    // several column groups: P a multiple of 8 puts the groups of one A tile
+    // on one XCD (shared L2); batches share nothing, and fill the machine
+    if (P >= 8 && ng > 1) P -= P % 8;
     P = std::max(1, std::min(P, ntask));
     const dim3 grid((unsigned)(P * ng * nb));
     if (grid_out) *grid_out = grid;
@@ -2784,150 +2787,231 @@ hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *
     return hipGetLastError();
 }
 
-// Winograd F(2x2,3x3) input transform: tile (ty, tx), channels 4c4..4c4+3.
-// The tile's 4x4 input patch d (rows 2ty-1 .. 2ty+2, columns 2tx-1 ..
-// 2tx+2, zero outside the plane) to V = B^T d B with
-// B^T = [1 0 -1 0; 0 1 1 0; 0 -1 1 0; 0 1 0 -1], rows then columns, stored as
-// V[4 xi + nu][tile][c]. One thread per (tile, float4 of channels);
-// consecutive threads read and write consecutive float4s.
-__global__ void k_wino_in(const float *__restrict__ in, int ldi, float *__restrict__ v, int H,
-                          int W, int C, int T) {
-    const int c4n = C >> 2;
+// Winograd F(4x4,3x3): a 4x4 output tile from its 6x6 input patch with 36
+// products per (input, output) channel pair instead of 144. The transforms
+// come from the Toom-Cook construction with the interpolation points
+// 0, 3/2, -3/2, 2/3, -2/3 and infinity (on unit-normal data at C = 180 their
+// fp32 error is about a third of that of the points 0, +-1, +-2):
+//   B^T = [1    0    -97/36  0      1  0]    G = [1       0       0    ]
+//         [0  -2/3   -4/9    3/2    1  0]        [8/65    12/65   18/65]
+//         [0   2/3   -4/9   -3/2    1  0]        [8/65   -12/65   18/65]
+//         [0  -3/2   -9/4    2/3    1  0]        [-81/130 -27/65 -18/65]
+//         [0   3/2   -9/4   -2/3    1  0]        [-81/130  27/65 -18/65]
+//         [0    1     0    -97/36   0  1]        [0       0       1    ]
+//   A^T = [1   1     1     1     1    0]
+//         [0  3/2  -3/2   2/3  -2/3   0]
+//         [0  9/4   9/4   4/9   4/9   0]
+//         [0 27/8 -27/8  8/27 -8/27   1]
+// so that, for the cross-correlation the conv layers compute (tap (a, b) of
+// output pixel (y, x) reads input (y + a - 1, x + b - 1)),
+// Y = A^T [ (G g G^T) .* (B^T d B) ] A per tile and channel pair, summed over
+// the input channels by the transform-domain GEMM.
+
+// B^T applied to the 6 values x[0], x[S], ..., x[5S], in place (14 VALU).
+template <int S> __device__ __forceinline__ void wino4_bt(float *x) {
+    const float d0 = x[0], d1 = x[S], d2 = x[2 * S], d3 = x[3 * S], d4 = x[4 * S], d5 = x[5 * S];
+    const float e1 = fmaf(-4.f / 9.f, d2, d4), o1 = fmaf(1.5f, d3, (-2.f / 3.f) * d1);
+    const float e2 = fmaf(-2.25f, d2, d4), o2 = fmaf(2.f / 3.f, d3, -1.5f * d1);
+    x[0] = fmaf(-97.f / 36.f, d2, d0 + d4);
+    x[S] = e1 + o1;
+    x[2 * S] = e1 - o1;
+    x[3 * S] = e2 + o2;
+    x[4 * S] = e2 - o2;
+    x[5 * S] = fmaf(-97.f / 36.f, d3, d1 + d5);
+}
+// A^T applied to m[0], m[S], ..., m[5S], into y[0], y[T], y[2T], y[3T].
+template <int S, int T> __device__ __forceinline__ void wino4_at(const float *m, float *y) {
+    const float s12 = m[S] + m[2 * S], d12 = m[S] - m[2 * S];
+    const float s34 = m[3 * S] + m[4 * S], d34 = m[3 * S] - m[4 * S];
+    y[0] = m[0] + s12 + s34;
+    y[T] = fmaf(1.5f, d12, (2.f / 3.f) * d34);
+    y[2 * T] = fmaf(2.25f, s12, (4.f / 9.f) * s34);
+    y[3 * T] = fmaf(3.375f, d12, fmaf(8.f / 27.f, d34, m[5 * S]));
+}
+
+// NE consecutive floats (4: a float4, 2: a float2) at p.
+template <int NE> __device__ __forceinline__ void ld_vec(const float *p, float *v) {
+    if constexpr (NE == 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(p);
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
+    } else {
+        const float2 t = *reinterpret_cast<const float2 *>(p);
+        v[0] = t.x;
+        v[1] = t.y;
+    }
+}
+template <int NE> __device__ __forceinline__ void st_vec(float *p, const float *v) {
+    if constexpr (NE == 4)
+        *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    else
+        *reinterpret_cast<float2 *>(p) = make_float2(v[0], v[1]);
+}
+
+// channels per thread of the two transforms
+#ifndef WINO_IN_NE
+#define WINO_IN_NE 4
+#endif
+#ifndef WINO_OUT_NE
+#define WINO_OUT_NE 2
+#endif
+
+// Input transform: tile (ty, tx) of the (H/4) x (W/4) grid (rounded up),
+// channels c .. c+NE-1: its 6x6 patch d (rows 4ty-1 .. 4ty+4, columns 4tx-1
+// .. 4tx+4, zero outside the plane) to V = B^T d B, stored as
+// V[6 xi + nu][tile][c]. One thread per (tile, NE channels); consecutive
+// threads read and write consecutive channel groups.
+template <int NE>
+__global__ __launch_bounds__(256) void k_wino_in(const float *__restrict__ in, int ldi,
+                                                  float *__restrict__ v, int H, int W, int C,
+                                                  int T, int tw) {
+    const int cgn = C / NE;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)T * c4n) return;
-    const int tile = (int)(i / c4n);
-    const int c = 4 * (int)(i - (long long)tile * c4n);
-    const int tw = W >> 1;
+    if (i >= (long long)T * cgn) return;
+    const int tile = (int)(i / cgn);
+    const int c = NE * (int)(i - (long long)tile * cgn);
     const int ty = tile / tw, tx = tile - (tile / tw) * tw;
-    float4 d[4][4];
+    float p[6][6][NE];  // [row][column][channel]
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 6; ++r)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int y = 2 * ty - 1 + r, x = 2 * tx - 1 + q;
-            d[r][q] = ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W)
-                          ? *reinterpret_cast<const float4 *>(in + ((size_t)y * W + x) * ldi + c)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < 6; ++q) {
+            const int y = 4 * ty - 1 + r, x = 4 * tx - 1 + q;
+            if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W) {
+                ld_vec<NE>(in + ((size_t)y * W + x) * ldi + c, p[r][q]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < NE; ++e) p[r][q][e] = 0.f;
+            }
         }
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+#pragma unroll
+        for (int e = 0; e < NE; ++e) wino4_bt<6 * NE>(&p[0][q][e]);
     const size_t plane = (size_t)T * C;
     float *out = v + (size_t)tile * C + c;
-    auto add = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
-    auto sub = [](float4 x, float4 y) { return make_float4(x.x - y.x, x.y - y.y, x.z - y.z, x.w - y.w); };
 #pragma unroll
-    for (int xi = 0; xi < 4; ++xi) {
-        // row xi of B^T d, then its four columns times B
-        float4 t[4];
+    for (int xi = 0; xi < 6; ++xi) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            t[q] = xi == 0 ? sub(d[0][q], d[2][q])
-                 : xi == 1 ? add(d[1][q], d[2][q])
-                 : xi == 2 ? sub(d[2][q], d[1][q])
-                           : sub(d[1][q], d[3][q]);
-        *reinterpret_cast<float4 *>(out + (4 * xi + 0) * plane) = sub(t[0], t[2]);
-        *reinterpret_cast<float4 *>(out + (4 * xi + 1) * plane) = add(t[1], t[2]);
-        *reinterpret_cast<float4 *>(out + (4 * xi + 2) * plane) = sub(t[2], t[1]);
-        *reinterpret_cast<float4 *>(out + (4 * xi + 3) * plane) = sub(t[1], t[3]);
+        for (int e = 0; e < NE; ++e) wino4_bt<NE>(&p[xi][0][e]);
+#pragma unroll
+        for (int nu = 0; nu < 6; ++nu) st_vec<NE>(out + (6 * xi + nu) * plane, p[xi][nu]);
     }
+}
+
+unsigned wino_in_grid(int H, int W, int C) {
+    return (unsigned)(((long long)wino_tiles(H, W) * (C / WINO_IN_NE) + 255) / 256);
 }
 
 hipError_t launch_wino_in(const float *in, int ldi, float *v, int H, int W, int C, hipStream_t st) {
-    if (H % 2 || W % 2 || C % 4 || ldi % 4) return hipErrorInvalidValue;
-    const int T = (H / 2) * (W / 2);
-    const long long n = (long long)T * (C / 4);
-    hipLaunchKernelGGL(k_wino_in, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, ldi, v,
-                       H, W, C, T);
+    if (H < 1 || W < 1 || C % 4 || ldi % 4) return hipErrorInvalidValue;
+    const int tw = (W + 3) / 4;
+    const int T = (int)wino_tiles(H, W);
+    hipLaunchKernelGGL(k_wino_in<WINO_IN_NE>, dim3(wino_in_grid(H, W, C)), dim3(256), 0, st, in,
+                       ldi, v, H, W, C, T, tw);
     return hipGetLastError();
 }
 
-// Winograd F(2x2,3x3) output transform: tile (ty, tx), channels 4c4..4c4+3:
-// M[b][tile][c] for the 16 positions b = 4 xi + nu, Y = A^T M A with
-// A^T = [1 1 1 0; 0 1 -1 -1] (rows, then columns), + bias, + the residual,
-// then LeakyReLU when asked, into the 2x2 output pixels (2ty + r, 2tx + c).
-// One thread per (tile, float4 of channels); M's 16 planes are read with
-// consecutive threads on consecutive float4s.
-__global__ void k_wino_out(const float *__restrict__ m, const float *__restrict__ bias,
-                           const float *__restrict__ res, int ldr, float *__restrict__ out,
-                           int ldo, int W, int C, int T, int lrelu, float slope) {
-    const int c4n = C >> 2;
+// Output transform: tile (ty, tx), channels c .. c+NE-1: M[6 xi + nu][tile][c]
+// to Y = A^T M A, + bias, + the residual, then LeakyReLU when asked, into the
+// tile's 4x4 output pixels that lie inside the plane. One thread per (tile,
+// NE channels); M's 36 planes are read with consecutive threads on
+// consecutive channel groups.
+template <int NE>
+__global__ __launch_bounds__(256) void k_wino_out(const float *__restrict__ m,
+                                                   const float *__restrict__ bias,
+                                                   const float *__restrict__ res, int ldr,
+                                                   float *__restrict__ out, int ldo, int H, int W,
+                                                   int C, int T, int tw, int lrelu, float slope) {
+    const int cgn = C / NE;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)T * c4n) return;
-    const int tile = (int)(i / c4n);
-    const int c = 4 * (int)(i - (long long)tile * c4n);
+    if (i >= (long long)T * cgn) return;
+    const int tile = (int)(i / cgn);
+    const int c = NE * (int)(i - (long long)tile * cgn);
     const size_t plane = (size_t)T * C;
-    float4 mv[16];
+    const float *src = m + (size_t)tile * C + c;
+    float t[6][4][NE];  // [xi][output column][channel]: M A, row by row
 #pragma unroll
-    for (int b = 0; b < 16; ++b)
-        mv[b] = *reinterpret_cast<const float4 *>(m + b * plane + (size_t)tile * C + c);
-    const float4 bv = bias ? *reinterpret_cast<const float4 *>(bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const int tw = W >> 1;
-    const int ty = tile / tw, tx = tile - (tile / tw) * tw;
-    auto comp = [&](int e, float *y) __attribute__((always_inline)) {
-        float t0[4], t1[4];
+    for (int xi = 0; xi < 6; ++xi) {
+        float mr[6][NE];
 #pragma unroll
-        for (int nu = 0; nu < 4; ++nu) {
-            const float m0 = (&mv[0 * 4 + nu].x)[e], m1 = (&mv[1 * 4 + nu].x)[e];
-            const float m2 = (&mv[2 * 4 + nu].x)[e], m3 = (&mv[3 * 4 + nu].x)[e];
-            t0[nu] = m0 + m1 + m2;
-            t1[nu] = m1 - m2 - m3;
-        }
-        y[0] = t0[0] + t0[1] + t0[2];
-        y[1] = t0[1] - t0[2] - t0[3];
-        y[2] = t1[0] + t1[1] + t1[2];
-        y[3] = t1[1] - t1[2] - t1[3];
-    };
-    float yx[4], yy[4], yz[4], yw[4];
-    comp(0, yx);
-    comp(1, yy);
-    comp(2, yz);
-    comp(3, yw);
+        for (int nu = 0; nu < 6; ++nu) ld_vec<NE>(src + (6 * xi + nu) * plane, mr[nu]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const size_t px = (size_t)(2 * ty + (q >> 1)) * W + 2 * tx + (q & 1);
-        float4 v = make_float4(yx[q] + bv.x, yy[q] + bv.y, yz[q] + bv.z, yw[q] + bv.w);
-        if (res) {
-            const float4 r = *reinterpret_cast<const float4 *>(res + px * ldr + c);
-            v.x += r.x;
-            v.y += r.y;
-            v.z += r.z;
-            v.w += r.w;
-        }
-        if (lrelu) {
-            v.x = v.x < 0.f ? v.x * slope : v.x;
-            v.y = v.y < 0.f ? v.y * slope : v.y;
-            v.z = v.z < 0.f ? v.z * slope : v.z;
-            v.w = v.w < 0.f ? v.w * slope : v.w;
-        }
-        *reinterpret_cast<float4 *>(out + px * ldo + c) = v;
+        for (int e = 0; e < NE; ++e) wino4_at<NE, NE>(&mr[0][e], &t[xi][0][e]);
     }
+    float y[4][4][NE];  // [output row][output column][channel]
+#pragma unroll
+    for (int cx = 0; cx < 4; ++cx)
+#pragma unroll
+        for (int e = 0; e < NE; ++e) wino4_at<4 * NE, 4 * NE>(&t[0][cx][e], &y[0][cx][e]);
+    float bv[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) bv[e] = 0.f;
+    if (bias) ld_vec<NE>(bias + c, bv);
+    const int ty = tile / tw, tx = tile - (tile / tw) * tw;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int oy = 4 * ty + r;
+        if (oy >= H) break;
+#pragma unroll
+        for (int cx = 0; cx < 4; ++cx) {
+            const int ox = 4 * tx + cx;
+            if (ox >= W) break;
+            const size_t px = (size_t)oy * W + ox;
+            float v[NE], rv[NE];
+#pragma unroll
+            for (int e = 0; e < NE; ++e) v[e] = y[r][cx][e] + bv[e];
+            if (res) {
+                ld_vec<NE>(res + px * ldr + c, rv);
+#pragma unroll
+                for (int e = 0; e < NE; ++e) v[e] += rv[e];
+            }
+            if (lrelu) {
+#pragma unroll
+                for (int e = 0; e < NE; ++e) v[e] = v[e] < 0.f ? v[e] * slope : v[e];
+            }
+            st_vec<NE>(out + px * ldo + c, v);
+        }
+    }
+}
+
+unsigned wino_out_grid(int H, int W, int C) {
+    return (unsigned)(((long long)wino_tiles(H, W) * (C / WINO_OUT_NE) + 255) / 256);
 }
 
 hipError_t launch_wino_out(const float *m, const float *bias, const float *res, int ldr,
                            float *out, int ldo, int H, int W, int C, int lrelu, float slope,
                            hipStream_t st) {
-    if (H % 2 || W % 2 || C % 4 || ldo % 4 || (res && ldr % 4)) return hipErrorInvalidValue;
-    const int T = (H / 2) * (W / 2);
-    const long long n = (long long)T * (C / 4);
-    hipLaunchKernelGGL(k_wino_out, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, bias,
-                       res, ldr, out, ldo, W, C, T, lrelu, slope);
+    if (H < 1 || W < 1 || C % 4 || ldo % 4 || (res && ldr % 4)) return hipErrorInvalidValue;
+    const int tw = (W + 3) / 4;
+    const int T = (int)wino_tiles(H, W);
+    hipLaunchKernelGGL(k_wino_out<WINO_OUT_NE>, dim3(wino_out_grid(H, W, C)), dim3(256), 0, st, m,
+                       bias, res, ldr, out, ldo, H, W, C, T, tw, lrelu, slope);
     return hipGetLastError();
 }
 
-// U = G g G^T per (co, ci), G = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1],
-// accumulated in double and rounded once, as the GEMM's B: [16][co][round4(ci)]
-// with batch b = 4 xi + nu.
+// U = G g G^T per (co, ci) with G above, accumulated in double and rounded
+// once, as the GEMM's B: [36][co][round4(ci)] with batch b = 6 xi + nu.
 void wino_weights(const float *w, int co, int ci, float *out) {
-    static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    static const double G[6][3] = {{1, 0, 0},
+                                   {8.0 / 65, 12.0 / 65, 18.0 / 65},
+                                   {8.0 / 65, -12.0 / 65, 18.0 / 65},
+                                   {-81.0 / 130, -27.0 / 65, -18.0 / 65},
+                                   {-81.0 / 130, 27.0 / 65, -18.0 / 65},
+                                   {0, 0, 1}};
     const int cp = (ci + 3) / 4 * 4;
-    for (size_t i = 0; i < (size_t)16 * co * cp; ++i) out[i] = 0.f;
+    for (size_t i = 0; i < (size_t)WINO_POS * co * cp; ++i) out[i] = 0.f;
     for (int o = 0; o < co; ++o)
         for (int i = 0; i < ci; ++i) {
             const float *g = w + ((size_t)o * ci + i) * 9;
-            for (int xi = 0; xi < 4; ++xi)
-                for (int nu = 0; nu < 4; ++nu) {
+            for (int xi = 0; xi < 6; ++xi)
+                for (int nu = 0; nu < 6; ++nu) {
                     double u = 0.0;
                     for (int a = 0; a < 3; ++a)
                         for (int b = 0; b < 3; ++b) u += G[xi][a] * (double)g[3 * a + b] * G[nu][b];
-                    out[((size_t)(4 * xi + nu) * co + o) * cp + i] = (float)u;
+                    out[((size_t)(6 * xi + nu) * co + o) * cp + i] = (float)u;
                 }
         }
 }

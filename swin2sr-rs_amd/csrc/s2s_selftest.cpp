@@ -178,11 +178,12 @@ extern "C" int s2s_selftest(const s2s_arch *arch, const s2s_tensor *tensors, siz
         }
     }
 
-    // the body's Winograd F(2x2,3x3) conv (the stage close, conv_after_body)
-    // at the released widths and the checkpoint's own, on even planes (one
-    // that is all border, and planes wider than one 64-lane wavefront)
+    // the body's Winograd F(4x4,3x3) conv (the stage close, conv_after_body)
+    // at the released widths and the checkpoint's own: a plane that is all
+    // border, planes whose sides are not multiples of the 4x4 tile, planes
+    // wider than one 64-lane wavefront
     {
-        const int shapes[4][3] = {{2, 4, 60}, {34, 40, 120}, {16, 70, 180}, {8, 10, arch->embed}};
+        const int shapes[4][3] = {{2, 4, 60}, {34, 41, 120}, {17, 70, 180}, {8, 10, arch->embed}};
         for (auto &sh : shapes) {
             const int h = sh[0], w = sh[1], c = sh[2];
             if (!wino_body(c)) continue;

@@ -332,18 +332,18 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
                               float *out) {
     if (epilogue != 0 && epilogue != 2 && epilogue != 5) return fail("winograd epilogue must be 0, 2 or 5");
     if (epilogue == 2 && !res) return fail("residual epilogue needs res");
-    if (h <= 0 || w <= 0 || h % 2 || w % 2) return fail("the Winograd conv needs an even plane");
+    if (h <= 0 || w <= 0) return fail("the Winograd conv needs a non-empty plane");
     if (!wino_body(c_in) || c_out != c_in)
         return fail("the Winograd conv is the body's C -> C conv, C in {60, 120, 180}");
-    const size_t P = (size_t)h * w, T = P / 4;
-    std::vector<float> u((size_t)16 * c_out * c_in);
+    const size_t P = (size_t)h * w, T = wino_tiles(h, w);
+    std::vector<float> u((size_t)WINO_POS * c_out * c_in);
     wino_weights(wgt, c_out, c_in, u.data());
     Dev d;
     const float *dx = d.up(x, P * c_in), *du = d.up(u.data(), u.size());
     const float *db = bias ? d.up(bias, c_out) : nullptr;
     const float *dr = res ? d.up(res, P * c_out) : nullptr;
-    // V [16][T][C], then M [16][T][C] over it row for row, as the forward does
-    float *dv = d.alloc<float>(16 * T * c_in), *dout = d.alloc<float>(P * c_out);
+    // V [36][T][C], then M [36][T][C] over it row for row, as the forward does
+    float *dv = d.alloc<float>(WINO_POS * T * c_in), *dout = d.alloc<float>(P * c_out);
     if (!dx || !du || !dv || !dout || (bias && !db) || (res && !dr))
         return fail("hipMalloc failed: out of memory");
     GemmArgs g{};
@@ -356,7 +356,7 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
     g.M = (int)T;
     g.N = c_out;
     g.K = c_in;
-    g.nb = 16;
+    g.nb = WINO_POS;
     g.a_bstride = T * c_in;
     g.o_bstride = T * c_out;
     g.b_bstride = (size_t)c_out * c_in;

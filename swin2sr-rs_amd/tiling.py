@@ -100,7 +100,8 @@ def _plan_terms(arch: M.Arch, h: int, w: int):
     if _unit_layout(arch):
         qkv = max(qkv, P * ((arch.heads + 1) // 2) * (6 * arch.head_dim + 2))
     if c in (60, 120, 180):
-        qkv = max(qkv, 4 * P * c)  # the Winograd convs' 16 transform planes of P/4 tiles
+        # the Winograd convs' 36 transform planes of 4x4-pixel tiles
+        qkv = max(qkv, 36 * ((hp + 3) // 4) * ((wp + 3) // 4) * c)
     terms = [P * c] * 3 + [qkv, P * c, P * arch.mlp_ratio * c]
     terms += [3 * h * w, 3 * h * s * w * s, P * 4]
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
@@ -127,7 +128,9 @@ def per_pixel_floats(arch: M.Arch) -> int:
     if _unit_layout(arch):
         qkv = max(qkv, ((arch.heads + 1) // 2) * (6 * arch.head_dim + 2))
     if c in (60, 120, 180):
-        qkv = max(qkv, 4 * c)
+        # 36 planes per 16 pixels, at most ceil(win/4)^2 tiles per win^2 pixels
+        t = (arch.window + 3) // 4
+        qkv = max(qkv, -(-36 * t * t * c // (arch.window * arch.window)))
     body = 3 * c + qkv + c + arch.mlp_ratio * c
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
         head = sum(f * 4 ** o for o in range(arch.octaves - _fused_octaves(arch) + 1))

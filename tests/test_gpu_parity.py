@@ -194,15 +194,16 @@ def test_conv3x3(pkg, orc, h, w, cin, cout, epi):
     assert err < 5e-5, err
 
 
-@pytest.mark.parametrize("h,w,c", [(2, 2, 180), (6, 10, 60), (34, 40, 120), (20, 70, 180),
-                                   (72, 80, 180), (264, 264, 180), (72, 72, 60)])
+@pytest.mark.parametrize("h,w,c", [(2, 2, 180), (5, 7, 60), (6, 10, 60), (34, 40, 120),
+                                   (33, 39, 180), (20, 70, 180), (72, 80, 180), (264, 264, 180),
+                                   (72, 72, 60)])
 @pytest.mark.parametrize("epi", [0, 2, 5])
 def test_conv3x3_winograd(pkg, orc, h, w, c, epi):
     """The body's C -> C convs (the stage close, conv_after_body) run as
-    Winograd F(2x2,3x3) at the released widths: against the oracle's direct
+    Winograd F(4x4,3x3) at the released widths: against the oracle's direct
     conv, at the same bar as the direct kernel, up to the headline plane
     (264 x 264 x 180, the borders' zero padding included); a 2x2 plane is
-    all border."""
+    all border, and 5x7 and 33x39 end in partial 4x4 tiles."""
     cin = cout = c
     r = rng(h * w + cin + cout + epi + 7)
     x = r.standard_normal((cin, h, w), dtype=np.float32)
