@@ -76,7 +76,6 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         # conv_first and patch_embed (its 1x1 folded into conv_first) + LayerNorm
         # in one VALU pass: two K = 27 convs
         "embed": ("valu", 2 * 2 * P * C * 27, f * P * (4 + 2 * C)),
-        "conv_before_upsample": ("mfma", 2 * P * F * 9 * C, f * P * (C + F)),
         "layernorm": ("hbm", 10 * P * C, f * P * 2 * C),
         "pad_input": ("hbm", 0, f * (3 * h * w + 4 * P)),
         "conv_last_finish": ("hbm", 2 * (h * s) * (w * s) * 3 * 9 * F,
@@ -91,6 +90,14 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "up2_last": ("mfma", 2 * min(hp * s // 4, -(-h * s // 4)) * (wp * s // 4) * 48 * 25 * F,
                      f * ((hp * s // 4) * (wp * s // 4) * F + 3 * h * s * w * s)),
     }
+    if C in (60, 120, 180) and F % 4 == 0 and F <= 64:
+        # conv_before_upsample (C -> F, LeakyReLU) as Winograd F(4x4,3x3): the
+        # same input transform, 36 GEMMs of T x F x C, the output transform
+        work["conv_before_upsample_in"] = ("hbm", 0, f * (P * C + VT * C))
+        work["conv_before_upsample"] = ("mfma", 2 * VT * F * C, f * (VT * (C + F) + 36 * F * C))
+        work["conv_before_upsample_out"] = ("hbm", 0, f * (VT * F + P * F))
+    else:
+        work["conv_before_upsample"] = ("mfma", 2 * P * F * 9 * C, f * P * (C + F))
     px = P
     for o in range(arch.octaves):
         work[f"conv3x3_shuffle2_o{o}"] = ("mfma", 2 * px * 4 * F * 9 * F, f * px * 5 * F)

@@ -302,8 +302,11 @@ int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const fl
  * transform with the bias and the epilogue (0 store, 2 += res, 5
  * LeakyReLU(slope)) - against the reference's direct cpu::conv3x3
  * (src/cpu.rs:400-414; the reference's own CUDA backend runs these convs as
- * Winograd with 6x6 tiles, src/gpu.rs:161-181). Channel-last `[h*w][C]` in
- * and out; any h, w >= 1, c_in == c_out == C in {60, 120, 180}. */
+ * Winograd with 6x6 tiles, src/gpu.rs:161-181). Also conv_before_upsample's
+ * C -> F conv, which the head runs the same way (F <= 64, a multiple of 4,
+ * on the narrow build of the GEMM, its products in a buffer of their own).
+ * Channel-last `[h*w][c_in]` in, `[h*w][c_out]` out; any h, w >= 1;
+ * c_in == c_out == C in {60, 120, 180}, or c_in = C and c_out = F. */
 int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
                               const float *bias, int epilogue, const float *res, float slope,
                               float *out);

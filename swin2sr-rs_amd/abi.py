@@ -390,7 +390,8 @@ def test_conv3x3(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
 
 
 def test_conv3x3_winograd(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
-    """The body's Winograd F(4x4,3x3) conv path (c_in == c_out in {60, 120, 180})."""
+    """The Winograd F(4x4,3x3) conv path: the body's C -> C convs (c_in ==
+    c_out in {60, 120, 180}) and conv_before_upsample's C -> F (F <= 64)."""
     lib = load_library()
     cout, cin = wgt.shape[0], wgt.shape[1]
     out = np.empty((h * w, cout), np.float32)

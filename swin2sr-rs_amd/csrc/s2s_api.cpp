@@ -112,6 +112,7 @@ struct AllocList {
 struct s2s_ctx {
     s2s_arch arch{};
     int c = 0, hd = 0, hidden = 0, feat = 0, octaves = 0;
+    bool cbu_wino = false;  // conv_before_upsample as Winograd (weights U [36][F][C])
     int device = 0;
     hipStream_t stream = nullptr;
     AllocList weight_allocs;
@@ -124,7 +125,7 @@ struct s2s_ctx {
     float *norm_w = nullptr, *norm_b = nullptr;
     float *cab_w = nullptr, *cab_b = nullptr;  // conv_after_body (body_conv_weights)
     std::vector<StageW> stages;
-    float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C]
+    float *cbu_w = nullptr, *cbu_b = nullptr;  // conv_before_upsample [F][9*C] or [36][F][C]
     std::vector<float *> up_w, up_b;           // octave convs, shuffle-permuted [4F][9*F]
     float *last_w = nullptr, *last_b = nullptr;  // conv_last [9][F][3]
     // pixelshuffle: the last octave's conv and conv_last composed (k_up_last):
@@ -191,6 +192,12 @@ struct s2s_ctx {
                              : plane;
         return wino_body(c) ? std::max(q, WINO_POS * wino_tiles(hp, wp) * c) : q;
     }
+    // MLP hidden buffer floats; it also holds conv_before_upsample's Winograd
+    // products (36 planes of wino_tiles(hp, wp) tiles x F) in the head
+    size_t hid_floats(int hp, int wp) const {
+        const size_t h = (size_t)hp * wp * hidden;
+        return cbu_wino ? std::max(h, WINO_POS * wino_tiles(hp, wp) * feat) : h;
+    }
     // The buffers of a padded plane's body, and of an image's head (with the
     // host path's device copies of the input and output when `io`); `bind`
     // points the specs at the context's members (else dst is null).
@@ -208,6 +215,9 @@ struct s2s_ctx {
     int stage_fwd(int s, int hp, int wp, const float *x_in, float *x_out);
     int conv_body(const char *name, const float *in, int H, int W, const float *u,
                   const float *bias, const float *res, float *out);
+    int conv_wino(const char *name, const float *in, int H, int W, int ci, int co,
+                  const float *u, const float *bias, const float *res, float *mbuf, float *out,
+                  int lrelu, float slope);
     int forward_device(int h, int w, const float *d_in, float *d_out);
     int head(int h, int w, float *d_out);
 };
@@ -330,7 +340,7 @@ void s2s_ctx::body_specs(int hp, int wp, bool bind, std::vector<BufSpec> &v) {
     v.push_back({d(&body), P * c, "body", false});
     v.push_back({d(&qkv), qkv_floats(hp, wp), "qkv", true});
     v.push_back({d(&o), P * c, "attn", false});
-    v.push_back({d(&hid), P * hidden, "mlp", false});
+    v.push_back({d(&hid), hid_floats(hp, wp), "mlp", false});
 }
 
 // Image buffers: the padded input (and, for the host path, device copies of
@@ -605,18 +615,32 @@ int s2s_ctx::conv_body(const char *name, const float *in, int H, int W, const fl
         }
         return 0;
     }
+    return conv_wino(name, in, H, W, c, c, u, bias, res, qkv, out, 0, 0.f);
+}
+
+// A 3x3 conv ci -> co as Winograd F(4x4,3x3) on the qkv buffer (free outside
+// the blocks): the input transform of `in` [H*W][ci] into V there, the 36
+// transform-position GEMMs into M at `mbuf` (M over V in place when mbuf is
+// the qkv buffer, which takes co == ci: every GEMM task then writes exactly
+// the rows it has read), then the output transform with the bias, the
+// residual `res` if set and LeakyReLU(slope) if `lrelu`, into out [H*W][co].
+int s2s_ctx::conv_wino(const char *name, const float *in, int H, int W, int ci, int co,
+                       const float *u, const float *bias, const float *res, float *mbuf,
+                       float *out, int lrelu, float slope) {
+    if (mbuf == qkv && co != ci) return fail(std::string(name) + ": in-place Winograd needs co == ci");
     const int T = (int)wino_tiles(H, W);
     const std::string in_name = std::string(name) + "_in", out_name = std::string(name) + "_out";
-    if (run(in_name.c_str(), dim3(wino_in_grid(H, W, c)), dim3(256),
-            [&] { return launch_wino_in(in, c, qkv, H, W, c, stream); }))
+    if (run(in_name.c_str(), dim3(wino_in_grid(H, W, ci)), dim3(256),
+            [&] { return launch_wino_in(in, ci, qkv, H, W, ci, stream); }))
         return -1;
-    GemmArgs g = rows_gemm(qkv, c, u, c, nullptr, qkv, c, T, c, c);
+    GemmArgs g = rows_gemm(qkv, ci, u, ci, nullptr, mbuf, co, T, co, ci);
     g.nb = WINO_POS;
-    g.a_bstride = g.o_bstride = (size_t)T * c;
-    g.b_bstride = (size_t)c * c;
+    g.a_bstride = (size_t)T * ci;
+    g.o_bstride = (size_t)T * co;
+    g.b_bstride = (size_t)co * ci;
     if (gemm(name, g, ALOAD_ROWS, EPI_STORE)) return -1;
-    return run(out_name.c_str(), dim3(wino_out_grid(H, W, c)), dim3(256), [&] {
-        return launch_wino_out(qkv, bias, res, c, out, c, H, W, c, 0, 0.f, stream);
+    return run(out_name.c_str(), dim3(wino_out_grid(H, W, co)), dim3(256), [&] {
+        return launch_wino_out(mbuf, bias, res, res ? co : 0, out, co, H, W, co, lrelu, slope, stream);
     });
 }
 
@@ -658,6 +682,15 @@ int s2s_ctx::head(int h, int w, float *d_out) {
     const int P = hp * wp;
     const int oh = h * s, ow = w * s;
     GemmArgs g{};
+    // conv_before_upsample + LeakyReLU(0.01) into the first feature plane
+    auto before_upsample = [&]() -> int {
+        if (cbu_wino)
+            return conv_wino("conv_before_upsample", cur, hp, wp, c, feat, cbu_w, cbu_b, nullptr,
+                             hid, fplanes[0], 1, 0.01f);
+        g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
+        g.slope = 0.01f;
+        return gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU);
+    };
     auto last = [&](const float *f, int H, int W) {
         return run("conv_last_finish", conv_last_grid(oh, ow), dim3(256), [&] {
             return launch_conv_last_finish(f, last_w, last_b, d_out, H, W, feat, oh, ow,
@@ -668,9 +701,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
     case S2S_PIXELSHUFFLE:
     case S2S_PIXELSHUFFLE_AUX: {
         const bool aux = arch.upsampler == S2S_PIXELSHUFFLE_AUX;
-        g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
-        g.slope = 0.01f;
-        if (gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+        if (before_upsample()) return -1;
         if (aux) {
             // the bicubic branch from the padded input, its conv; the aux image
             // and its conv back to features (reference network_swin2sr.py:948-958)
@@ -743,9 +774,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
         return gemm("conv_shuffle_finish", g, ALOAD_IM2COL, EPI_SHUFFLE_FINISH);
     }
     case S2S_NEAREST_CONV: {
-        g = conv_gemm(cur, hp, wp, c, cbu_w, cbu_b, fplanes[0], feat, feat);
-        g.slope = 0.01f;
-        if (gemm("conv_before_upsample", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
+        if (before_upsample()) return -1;
         // two nearest-2x steps, each read by the next conv's operand loader
         g = conv_gemm(fplanes[0], 2 * hp, 2 * wp, feat, nu1_w, nu1_b, fplanes[1], feat, feat);
         g.slope = 0.2f;
@@ -1001,7 +1030,8 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
         int F = 0;
         if (head_feat_of(ts, A.embed, &F)) return -1;
         const uint64_t F_ = F, F4 = round4(F);
-        f += F_ * 9 * C4 + F_;          // conv_before_upsample
+        // conv_before_upsample: Winograd weights [36][F][C4] or direct [F][9][C4]
+        f += (wino_head(A.embed, F) ? WINO_POS * F_ * C4 : F_ * 9 * C4) + F_;
         f += 9 * F_ * 3 + 3;            // conv_last
         if (up == S2S_NEAREST_CONV) {
             f += 3 * (F_ * 9 * F4 + F_);  // conv_up1, conv_up2, conv_hr
@@ -1090,6 +1120,16 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                       const std::vector<int> *perm) -> int {
         if (ts.get(name, {co, ci, 3, 3}, &x)) return -1;
         return ctx->upload(conv_relayout(x->data, co, ci, perm), dst);
+    };
+    // conv_before_upsample [F][C][3][3]: the Winograd transform [36][F][C]
+    // when wino_head takes it, else the implicit GEMM's layout
+    auto up_before_upsample = [&](int F) -> int {
+        ctx->cbu_wino = wino_head(C, F);
+        if (!ctx->cbu_wino) return upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
+        if (ts.get("conv_before_upsample.0.weight", {F, C, 3, 3}, &x)) return -1;
+        std::vector<float> u((size_t)WINO_POS * F * round4(C));
+        wino_weights(x->data, F, C, u.data());
+        return ctx->upload(u, &ctx->cbu_w);
     };
 
     rc = rc || up("conv_first.bias", {C}, &ctx->cf_b);
@@ -1282,7 +1322,7 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             const int F = ctx->feat;
             const int oct = octaves_of(A.scale);
             ctx->octaves = oct;
-            rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
+            rc = rc || up_before_upsample(F);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
             const std::vector<int> perm = shuffle_perm(F);
             // the plain pixel-shuffle head composes its last octave with
@@ -1360,7 +1400,7 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
         rc = rc || head_feat();
         if (!rc) {
             const int F = ctx->feat;
-            rc = rc || upconv("conv_before_upsample.0.weight", F, C, &ctx->cbu_w, nullptr);
+            rc = rc || up_before_upsample(F);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
             rc = rc || upconv("conv_up1.weight", F, F, &ctx->nu1_w, nullptr);
             rc = rc || up("conv_up1.bias", {F}, &ctx->nu1_b);

@@ -194,6 +194,10 @@ void wino_weights(const float *w, int co, int ci, float *out);
 // the weight-stationary kernel with every column in one workgroup (so it may
 // write M over V in place): C in {60, 120, 180}, every released width.
 inline bool wino_body(int c) { return c == 60 || c == 120 || c == 180; }
+// conv_before_upsample (C -> F, then LeakyReLU) takes the Winograd path when C
+// is a body width above and F fits one narrow (64-column) group of the
+// weight-stationary kernel; its products go to a buffer of their own.
+inline bool wino_head(int c, int f) { return wino_body(c) && f % 4 == 0 && f <= 64; }
 hipError_t launch_wino_in(const float *in, int ldi, float *v, int H, int W, int C, hipStream_t st);
 unsigned wino_in_grid(int H, int W, int C);   // the launches' 1-D grids of 256 threads
 unsigned wino_out_grid(int H, int W, int C);

@@ -501,9 +501,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 // 540 x 360 floats, while M is the whole plane (69,696 tokens at 256x256).
 // So the weight slice a wavefront needs is loaded into VGPRs once, and the
 // activations stream past it exactly once:
-//   - a workgroup owns one column group of <= 192 output columns (4 waves x
-//     48 columns = 3 MFMA tiles of 16) and, for K = 2*KPW, a second set of 4
-//     waves holding the other half of K (their partial sums meet in LDS);
+//   - a workgroup owns one column group of <= 64 NTW output columns (4 waves
+//     x NTW MFMA tiles of 16 columns: NTW = 3, 192 columns, in general; NTW =
+//     1 for a GEMM of at most 64 columns) and, for K = 2*KPW, a second set of
+//     4 waves holding the other half of K (their partial sums meet in LDS);
 //   - it is persistent: it walks 16-row tasks p, p+P, p+2P, ... of the plane;
 //     each task's A tile (16 rows x K, contiguous in HBM) is loaded once,
 //     coalesced, into LDS (double-buffered: the next task's loads are in flight
@@ -627,7 +628,7 @@ __device__ __forceinline__ float half_max(float x) {
     return fmaxf(lo, hi);
 }
 
-template <int KPW, int KS, int RB, int EPI>
+template <int KPW, int KS, int RB, int EPI, int NTW>
 __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int NT = 256 * KS;
     constexpr int NW = 4 * KS;                 // waves
@@ -646,8 +647,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr int CA = (TR * KT * 4 + 1023) / 1024;
     constexpr int NCA = (CA + NW - 1) / NW;
     constexpr int ATILE = NCA * NW * 256;      // floats reserved per buffer
-    // residual tile: TR rows x N (<= 192) floats
-    constexpr int CR = HAS_RES ? (TR * 192 * 4 + 1023) / 1024 : 0;
+    // a column group: 4 waves x NTW MFMA tiles of 16 columns
+    constexpr int GW = 64 * NTW;
+    // residual tile: TR rows x N (<= GW) floats
+    constexpr int CR = HAS_RES ? (TR * GW * 4 + 1023) / 1024 : 0;
     constexpr int NCR = HAS_RES ? (CR + NW - 1) / NW : 0;
     constexpr int RTILE = HAS_RES ? NCR * NW * 256 : 1;
     // The MFMA computes the transposed tile (a lane holds one row, 4
@@ -657,7 +660,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     constexpr bool TT = !WIN;
     // buffer stores per lane per task: a float4 per tile (float2 with K
     // split), or one dword per value for the unit layout
-    constexpr int NSTORE = TT ? 3 * RB : (KS == 2 ? 2 : 4) * 3 * RB;
+    constexpr int NSTORE = TT ? NTW * RB : (KS == 2 ? 2 : 4) * NTW * RB;
     static_assert(KPW % 4 == 0, "K must be a multiple of 4");
     (void)NT;
 
@@ -669,12 +672,12 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     __shared__ __attribute__((aligned(16))) float Rs1[RTILE];
     // K halves swap their accumulators: [sender half][column wave][rb][tile]
     // [lane][register]
-    __shared__ __attribute__((aligned(16))) float ksum[KS == 2 ? 2 * 4 * RB * 3 * 4 * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float ksum[KS == 2 ? 2 * 4 * RB * NTW * 4 * 64 : 1];
     // row statistics: [K half * 4 + column wave][row][sum, sum of squares]
     __shared__ float rst0[4 * KS][TR][2];
     __shared__ float rst1[4 * KS][TR][2];
     // bias, LN weight, LN bias of the group's columns
-    __shared__ __attribute__((aligned(16))) float prm[3][192];
+    __shared__ __attribute__((aligned(16))) float prm[3][GW];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -716,13 +719,13 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     // output byte offsets: a column part per tile (out of range past the
     // group) plus a row part; their sum stays below 2^32, so an out-of-range
     // part keeps the whole offset out of range
-    unsigned colo[3];
+    unsigned colo[NTW];
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
+    for (int t = 0; t < NTW; ++t) {
         // the first of the NR consecutive columns this lane finishes in tile t
         // (a run never straddles the group's end, a multiple of 4), or the
         // lane's column for the unit layout
-        const int cl = TT ? 48 * cg + 16 * t + 4 * q + R0 : 48 * cg + 16 * t + j;
+        const int cl = TT ? 16 * NTW * cg + 16 * t + 4 * q + R0 : 16 * NTW * cg + 16 * t + j;
         if (WIN) {
             // column seg*C + head*hd + d -> unit (head/2), segment seg, the
             // head's half of it, d
@@ -741,10 +744,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                                                   HAS_RES ? (size_t)g.M * g.ldr * 4 : 0);
 
     // ---- the weight slice, once (columns outside the group read as zero) ----
-    float bw[3][S];
+    float bw[NTW][S];
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
-        const int cl = 48 * cg + 16 * t + j;  // (the MFMA's A row l%16: an output column)
+    for (int t = 0; t < NTW; ++t) {
+        const int cl = 16 * NTW * cg + 16 * t + j;  // (the MFMA's A row l%16: an output column)
         const int boff = cl < gw ? ((gc0 + cl) * g.ldb + kbase) * 4 : BUF_OOB;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
@@ -757,7 +760,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
         for (int i = 0; i < R; ++i) bw[t][4 * G + i] = buf_load1(rb_rs, boff + (16 * G + R * q + i) * 4);
     }
-    if (tid < 192) {
+    if (tid < GW) {
         const bool ok = tid < gw;
         prm[0][tid] = (ok && g.bias) ? g.bias[gc0 + tid] : 0.f;
         prm[1][tid] = (HAS_LN && ok) ? g.ln_w[gc0 + tid] : 0.f;
@@ -826,7 +829,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     // one task late, under the next task's MFMAs: `pacc` holds the previous
     // task's bias-added sums, its row statistics sit in `prst`, its residual
     // tile in `pres`.
-    f4v pacc[RB][3];
+    f4v pacc[RB][NTW];
     auto finish = [&](int task, const float (*prst)[TR][2], const float *pres)
         __attribute__((always_inline)) {
         const float invn = 1.0f / (float)gw;
@@ -847,7 +850,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             // the buffer
             const unsigned tro = tofs + (unsigned)(((task - wi * TPW) * TR + 4 * q + R0) * RSU) * 4u;
 #pragma unroll
-            for (int t = 0; t < 3; ++t) {
+            for (int t = 0; t < NTW; ++t) {
                 const int vo = (int)(tro + colo[t]);
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
@@ -880,10 +883,10 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
                 mr = mean * rstd;
             }
 #pragma unroll
-            for (int t = 0; t < 3; ++t) {
+            for (int t = 0; t < NTW; ++t) {
                 // columns cl .. cl + NR - 1; columns past the group read
                 // inside the tile's allocation and are dropped at the store
-                const int cl = 48 * cg + 16 * t + 4 * q + R0;
+                const int cl = 16 * NTW * cg + 16 * t + 4 * q + R0;
                 float v[NR], lw[NR], lb[NR], rs[NR];
 #pragma unroll
                 for (int rr = 0; rr < NR; ++rr) v[rr] = pacc[rb][t][rr];
@@ -943,21 +946,21 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         const int nxt = task + g.P;
         dma_a(nxt < ntask ? nxt : task, nxt_buf);
 
-        f4v acc[RB][3];
+        f4v acc[RB][NTW];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int t = 0; t < 3; ++t) {
+            for (int t = 0; t < NTW; ++t) {
                 // the accumulators start from the bias (the reference's CPU
                 // order: bias first, then the K sum) of the lane's 4 columns;
                 // with K split, one half carries it
                 if (TT) {
                     const float4 b4 = (KS == 1 || kq == 0)
-                                          ? *reinterpret_cast<const float4 *>(&prm[0][48 * cg + 16 * t + 4 * q])
+                                          ? *reinterpret_cast<const float4 *>(&prm[0][16 * NTW * cg + 16 * t + 4 * q])
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
                     acc[rb][t] = f4v{b4.x, b4.y, b4.z, b4.w};
                 } else {
-                    const float bv = (KS == 1 || kq == 0) ? prm[0][48 * cg + 16 * t + j] : 0.f;
+                    const float bv = (KS == 1 || kq == 0) ? prm[0][16 * NTW * cg + 16 * t + j] : 0.f;
                     acc[rb][t] = f4v{bv, bv, bv, bv};
                 }
             }
@@ -978,7 +981,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int t = 0; t < 3; ++t)
+                    for (int t = 0; t < NTW; ++t)
                         acc[rb][t] = TT ? MFMA16(bw[t][4 * gi + i], av[rb][i], acc[rb][t])
                                         : MFMA16(av[rb][i], bw[t][4 * gi + i], acc[rb][t]);
             // the previous task's epilogue, issued while these MFMAs run
@@ -992,7 +995,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
             for (int rb = 0; rb < RB; ++rb) {
                 const float a = cur[(rb * 16 + j) * KT + kbase + 16 * G + R * q + i];
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
+                for (int t = 0; t < NTW; ++t)
                     acc[rb][t] = TT ? MFMA16(bw[t][4 * G + i], a, acc[rb][t])
                                     : MFMA16(a, bw[t][4 * G + i], acc[rb][t]);
             }
@@ -1007,18 +1010,18 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
-                    *reinterpret_cast<f4v *>(&ksum[((((kq * 4 + cg) * RB + rb) * 3 + t) * 64 + lane) * 4]) =
+                for (int t = 0; t < NTW; ++t)
+                    *reinterpret_cast<f4v *>(&ksum[((((kq * 4 + cg) * RB + rb) * NTW + t) * 64 + lane) * 4]) =
                         acc[rb][t];
             lds_sync();
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int t = 0; t < 3; ++t) {
+                for (int t = 0; t < NTW; ++t) {
                     const float2 own = *reinterpret_cast<const float2 *>(
-                        &ksum[((((kq * 4 + cg) * RB + rb) * 3 + t) * 64 + lane) * 4 + R0]);
+                        &ksum[((((kq * 4 + cg) * RB + rb) * NTW + t) * 64 + lane) * 4 + R0]);
                     const float2 oth = *reinterpret_cast<const float2 *>(
-                        &ksum[(((((1 - kq) * 4 + cg) * RB + rb) * 3 + t) * 64 + lane) * 4 + R0]);
+                        &ksum[(((((1 - kq) * 4 + cg) * RB + rb) * NTW + t) * 64 + lane) * 4 + R0]);
                     acc[rb][t][0] = own.x + oth.x;
                     acc[rb][t][1] = own.y + oth.y;
                 }
@@ -1028,13 +1031,13 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         // reference's channel LayerNorm computes them; padding columns hold
         // exact zeros)
         if (HAS_LN) {
-            // this row's sums over the lane's NR x 3 columns, then over the 4
+            // this row's sums over the lane's NR x NTW columns, then over the 4
             // lane groups (the row's other columns in this wave)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 float s1 = acc[rb][0][0], s2 = acc[rb][0][0] * acc[rb][0][0];
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
+                for (int t = 0; t < NTW; ++t)
 #pragma unroll
                     for (int rr = (t == 0 ? 1 : 0); rr < NR; ++rr) {
                         const float x = acc[rb][t][rr];
@@ -1049,7 +1052,7 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int t = 0; t < 3; ++t) pacc[rb][t] = acc[rb][t];
+            for (int t = 0; t < NTW; ++t) pacc[rb][t] = acc[rb][t];
 
         // everything this task needs next (the next A tile, and the residual
         // tile copied during the previous task) has landed; the previous
@@ -2489,6 +2492,12 @@ static int cu_count() {
 // k_bsgemm takes a row GEMM whose K per wave is one it is built for (the
 // embed widths of the released checkpoints: 180 and 60, with K = 2*KPW split
 // over two wave sets).
+// MFMA tiles of 16 columns per wave: one for a GEMM of at most 64 columns
+// whose epilogue has a narrow build (a column group of 64), else three (192).
+static int bs_ntw(const GemmArgs &g, int epi) {
+    return (g.N <= 64 && (epi == EPI_STORE || epi == EPI_LN_RES)) ? 1 : 3;
+}
+
 static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks) {
     if (aload != ALOAD_ROWS || epi == EPI_SHUFFLE) return false;
     if (g.nb > 1 && (epi != EPI_STORE || g.bias)) return false;
@@ -2496,7 +2505,8 @@ static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks
     // each lane stores runs of 4 (2) consecutive columns as one float4 (float2):
     // the column groups and the row strides are multiples of 4
     {
-        const int ng = (g.N + 191) / 192;
+        const int gw = 64 * bs_ntw(g, epi);
+        const int ng = (g.N + gw - 1) / gw;
         if (g.N % 4 || ((g.N + ng - 1) / ng) % 4 || g.ldo % 4) return false;
         if ((epi == EPI_RES || epi == EPI_LN_RES) && g.ldr % 4) return false;
     }
@@ -2522,12 +2532,12 @@ static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks
     return true;
 }
 
-template <int KPW, int KS, int RB, int EPI>
+template <int KPW, int KS, int RB, int EPI, int NTW>
 static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *grid_out) {
     static int per_cu = 0;  // resident workgroups per CU, from the occupancy query
     if (!per_cu) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_bsgemm<KPW, KS, RB, EPI>, 256 * KS,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_bsgemm<KPW, KS, RB, EPI, NTW>, 256 * KS,
                                                          0) != hipSuccess ||
             nb < 1) {
             (void)hipGetLastError();
@@ -2535,7 +2545,7 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
         }
         per_cu = nb;
     }
-    const int ng = (g.N + 191) / 192;
+    const int ng = (g.N + 64 * NTW - 1) / (64 * NTW);
     const int ngw = (g.N + ng - 1) / ng;
     const int nb = std::max(g.nb, 1);
     const int ntask = (g.M + 16 * RB - 1) / (16 * RB);
@@ -2575,38 +2585,44 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     a.a_bs = g.a_bstride;
     a.b_bs = g.b_bstride;
     a.o_bs = g.o_bstride;
-    hipLaunchKernelGGL((k_bsgemm<KPW, KS, RB, EPI>), grid, dim3(256 * KS), 0, st, a);
+    hipLaunchKernelGGL((k_bsgemm<KPW, KS, RB, EPI, NTW>), grid, dim3(256 * KS), 0, st, a);
     return hipGetLastError();
 }
 
 template <int KPW, int KS, int RB>
 static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool launch, dim3 *grid) {
+    if (bs_ntw(g, epi) == 1) {
+        // the narrow builds
+        if (epi == EPI_STORE) return run_bs<KPW, KS, RB, EPI_STORE, 1>(g, st, launch, grid);
+        if constexpr (RB == 1) {
+            if (epi == EPI_LN_RES) return run_bs<KPW, KS, RB, EPI_LN_RES, 1>(g, st, launch, grid);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (epi) {
-    case EPI_STORE: return run_bs<KPW, KS, RB, EPI_STORE>(g, st, launch, grid);
-    case EPI_GELU: return run_bs<KPW, KS, RB, EPI_GELU>(g, st, launch, grid);
-    case EPI_LRELU: return run_bs<KPW, KS, RB, EPI_LRELU>(g, st, launch, grid);
-    case EPI_QKV_WIN: return run_bs<KPW, KS, RB, EPI_QKV_WIN>(g, st, launch, grid);
+    case EPI_STORE: return run_bs<KPW, KS, RB, EPI_STORE, 3>(g, st, launch, grid);
+    case EPI_GELU: return run_bs<KPW, KS, RB, EPI_GELU, 3>(g, st, launch, grid);
+    case EPI_LRELU: return run_bs<KPW, KS, RB, EPI_LRELU, 3>(g, st, launch, grid);
+    case EPI_QKV_WIN: return run_bs<KPW, KS, RB, EPI_QKV_WIN, 3>(g, st, launch, grid);
     default: break;
     }
     // residual and LayerNorm epilogues run with 16-row tasks only (bs_rb)
     if constexpr (RB == 1) {
         switch (epi) {
-        case EPI_RES: return run_bs<KPW, KS, RB, EPI_RES>(g, st, launch, grid);
-        case EPI_LN: return run_bs<KPW, KS, RB, EPI_LN>(g, st, launch, grid);
-        case EPI_LN_RES: return run_bs<KPW, KS, RB, EPI_LN_RES>(g, st, launch, grid);
+        case EPI_RES: return run_bs<KPW, KS, RB, EPI_RES, 3>(g, st, launch, grid);
+        case EPI_LN: return run_bs<KPW, KS, RB, EPI_LN, 3>(g, st, launch, grid);
+        case EPI_LN_RES: return run_bs<KPW, KS, RB, EPI_LN_RES, 3>(g, st, launch, grid);
         default: break;
         }
     }
     return hipErrorInvalidValue;
 }
 
-// Rows per task: 32 (twice the MFMA work per task for the same per-task
-// overhead) where the task count still divides well over the workgroups
-// (several column groups, or batches) and the epilogue leaves room in the
-// register file;
-// 16 otherwise.
+// 32-row tasks (two row blocks) when several column groups or batches share
+// the machine and the epilogue keeps no per-row state; else 16-row tasks.
 static int bs_rb(const GemmArgs &g, int ks, int epi) {
-    const int ng = (g.N + 191) / 192 * std::max(g.nb, 1);  // column groups x batches
+    const int gw = 64 * bs_ntw(g, epi);
+    const int ng = (g.N + gw - 1) / gw * std::max(g.nb, 1);  // column groups x batches
     const bool simple = epi == EPI_STORE || epi == EPI_GELU || epi == EPI_LRELU || epi == EPI_QKV_WIN;
     (void)ks;
     return (ng >= 2 && simple) ? 2 : 1;

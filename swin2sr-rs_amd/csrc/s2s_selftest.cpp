@@ -200,6 +200,22 @@ extern "C" int s2s_selftest(const s2s_arch *arch, const s2s_tensor *tensors, siz
         }
     }
 
+    // conv_before_upsample's Winograd conv (C -> F, then LeakyReLU) at the
+    // checkpoint's width and a head of 64 features, on a plane ending in
+    // partial tiles
+    if (wino_head(arch->embed, 64)) {
+        const int h = 11, w = 13, c = arch->embed, f = 64;
+        std::vector<float> x = seq((size_t)h * w * c, 0.4f), wgt = seq((size_t)f * c * 9, 1.3f),
+                           b = seq(f, 2.5f), got((size_t)h * w * f);
+        for (float &v : wgt) v /= std::sqrt(9.0f * c);
+        CHECK(s2s_test_conv3x3_winograd(h, w, c, f, x.data(), wgt.data(), b.data(), 5, nullptr, 0.01f,
+                                        got.data()));
+        std::vector<double> want = conv3x3(x, h, w, c, f, wgt, b);
+        for (double &v : want) v = v < 0 ? v * 0.01 : v;
+        CHECK(cnt.ok(close("winograd conv3x3 " + std::to_string(c) + "->64 + LeakyReLU at 11x13",
+                           want, got, tol)));
+    }
+
     // conv3x3 + pixel_shuffle(2) (the head's octave) at the reference's shapes
     {
         const int shapes[5][4] = {{4, 3, 5, 7}, {4, 3, 1, 6}, {6, 24, 4, 5}, {2, 2, 3, 61}, {2, 2, 1, 1025}};

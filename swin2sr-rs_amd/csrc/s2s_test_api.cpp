@@ -333,8 +333,10 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
     if (epilogue != 0 && epilogue != 2 && epilogue != 5) return fail("winograd epilogue must be 0, 2 or 5");
     if (epilogue == 2 && !res) return fail("residual epilogue needs res");
     if (h <= 0 || w <= 0) return fail("the Winograd conv needs a non-empty plane");
-    if (!wino_body(c_in) || c_out != c_in)
-        return fail("the Winograd conv is the body's C -> C conv, C in {60, 120, 180}");
+    const bool body = c_out == c_in && wino_body(c_in);
+    if (!body && !wino_head(c_in, c_out))
+        return fail("the Winograd conv is the body's C -> C conv, C in {60, 120, 180}, or "
+                    "conv_before_upsample's C -> F, F <= 64 and a multiple of 4");
     const size_t P = (size_t)h * w, T = wino_tiles(h, w);
     std::vector<float> u((size_t)WINO_POS * c_out * c_in);
     wino_weights(wgt, c_out, c_in, u.data());
@@ -342,16 +344,19 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
     const float *dx = d.up(x, P * c_in), *du = d.up(u.data(), u.size());
     const float *db = bias ? d.up(bias, c_out) : nullptr;
     const float *dr = res ? d.up(res, P * c_out) : nullptr;
-    // V [36][T][C], then M [36][T][C] over it row for row, as the forward does
+    // V [36][T][C_in], then M [36][T][C_out] - over V row for row for the
+    // body's convs, in a buffer of its own for conv_before_upsample, as the
+    // forward does
     float *dv = d.alloc<float>(WINO_POS * T * c_in), *dout = d.alloc<float>(P * c_out);
-    if (!dx || !du || !dv || !dout || (bias && !db) || (res && !dr))
+    float *dm = body ? dv : d.alloc<float>(WINO_POS * T * c_out);
+    if (!dx || !du || !dv || !dm || !dout || (bias && !db) || (res && !dr))
         return fail("hipMalloc failed: out of memory");
     GemmArgs g{};
     g.A = dv;
     g.lda = c_in;
     g.B = du;
     g.ldb = c_in;
-    g.out = dv;
+    g.out = dm;
     g.ldo = c_out;
     g.M = (int)T;
     g.N = c_out;
@@ -363,7 +368,7 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
     hipError_t e = launch_wino_in(dx, c_in, dv, h, w, c_in, 0);
     if (e == hipSuccess) e = launch_gemm(g, ALOAD_ROWS, EPI_STORE, 0);
     if (e == hipSuccess)
-        e = launch_wino_out(dv, db, epilogue == 2 ? dr : nullptr, c_out, dout, c_out, h, w, c_out,
+        e = launch_wino_out(dm, db, epilogue == 2 ? dr : nullptr, c_out, dout, c_out, h, w, c_out,
                             epilogue == 5, slope, 0);
     if (int rc = finish(e, "winograd conv3x3")) return rc;
     if (hipMemcpy(out, dout, P * c_out * 4, hipMemcpyDeviceToHost) != hipSuccess)

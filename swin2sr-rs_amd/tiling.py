@@ -90,6 +90,12 @@ def _fused_octaves(arch: M.Arch) -> int:
     return 2 if arch.octaves >= 2 and arch.feat == 64 else 1
 
 
+def _wino_before_upsample(arch: M.Arch) -> bool:
+    """conv_before_upsample runs as Winograd (its products in the MLP buffer)."""
+    return (arch.upsampler in ("pixelshuffle", "pixelshuffle_aux", "nearest+conv")
+            and arch.embed in (60, 120, 180) and arch.feat % 4 == 0 and arch.feat <= 64)
+
+
 def _plan_terms(arch: M.Arch, h: int, w: int):
     """(floats per buffer) of the library's plan for an h x w image, in
     s2s_ctx::body_specs + image_specs order (host-path copies included)."""
@@ -102,7 +108,11 @@ def _plan_terms(arch: M.Arch, h: int, w: int):
     if c in (60, 120, 180):
         # the Winograd convs' 36 transform planes of 4x4-pixel tiles
         qkv = max(qkv, 36 * ((hp + 3) // 4) * ((wp + 3) // 4) * c)
-    terms = [P * c] * 3 + [qkv, P * c, P * arch.mlp_ratio * c]
+    hid = P * arch.mlp_ratio * c
+    if _wino_before_upsample(arch):
+        # conv_before_upsample's Winograd products (36 planes of F per tile)
+        hid = max(hid, 36 * ((hp + 3) // 4) * ((wp + 3) // 4) * f)
+    terms = [P * c] * 3 + [qkv, P * c, hid]
     terms += [3 * h * w, 3 * h * s * w * s, P * 4]
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
         terms += [P * 4 ** o * f for o in range(arch.octaves - _fused_octaves(arch) + 1)]
@@ -131,7 +141,11 @@ def per_pixel_floats(arch: M.Arch) -> int:
         # 36 planes per 16 pixels, at most ceil(win/4)^2 tiles per win^2 pixels
         t = (arch.window + 3) // 4
         qkv = max(qkv, -(-36 * t * t * c // (arch.window * arch.window)))
-    body = 3 * c + qkv + c + arch.mlp_ratio * c
+    hid = arch.mlp_ratio * c
+    if _wino_before_upsample(arch):
+        t = (arch.window + 3) // 4
+        hid = max(hid, -(-36 * t * t * f // (arch.window * arch.window)))
+    body = 3 * c + qkv + c + hid
     if arch.upsampler in ("pixelshuffle", "pixelshuffle_aux"):
         head = sum(f * 4 ** o for o in range(arch.octaves - _fused_octaves(arch) + 1))
         if arch.upsampler == "pixelshuffle_aux":

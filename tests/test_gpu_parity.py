@@ -223,6 +223,25 @@ def test_conv3x3_winograd(pkg, orc, h, w, c, epi):
     assert err < 5e-5, err
 
 
+@pytest.mark.parametrize("h,w,cin,cout", [(2, 2, 180, 64), (5, 7, 60, 64), (33, 39, 180, 64),
+                                         (72, 80, 120, 32), (264, 264, 180, 64), (40, 48, 180, 4)])
+@pytest.mark.parametrize("epi", [0, 5])
+def test_conv3x3_winograd_narrow(pkg, orc, h, w, cin, cout, epi):
+    """conv_before_upsample's C -> F conv (F <= 64) as the head runs it:
+    Winograd F(4x4,3x3) with the transform-domain GEMM on the weight-stationary
+    kernel's narrow (64-column) build and its products in a buffer of their
+    own, then LeakyReLU(0.01); against the oracle's direct conv."""
+    r = rng(h * w + cin * cout + epi)
+    x = r.standard_normal((cin, h, w), dtype=np.float32)
+    wt = (r.standard_normal((cout, cin, 3, 3), dtype=np.float32) / np.sqrt(9 * cin)).astype(np.float32)
+    b = r.standard_normal(cout, dtype=np.float32)
+    base = orc.conv3x3(x, wt, b)
+    want = base if epi == 0 else np.where(base < 0, base * np.float32(0.01), base)
+    got = pkg.abi.test_conv3x3_winograd(nchw_to_hwc(x), h, w, wt, b, epilogue=epi, slope=0.01)
+    err = np.abs(hwc_to_nchw(got, h, w) - want).max()
+    assert err < 5e-5, err
+
+
 @pytest.mark.parametrize("cin,feat,h,w", [(4, 3, 5, 7), (4, 4, 1, 6), (6, 24, 4, 5), (64, 64, 9, 70),
                                           (8, 8, 3, 61)])
 def test_conv3x3_shuffle2(pkg, orc, cin, feat, h, w):
