@@ -90,6 +90,16 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "up2_last": ("mfma", 2 * min(hp * s // 4, -(-h * s // 4)) * (wp * s // 4) * 48 * 25 * F,
                      f * ((hp * s // 4) * (wp * s // 4) * F + 3 * h * s * w * s)),
     }
+    if arch.upsampler == "pixelshuffle" and s == 4 and F == 64:
+        # the x4 head's composed 5x5 conv as Winograd F(2x2,5x5) over the
+        # T5 2x2 tiles of the pixels whose outputs survive the crop: the input
+        # transform (the plane in, 36 planes of T5 x F out), 36 GEMMs of
+        # T5 x 48 x F, the output transform (M in, the cropped image out)
+        ho, wo = min(hp, -(-h * s // 4)), min(wp, -(-w * s // 4))
+        T5 = 36 * ((ho + 1) // 2) * ((wo + 1) // 2)
+        work["up2_last_in"] = ("hbm", 0, f * (ho * wo * F + T5 * F))
+        work["up2_last"] = ("mfma", 2 * T5 * 48 * F, f * (T5 * (F + 48) + 36 * 48 * F))
+        work["up2_last_out"] = ("hbm", 0, f * (T5 * 48 + 3 * h * s * w * s))
     if C in (60, 120, 180) and F % 4 == 0 and F <= 64:
         # conv_before_upsample (C -> F, LeakyReLU) as Winograd F(4x4,3x3): the
         # same input transform, 36 GEMMs of T x F x C, the output transform

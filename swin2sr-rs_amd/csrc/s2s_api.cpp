@@ -137,6 +137,7 @@ struct s2s_ctx {
     // to 48 outputs, stored through pixel_shuffle(4)): [48][25F], [48],
     // [4][48][25][F], [4][48]; the last two octaves' planes are never made
     bool fuse2 = false;
+    bool up2_wino = false;  // the composed 5x5 conv as Winograd F(2x2,5x5) (u2_w [36][48][F])
     float *u2_w = nullptr, *u2_b = nullptr, *u2_we = nullptr, *u2_be = nullptr;
     int fused_octaves() const { return fuse2 ? 2 : (fuse_last ? 1 : 0); }
     // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [4][9*F] (its fourth
@@ -184,13 +185,16 @@ struct s2s_ctx {
               bool planned = false);
     // qkv buffer floats: the plane layout, or the attention unit layout; it
     // also holds the body's Winograd convs' transform-domain products (36
-    // planes of wino_tiles(hp, wp) tiles x C) between blocks
+    // planes of wino_tiles(hp, wp) tiles x C) between blocks, and the head's
     size_t qkv_floats(int hp, int wp) const {
         const size_t plane = (size_t)hp * wp * 3 * c;
         const size_t q = qkv_unit_layout(arch.heads, hd, c)
                              ? std::max(plane, attn_unit_floats(hp, wp, arch.heads, hd))
                              : plane;
-        return wino_body(c) ? std::max(q, WINO_POS * wino_tiles(hp, wp) * c) : q;
+        const size_t qb = wino_body(c) ? std::max(q, WINO_POS * wino_tiles(hp, wp) * c) : q;
+        // the x4 head's Winograd 5x5 conv: V and M (stride F) at most the
+        // whole plane's tiles
+        return up2_wino ? std::max(qb, WINO_POS * wino5_tiles(hp, wp) * feat) : qb;
     }
     // MLP hidden buffer floats; it also holds conv_before_upsample's Winograd
     // products (36 planes of wino_tiles(hp, wp) tiles x F) in the head
@@ -733,6 +737,35 @@ int s2s_ctx::head(int h, int w, float *d_out) {
             H *= 2;
             W *= 2;
         }
+        if (fuse2 && up2_wino) {
+            // the last two octaves and conv_last: one 5x5 conv to 48 channels
+            // as Winograd F(2x2,5x5) over the pixels whose outputs survive the
+            // crop (V, then M over it at a row stride of F, in the qkv
+            // buffer), stored through pixel_shuffle(4), denormalised and
+            // cropped by the output transform; then the input row 0 / column 0
+            // outputs recomputed
+            const int Ho = std::min(H, (oh + 3) / 4), Wo = std::min(W, (ow + 3) / 4);
+            const int T = (int)wino5_tiles(Ho, Wo);
+            const float *src = fplanes[octaves - 2];
+            if (run("up2_last_in", dim3(wino5_in_grid(Ho, Wo, feat)), dim3(256),
+                    [&] { return launch_wino5_in(src, feat, qkv, H, W, Ho, Wo, feat, stream); }))
+                return -1;
+            g = rows_gemm(qkv, feat, u2_w, feat, nullptr, qkv, feat, T, 48, feat);
+            g.nb = WINO_POS;
+            g.a_bstride = g.o_bstride = (size_t)T * feat;
+            g.b_bstride = (size_t)48 * feat;
+            if (gemm("up2_last", g, ALOAD_ROWS, EPI_STORE)) return -1;
+            if (run("up2_last_out", dim3(wino5_finish_grid(Ho, Wo)), dim3(256), [&] {
+                    return launch_wino5_finish(qkv, feat, u2_b, d_out, Ho, Wo, oh, ow, arch.img_range,
+                                               arch.mean, stream);
+                }))
+                return -1;
+            const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
+            return run("up2_last_edge", dim3((nb + 3) / 4), dim3(256), [&] {
+                return launch_up2_last_edge(src, u2_we, u2_be, d_out, H, W, feat, oh, ow,
+                                            arch.img_range, arch.mean, stream);
+            });
+        }
         if (fuse2) {
             // the last two octaves and conv_last: one 5x5 conv to 48 channels
             // stored through pixel_shuffle(4), denormalised and cropped, then
@@ -934,10 +967,11 @@ void compose_up_last(const float *Wo, const float *bo, const float *Wl, const fl
 // the plane dropped (o1's zero padding). Output s48 = k*16 + a*4 + b (torch's
 // pixel_shuffle(4) channel order); w48 and b48 [4][48] in
 // double, rounded once; wg [48][25*F] (variant 0, the GEMM's [n][k] with
-// k = tap*F + ci) and bg [48]; w48 [4][48][25][F].
+// k = tap*F + ci) and bg [48]; w48 [4][48][25][F]; with u5, variant 0 also as
+// Winograd F(2x2,5x5) weights [36][48][F] (wino5_weights).
 void compose_up2_last(const std::vector<float> &ue, const std::vector<float> &ub, const float *Wo,
                       const float *bo, int F, std::vector<float> &wg, std::vector<float> &bg,
-                      std::vector<float> &w48, std::vector<float> &b48) {
+                      std::vector<float> &w48, std::vector<float> &b48, std::vector<float> *u5) {
     const size_t kk = (size_t)25 * F;
     std::vector<double> W((size_t)4 * 48 * kk, 0.0), B(4 * 48, 0.0);
     for (int var = 0; var < 4; ++var) {
@@ -978,6 +1012,11 @@ void compose_up2_last(const std::vector<float> &ue, const std::vector<float> &ub
     }
     wg.assign((size_t)48 * kk, 0.f);
     for (size_t i = 0; i < (size_t)48 * kk; ++i) wg[i] = (float)W[i];
+    if (u5) {
+        // variant 0 as Winograd F(2x2,5x5) weights, from the double sums
+        u5->assign((size_t)WINO_POS * 48 * round4(F), 0.f);
+        wino5_weights(W.data(), 48, F, u5->data());
+    }
     bg.assign(B.begin(), B.begin() + 48);
     w48.assign(W.begin(), W.end());
     b48.assign(B.begin(), B.end());
@@ -1039,8 +1078,9 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
             const int oct = octaves_of(A.scale);
             f += (uint64_t)oct * (4 * F_ * 9 * F4 + 4 * F_);  // the octave convs
             if (up == S2S_PIXELSHUFFLE && F % 8 == 0) {
-                if (oct >= 2 && F == 64)
-                    f += 5 * 48 * 25 * F_ + 5 * 48;  // two octaves and conv_last composed
+                if (oct >= 2 && F == 64)     // two octaves and conv_last composed (the
+                    f += (wino_up2(oct, F) ? WINO_POS * 48 * F4 : 48 * 25 * F_)  // GEMM's,
+                         + 4 * 48 * 25 * F_ + 5 * 48;                           // the edges')
                 else
                     f += 5 * 12 * 25 * F_ + 5 * 12;  // the last octave and conv_last composed
             }
@@ -1358,10 +1398,13 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                         rc = rc || ts.get(b0 + ".weight", {4 * F, F, 3, 3}, &u0w);
                         rc = rc || ts.get(b0 + ".bias", {4 * F}, &u0b);
                         if (!rc) {
-                            std::vector<float> wg, bg, w48, b48;
-                            compose_up2_last(we, be, u0w->data, u0b->data, F, wg, bg, w48, b48);
-                            rc = ctx->upload(wg, &ctx->u2_w) || ctx->upload(bg, &ctx->u2_b) ||
-                                 ctx->upload(w48, &ctx->u2_we) || ctx->upload(b48, &ctx->u2_be);
+                            std::vector<float> wg, bg, w48, b48, u5;
+                            ctx->up2_wino = wino_up2(oct, F);
+                            compose_up2_last(we, be, u0w->data, u0b->data, F, wg, bg, w48, b48,
+                                             ctx->up2_wino ? &u5 : nullptr);
+                            rc = ctx->upload(ctx->up2_wino ? u5 : wg, &ctx->u2_w) ||
+                                 ctx->upload(bg, &ctx->u2_b) || ctx->upload(w48, &ctx->u2_we) ||
+                                 ctx->upload(b48, &ctx->u2_be);
                             ctx->fuse2 = true;
                         }
                     } else {

@@ -189,6 +189,24 @@ hipError_t launch_attention(const AttnArgs &g, hipStream_t st, unsigned *grid_ou
 // `lrelu`, into out [H*W][ldo] (the tiles' pixels inside the plane).
 constexpr int WINO_POS = 36;
 inline size_t wino_tiles(int H, int W) { return (size_t)((H + 3) / 4) * ((W + 3) / 4); }
+// Winograd F(2x2,5x5) for the x4 head's composed 5x5 conv (F = 64 -> 48, the
+// pixel_shuffle(4) finish): the same six points and B^T; the 2x2 output
+// tiles covering Ho x Wo pixels of an H x W plane, the patch origin 2t - 2.
+// wino5_weights: U = G5 g G5^T from the composed weights [48][25][F] (double,
+// rounded once) as [36][48][F]; launch_wino5_in writes V [36][T][F];
+// launch_wino5_finish takes M [36][T][ldm] (48 used) to Y = A5^T M A5 + bias,
+// pixel_shuffle(4), denormalised (v / img_range + mean) and cropped to oh x ow
+// into out [3][oh][ow].
+inline size_t wino5_tiles(int Ho, int Wo) { return (size_t)((Ho + 1) / 2) * ((Wo + 1) / 2); }
+inline bool wino_up2(int octaves, int feat) { return octaves == 2 && feat == 64; }
+void wino5_weights(const double *w, int co, int ci, float *out);
+hipError_t launch_wino5_in(const float *in, int ldi, float *v, int H, int W, int Ho, int Wo, int C,
+                           hipStream_t st);
+unsigned wino5_in_grid(int Ho, int Wo, int C);
+hipError_t launch_wino5_finish(const float *m, int ldm, const float *bias, float *out, int Ho,
+                               int Wo, int oh, int ow, float img_range, const float *mean,
+                               hipStream_t st);
+unsigned wino5_finish_grid(int Ho, int Wo);
 void wino_weights(const float *w, int co, int ci, float *out);
 // The body's C -> C convs take the Winograd path when the batched GEMM runs on
 // the weight-stationary kernel with every column in one workgroup (so it may

@@ -2516,6 +2516,10 @@ static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks
     if (g.K == 180 || g.K == 60) {
         *kpw = g.K;
         *ks = 1;
+    } else if (g.K == 64 && epi == EPI_STORE && bs_ntw(g, epi) == 1) {
+        // the x4 head's Winograd 5x5 products (64 features in, 48 out)
+        *kpw = 64;
+        *ks = 1;
     } else if (g.K == 360 || g.K == 120) {
         *kpw = g.K / 2;
         *ks = 2;
@@ -2631,6 +2635,11 @@ static int bs_rb(const GemmArgs &g, int ks, int epi) {
 static hipError_t run_bs_any(const GemmArgs &g, int kpw, int ks, int epi, hipStream_t st,
                              bool launch, dim3 *grid) {
     const int rb = bs_rb(g, ks, epi);
+    if (kpw == 64) {
+        if (ks != 1 || epi != EPI_STORE || bs_ntw(g, epi) != 1) return hipErrorInvalidValue;
+        return rb == 1 ? run_bs<64, 1, 1, EPI_STORE, 1>(g, st, launch, grid)
+                       : run_bs<64, 1, 2, EPI_STORE, 1>(g, st, launch, grid);
+    }
     if (kpw == 180) {
         if (ks == 1) return rb == 1 ? run_bs_e<180, 1, 1>(g, epi, st, launch, grid)
                                     : run_bs_e<180, 1, 2>(g, epi, st, launch, grid);
@@ -2874,12 +2883,14 @@ template <int NE> __device__ __forceinline__ void st_vec(float *p, const float *
 #define WINO_OUT_NE 2
 #endif
 
-// Input transform: tile (ty, tx) of the (H/4) x (W/4) grid (rounded up),
-// channels c .. c+NE-1: its 6x6 patch d (rows 4ty-1 .. 4ty+4, columns 4tx-1
-// .. 4tx+4, zero outside the plane) to V = B^T d B, stored as
-// V[6 xi + nu][tile][c]. One thread per (tile, NE channels); consecutive
-// threads read and write consecutive channel groups.
-template <int NE>
+// Input transform: tile (ty, tx) of the grid of MT x MT output tiles that
+// covers Ho x Wo (rounded up), channels c .. c+NE-1: its 6x6 patch d (rows
+// MT ty - PAD .. MT ty - PAD + 5, the same for columns, zero outside the H x W
+// plane) to V = B^T d B, stored as V[6 xi + nu][tile][c]. F(4x4,3x3) takes
+// MT = 4, PAD = 1; F(2x2,5x5) MT = 2, PAD = 2 - the same B^T for the same six
+// points. One thread per (tile, NE channels); consecutive threads read and
+// write consecutive channel groups.
+template <int NE, int MT, int PAD>
 __global__ __launch_bounds__(256) void k_wino_in(const float *__restrict__ in, int ldi,
                                                   float *__restrict__ v, int H, int W, int C,
                                                   int T, int tw) {
@@ -2894,7 +2905,7 @@ __global__ __launch_bounds__(256) void k_wino_in(const float *__restrict__ in, i
     for (int r = 0; r < 6; ++r)
 #pragma unroll
         for (int q = 0; q < 6; ++q) {
-            const int y = 4 * ty - 1 + r, x = 4 * tx - 1 + q;
+            const int y = MT * ty - PAD + r, x = MT * tx - PAD + q;
             if ((unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W) {
                 ld_vec<NE>(in + ((size_t)y * W + x) * ldi + c, p[r][q]);
             } else {
@@ -2925,8 +2936,22 @@ hipError_t launch_wino_in(const float *in, int ldi, float *v, int H, int W, int 
     if (H < 1 || W < 1 || C % 4 || ldi % 4) return hipErrorInvalidValue;
     const int tw = (W + 3) / 4;
     const int T = (int)wino_tiles(H, W);
-    hipLaunchKernelGGL(k_wino_in<WINO_IN_NE>, dim3(wino_in_grid(H, W, C)), dim3(256), 0, st, in,
-                       ldi, v, H, W, C, T, tw);
+    hipLaunchKernelGGL((k_wino_in<WINO_IN_NE, 4, 1>), dim3(wino_in_grid(H, W, C)), dim3(256), 0, st,
+                       in, ldi, v, H, W, C, T, tw);
+    return hipGetLastError();
+}
+
+unsigned wino5_in_grid(int Ho, int Wo, int C) {
+    return (unsigned)(((long long)wino5_tiles(Ho, Wo) * (C / WINO_IN_NE) + 255) / 256);
+}
+
+hipError_t launch_wino5_in(const float *in, int ldi, float *v, int H, int W, int Ho, int Wo, int C,
+                           hipStream_t st) {
+    if (H < 1 || W < 1 || Ho < 1 || Wo < 1 || C % 4 || ldi % 4) return hipErrorInvalidValue;
+    const int tw = (Wo + 1) / 2;
+    const int T = (int)wino5_tiles(Ho, Wo);
+    hipLaunchKernelGGL((k_wino_in<WINO_IN_NE, 2, 2>), dim3(wino5_in_grid(Ho, Wo, C)), dim3(256), 0,
+                       st, in, ldi, v, H, W, C, T, tw);
     return hipGetLastError();
 }
 
@@ -3006,6 +3031,114 @@ hipError_t launch_wino_out(const float *m, const float *bias, const float *res, 
     hipLaunchKernelGGL(k_wino_out<WINO_OUT_NE>, dim3(wino_out_grid(H, W, C)), dim3(256), 0, st, m,
                        bias, res, ldr, out, ldo, H, W, C, T, tw, lrelu, slope);
     return hipGetLastError();
+}
+
+// F(2x2,5x5) output transform with the x4 head's finish: tile (ty, tx) of
+// the 2x2 tiles covering Ho x Wo input pixels, channels n, n+1 of the 48 (in
+// torch's pixel_shuffle(4) order n = 16k + 4a + b, b even): M[6 xi + nu][tile]
+// [n] (row stride ldm) to Y = A^T M A with
+//   A^T = [1  1    1    1    1   0]
+//         [0 3/2 -3/2  2/3 -2/3  1]
+// + bias. Input pixel (y, x) = (2ty + r, 2tx + c) holds image pixels
+// (4y + a, 4x + b) and (4y + a, 4x + b + 1) of channel k, denormalised as
+// v / img_range + mean[k] and cropped to oh x ow, into out [3][oh][ow].
+__global__ __launch_bounds__(256) void k_wino5_finish(const float *__restrict__ m, int ldm,
+                                                       const float *__restrict__ bias,
+                                                       float *__restrict__ out, int T, int tw,
+                                                       int Ho, int Wo, int oh, int ow,
+                                                       float img_range, float mean0, float mean1,
+                                                       float mean2) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)T * 24) return;
+    const int tile = (int)(i / 24);
+    const int n = 2 * (int)(i - (long long)tile * 24);
+    const size_t plane = (size_t)T * ldm;
+    const float *src = m + (size_t)tile * ldm + n;
+    auto at2 = [](const float *v, int s, float &y0, float &y1) {
+        const float s12 = v[s] + v[2 * s], d12 = v[s] - v[2 * s];
+        const float s34 = v[3 * s] + v[4 * s], d34 = v[3 * s] - v[4 * s];
+        y0 = v[0] + s12 + s34;
+        y1 = fmaf(1.5f, d12, fmaf(2.f / 3.f, d34, v[5 * s]));
+    };
+    float t[6][2][2];  // [xi][output column][channel]
+#pragma unroll
+    for (int xi = 0; xi < 6; ++xi) {
+        float mr[6][2];
+#pragma unroll
+        for (int nu = 0; nu < 6; ++nu) ld_vec<2>(src + (6 * xi + nu) * plane, mr[nu]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) at2(&mr[0][e], 2, t[xi][0][e], t[xi][1][e]);
+    }
+    float y[2][2][2];  // [output row][output column][channel]
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) at2(&t[0][c][e], 4, y[0][c][e], y[1][c][e]);
+    const float b0 = bias[n], b1 = bias[n + 1];
+    const int k = n >> 4, a = (n >> 2) & 3, b = n & 3;
+    const float mk = k == 0 ? mean0 : (k == 1 ? mean1 : mean2);
+    const int ty = tile / tw, tx = tile - (tile / tw) * tw;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int py = 2 * ty + r, px = 2 * tx + c;
+            const int oy = 4 * py + a, ox = 4 * px + b;
+            if (py >= Ho || px >= Wo || oy >= oh || ox >= ow) continue;
+            float *dst = out + ((size_t)k * oh + oy) * ow + ox;
+            const float v0 = (y[r][c][0] + b0) / img_range + mk;
+            const float v1 = (y[r][c][1] + b1) / img_range + mk;
+            if (ox + 1 < ow && !(ow & 1)) {
+                *reinterpret_cast<float2 *>(dst) = make_float2(v0, v1);
+            } else {
+                dst[0] = v0;
+                if (ox + 1 < ow) dst[1] = v1;
+            }
+        }
+}
+
+unsigned wino5_finish_grid(int Ho, int Wo) {
+    return (unsigned)(((long long)wino5_tiles(Ho, Wo) * 24 + 255) / 256);
+}
+
+hipError_t launch_wino5_finish(const float *m, int ldm, const float *bias, float *out, int Ho,
+                               int Wo, int oh, int ow, float img_range, const float *mean,
+                               hipStream_t st) {
+    if (Ho < 1 || Wo < 1 || ldm < 48 || ldm % 2 || !bias) return hipErrorInvalidValue;
+    const int tw = (Wo + 1) / 2;
+    const int T = (int)wino5_tiles(Ho, Wo);
+    hipLaunchKernelGGL(k_wino5_finish, dim3(wino5_finish_grid(Ho, Wo)), dim3(256), 0, st, m, ldm,
+                       bias, out, T, tw, Ho, Wo, oh, ow, img_range, mean[0], mean[1], mean[2]);
+    return hipGetLastError();
+}
+
+// U = G5 g G5^T per (co, ci) for F(2x2,5x5) with the points above,
+//   G5 = [1        0       0      0       0     ]
+//        [8/65     12/65   18/65  27/65   81/130]
+//        [8/65    -12/65   18/65 -27/65   81/130]
+//        [-81/130 -27/65  -18/65 -12/65  -8/65  ]
+//        [-81/130  27/65  -18/65  12/65  -8/65  ]
+//        [0        0       0      0       1     ],
+// from weights w [co][25][ci] (tap-major, in double) as [36][co][round4(ci)].
+void wino5_weights(const double *w, int co, int ci, float *out) {
+    static const double G[6][5] = {{1, 0, 0, 0, 0},
+                                   {8.0 / 65, 12.0 / 65, 18.0 / 65, 27.0 / 65, 81.0 / 130},
+                                   {8.0 / 65, -12.0 / 65, 18.0 / 65, -27.0 / 65, 81.0 / 130},
+                                   {-81.0 / 130, -27.0 / 65, -18.0 / 65, -12.0 / 65, -8.0 / 65},
+                                   {-81.0 / 130, 27.0 / 65, -18.0 / 65, 12.0 / 65, -8.0 / 65},
+                                   {0, 0, 0, 0, 1}};
+    const int cp = (ci + 3) / 4 * 4;
+    for (size_t i = 0; i < (size_t)WINO_POS * co * cp; ++i) out[i] = 0.f;
+    for (int o = 0; o < co; ++o)
+        for (int i = 0; i < ci; ++i)
+            for (int xi = 0; xi < 6; ++xi)
+                for (int nu = 0; nu < 6; ++nu) {
+                    double u = 0.0;
+                    for (int a = 0; a < 5; ++a)
+                        for (int b = 0; b < 5; ++b)
+                            u += G[xi][a] * w[((size_t)o * 25 + 5 * a + b) * ci + i] * G[nu][b];
+                    out[((size_t)(6 * xi + nu) * co + o) * cp + i] = (float)u;
+                }
 }
 
 // U = G g G^T per (co, ci) with G above, accumulated in double and rounded

@@ -96,6 +96,11 @@ def _wino_before_upsample(arch: M.Arch) -> bool:
             and arch.embed in (60, 120, 180) and arch.feat % 4 == 0 and arch.feat <= 64)
 
 
+def _wino_up2(arch: M.Arch) -> bool:
+    """The x4 head's composed 5x5 conv runs as Winograd F(2x2,5x5)."""
+    return _fused_octaves(arch) == 2 and arch.octaves == 2
+
+
 def _plan_terms(arch: M.Arch, h: int, w: int):
     """(floats per buffer) of the library's plan for an h x w image, in
     s2s_ctx::body_specs + image_specs order (host-path copies included)."""
@@ -108,6 +113,9 @@ def _plan_terms(arch: M.Arch, h: int, w: int):
     if c in (60, 120, 180):
         # the Winograd convs' 36 transform planes of 4x4-pixel tiles
         qkv = max(qkv, 36 * ((hp + 3) // 4) * ((wp + 3) // 4) * c)
+    if _wino_up2(arch):
+        # the x4 head's Winograd 5x5 conv: 36 planes of 2x2-pixel tiles x F
+        qkv = max(qkv, 36 * ((hp + 1) // 2) * ((wp + 1) // 2) * f)
     hid = P * arch.mlp_ratio * c
     if _wino_before_upsample(arch):
         # conv_before_upsample's Winograd products (36 planes of F per tile)
@@ -141,6 +149,9 @@ def per_pixel_floats(arch: M.Arch) -> int:
         # 36 planes per 16 pixels, at most ceil(win/4)^2 tiles per win^2 pixels
         t = (arch.window + 3) // 4
         qkv = max(qkv, -(-36 * t * t * c // (arch.window * arch.window)))
+    if _wino_up2(arch):
+        t = (arch.window + 1) // 2
+        qkv = max(qkv, -(-36 * t * t * f // (arch.window * arch.window)))
     hid = arch.mlp_ratio * c
     if _wino_before_upsample(arch):
         t = (arch.window + 3) // 4

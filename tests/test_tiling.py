@@ -65,17 +65,19 @@ def test_per_pixel_floats_stays_within_the_crates_device_model(pkg):
 def test_plan_floats_counts_the_unit_layout_and_the_composed_octaves(pkg):
     """The terms the old figure missed: the qkv buffer's real size (the
     attention's unit layout, (heads+1)/2 x (6 hd + 2) floats a pixel = 546 at
-    hd = 30, or the Winograd convs' 36 transform planes of 4x4-pixel tiles,
-    9 C / 4 = 405 floats a pixel, between blocks, whichever is larger) and the
-    head planes the composed octaves never allocate."""
+    hd = 30; the body's Winograd convs' 36 transform planes of 4x4-pixel
+    tiles, 9 C / 4 = 405 floats a pixel; the x4 head's Winograd 5x5 conv's 36
+    planes of 2x2-pixel tiles of F = 64, 576 a pixel: whichever is largest)
+    and the head planes the composed octaves never allocate."""
     M, T = pkg.model, pkg.tiling
     a = M.classical(4)
     P = 264 * 264
     terms = T._plan_terms(a, 256, 256)
-    assert terms[3] == P * 546                  # qkv: the unit layout (546) > Winograd products (405)
+    assert terms[3] == P * 576                  # qkv: the head's 5x5 products > unit layout (546)
+    assert T._plan_terms(M.classical(2), 256, 256)[3] == P * 546  # x2: no 5x5 conv
     assert terms[-1] == P * 64                  # one head plane: both octaves composed
     assert T.plan_floats(M.classical(2), 256, 256) - T.plan_floats(a, 256, 256) == \
-        3 * 256 * 256 * (4 - 16)                # x2: one composed octave, plane 0 only
+        3 * 256 * 256 * (4 - 16) - P * 30       # x2: one composed octave, plane 0 only; no 5x5
 
 
 def test_auto_tile(pkg):
