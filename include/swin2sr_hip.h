@@ -147,8 +147,8 @@ int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_o
  * serving loops, harnesses that forbid it. The caller passes the device input
  * and output as for `s2s_forward_device`; enqueued on the context's stream,
  * not synchronised. Planes whose buffers do not fit the workspace are refused
- * with an error (classical x4 at C = 180: padded planes up to ~35,800 pixels,
- * i.e. images up to 183 x 183; `s2s_plan_bytes` less the two host-path copies
+ * with an error (classical x4 at C = 180: padded planes up to ~38,900 pixels,
+ * i.e. images up to 191 x 191; `s2s_plan_bytes` less the two host-path copies
  * is the figure). Every call on one GPU shares that GPU's workspace, which
  * keeps the last call's contents: calls that overlap on one GPU (other
  * contexts or streams) race. */
