@@ -56,6 +56,10 @@ def kernel_work(arch, h, w, hp=None, wp=None):
     f = 4
     work = {
         "qkv": ("mfma", 2 * P * 3 * C * C, f * P * (C + 3 * C)),
+        # 6 heads of 30: the qkv projection and the window attention as one
+        # kernel (x in, the attention output out; q, k, v stay on the CU)
+        "qkv_window_attention": ("mfma", 2 * P * 3 * C * C + 4 * P * win * win * C,
+                                 f * (P * 2 * C + 3 * C * C)),
         "window_attention": ("mfma", 4 * P * win * win * C, f * P * (3 * C + C)),
         "proj_ln_res": ("mfma", 2 * P * C * C, f * P * 3 * C),
         "fc1_gelu": ("mfma", 2 * P * Hd * C, f * P * (C + Hd)),

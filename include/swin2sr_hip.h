@@ -253,9 +253,11 @@ int s2s_test_qkv_windows(int hp, int wp, int heads, int head_dim, int shift, con
 /* The production attention half of a block: the qkv GEMM above, then the
  * window attention with the shift mask (`Plan::region`, reference
  * src/plan.rs:84-108) and the scatter back to the plane (`cpu::scatter`,
- * src/cpu.rs:1200-1222), exactly as the forward launches them. `x` is
- * `[hp*wp][c]`, `cpb` `[n*n][heads]` (the checkpoint's cpb_pre layout), `out`
- * `[hp*wp][c]`. */
+ * src/cpu.rs:1200-1222), exactly as the forward launches them - for 6 heads
+ * of 30 as the forward's one fused kernel (the qkv projection and the
+ * attention together, the projection's shifted-window gather inside it).
+ * `x` is `[hp*wp][c]`, `wqkv` the fused `[3c][c]` (rows q, k, v), `cpb`
+ * `[n*n][heads]` (the checkpoint's cpb_pre layout), `out` `[hp*wp][c]`. */
 int s2s_test_block_attention(int hp, int wp, int heads, int head_dim, int shift, const float *x,
                              const float *wqkv, const float *bqkv, const float *logit_scale,
                              const float *cpb, float *out);

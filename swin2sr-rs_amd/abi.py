@@ -312,7 +312,8 @@ def test_qkv_windows(hp, wp, heads, head_dim, shift, x, wqkv, bqkv):
 
 
 def test_block_attention(hp, wp, heads, head_dim, shift, x, wqkv, bqkv, logit_scale, cpb):
-    """The production qkv GEMM + window attention; the plane [hp*wp][c]."""
+    """The production qkv projection + window attention (one fused kernel for
+    6 heads of 30); the plane [hp*wp][c]."""
     lib = load_library()
     c = heads * head_dim
     out = np.empty((hp * wp, c), np.float32)

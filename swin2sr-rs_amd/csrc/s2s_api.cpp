@@ -547,16 +547,34 @@ GemmArgs conv_gemm(const float *in, int H, int W, int cin, const float *wt, cons
 int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *x_in,
                        float *x_out) {
     const int P = hp * wp;
-    // qkv straight into the window attention's unit layout where its kernel
-    // takes the head shape, else the plane layout [P][3c]
     GemmArgs g;
-    const int epi = qkv_gemm_args(x_in, b.wqkv, b.bqkv, qkv, hp, wp, shift, arch.heads, hd, &g);
-    if (gemm("qkv", g, ALOAD_ROWS, epi)) return -1;
-    const AttnArgs a = window_attn_args(qkv, b.cpbt, b.ls, o, hp, wp, shift, arch.heads, hd);
-    const unsigned ag = attention_grid(a);
-    if (run("window_attention", dim3(ag), dim3(256),
-            [&] { return launch_attention(a, stream, nullptr); }))
-        return -1;
+    if (qkv_attn_fused(arch.heads, hd)) {
+        // 6 heads of 30: the qkv projection and the window attention as one
+        // kernel (the head pair's q, k, v never leave the CU)
+        QkvAttnArgs a{};
+        a.x = x_in;
+        a.w = b.wqkv;
+        a.bias = b.bqkv;
+        a.cpbt = b.cpbt;
+        a.logit_scale = b.ls;
+        a.out = o;
+        a.hp = hp;
+        a.wp = wp;
+        a.shift = shift;
+        if (run("qkv_window_attention", dim3(qkv_attention_grid(hp, wp)), dim3(256),
+                [&] { return launch_qkv_attention(a, stream, nullptr); }))
+            return -1;
+    } else {
+        // qkv straight into the window attention's unit layout where its
+        // kernel takes the head shape, else the plane layout [P][3c]
+        const int epi = qkv_gemm_args(x_in, b.wqkv, b.bqkv, qkv, hp, wp, shift, arch.heads, hd, &g);
+        if (gemm("qkv", g, ALOAD_ROWS, epi)) return -1;
+        const AttnArgs a = window_attn_args(qkv, b.cpbt, b.ls, o, hp, wp, shift, arch.heads, hd);
+        const unsigned ag = attention_grid(a);
+        if (run("window_attention", dim3(ag), dim3(256),
+                [&] { return launch_attention(a, stream, nullptr); }))
+            return -1;
+    }
 
     g = rows_gemm(o, c, b.wproj, c, b.bproj, x_out, c, P, c, c);
     g.res = x_in;
@@ -1279,6 +1297,14 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             std::copy(wv->data, wv->data + (size_t)C * C, wqkv.begin() + (size_t)2 * C * C);
             std::copy(qb->data, qb->data + C, bqkv.begin());
             std::copy(vb->data, vb->data + C, bqkv.begin() + 2 * C);
+            if (qkv_attn_fused(NH, C / NH)) {
+                // the fused qkv + attention kernel's order: each head pair's
+                // q|k|v rows as the attention unit's columns
+                std::vector<float> wp(wqkv.size()), bp(bqkv.size());
+                qkv_pair_weights(wqkv.data(), bqkv.data(), NH, C / NH, wp.data(), bp.data());
+                wqkv.swap(wp);
+                bqkv.swap(bp);
+            }
             rc = rc || ctx->upload(wqkv, &bw.wqkv) || ctx->upload(bqkv, &bw.bqkv);
             const s2s_tensor *lsx;
             rc = rc || ts.get(p + "attn.logit_scale", {NH, 1, 1}, &lsx);

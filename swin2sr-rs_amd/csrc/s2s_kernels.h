@@ -118,6 +118,31 @@ struct AttnArgs {
     int nws;                   // k_wattn: window lanes per XCD (set by launch_attention)
 };
 
+// A block's qkv projection and window attention in one kernel (k_qkv_wattn)
+// for 6 heads of 30: x [hp*wp][180], the q|k|v weight rows of each head pair
+// in the attention unit's column order w [3][180][180] and bias [3][180]
+// (qkv_pair_weights), the CPB table and logit scales as for AttnArgs; out
+// [hp*wp][180].
+struct QkvAttnArgs {
+    const float *x;
+    const float *w;
+    const float *bias;
+    const float *cpbt;         // [6][64][64], CPB bias x ATTN_LOG2E
+    const float *logit_scale;  // [6]
+    float *out;
+    int hp, wp, nww, nw;
+    int shift;
+    int nws;                   // window lanes per XCD (set by launch_qkv_attention)
+};
+inline bool qkv_attn_fused(int heads, int hd) { return heads == 6 && hd == 30; }
+// The fused [3c][c] qkv weight (rows q, k, v) and bias [3c] re-laid out per
+// head pair: w_out [heads/2][6 hd][c] with rows [q_2p | q_2p+1 | k_2p |
+// k_2p+1 | v_2p | v_2p+1], b_out [heads/2][6 hd] alike.
+void qkv_pair_weights(const float *w, const float *b, int heads, int hd, float *w_out,
+                      float *b_out);
+hipError_t launch_qkv_attention(const QkvAttnArgs &g, hipStream_t st, unsigned *grid_out);
+unsigned qkv_attention_grid(int hp, int wp);
+
 // A block's qkv projection as the forward launches it: x [hp*wp][c] times
 // the fused [3c][c] weight plus [q_bias | 0 | v_bias], written in the window
 // attention's unit layout (EPI_QKV_WIN; A rows read in the block's

@@ -1656,6 +1656,330 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// k_qkv_wattn: a block's qkv projection and window attention in one kernel,
+// for 6 heads of 30 (C = 180: the released classical, real-world and
+// compressed checkpoints). The unit a head pair's attention reads never
+// leaves the CU: a workgroup owns one head pair and walks windows as k_wattn
+// does, and per window
+//   - copies the window's 64 token rows of x (the block's shifted-window
+//     order, torch.roll's wrap at the plane edge, as EPI_QKV_WIN gathers them)
+//     into LDS by buffer_load ... lds, as a 64 x 180 A tile;
+//   - multiplies them by the pair's 180 q|k|v weight rows held in registers
+//     (the weight-stationary layout of k_bsgemm: wave w owns columns
+//     48w .. 48w + 47, the transposed 16x16x4 tile, 64 rows as 4 row blocks);
+//   - writes the products (+ bias) over the A tile as the attention's unit,
+//     [q_A | q_B | k_A | k_B | v_A | v_B | 1 | 0] per token (the weight rows
+//     are stored in that order at upload), and then runs k_wattn's
+//     per-window attention on it, its output stored through the plane's
+//     shifted-window pixels.
+// The A tile and the unit share one 48 KiB buffer, so two workgroups run per
+// CU and one's copy overlaps the other's arithmetic. Window assignment as in
+// k_wattn: workgroup b on XCD b % 8, its slot fixing the head pair and a
+// window lane, so the three head pairs of a window read its rows from the
+// same L2.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
+    constexpr int HD = 30, C = 180, HG = 3;
+    constexpr int NS = HD / 2;          // attention MFMA k-steps over d
+    constexpr int G4 = HD / 4;          // float2 pairs of steps
+    constexpr int W2 = 2 * HD;          // floats per segment (two heads)
+    constexpr int RS = attn_unit_stride(HD);  // unit row stride (182)
+    constexpr int GK = C / 16;          // GEMM k-groups of 16 (11), then one of 4
+    constexpr int S = C / 4;            // weight registers per column tile (45)
+    constexpr int BUFF = 64 * RS;       // floats: the unit, over the 64 x 180 A tile
+    static_assert(64 * C <= BUFF, "the A tile fits the unit's buffer");
+    constexpr int NST = 4;              // output stores per thread
+    constexpr int SUM_E = 4 * (HD / 8) + (HD % 8) % 4;
+    constexpr int SUM_HH = (HD % 8) / 4;
+    __shared__ __attribute__((aligned(16))) float buf[BUFF];
+    __shared__ __attribute__((aligned(16))) float prm[192];
+
+    const int xcd = blockIdx.x & 7;
+    const int slot = blockIdx.x >> 3;
+    const int hg = slot % HG;
+    const int ws = slot / HG;
+    const int wstep = 8 * g.nws;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int hl = wave >> 1;
+    const int qt = wave & 1;
+    const int r = lane & 31;
+    const int hh = lane >> 5;
+    const int shift = g.shift;
+    const int head = 2 * hg + hl;
+    const int qtok = 32 * qt + r;
+
+    // ---- the pair's weights, once: wave w, column tile t, MFMA A row j is
+    // unit column 48w + 16t + j; step 4gi + i takes k = 16gi + 4q + i, the
+    // tail step k = 176 + q ----
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(g.w + (size_t)hg * C * C, (size_t)C * C * 4);
+    float bw[3][S];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        const int cl = 48 * wave + 16 * t + j;
+        const int boff = cl < C ? cl * C * 4 : BUF_OOB;
+#pragma unroll
+        for (int gi = 0; gi < GK; ++gi) {
+            const float4 v = buf_load4(rw, boff + (16 * gi + 4 * q) * 4);
+            bw[t][4 * gi + 0] = v.x;
+            bw[t][4 * gi + 1] = v.y;
+            bw[t][4 * gi + 2] = v.z;
+            bw[t][4 * gi + 3] = v.w;
+        }
+        bw[t][4 * GK] = buf_load1(rw, boff + (16 * GK + q) * 4);
+    }
+    if (tid < 192) prm[tid] = tid < C ? g.bias[hg * C + tid] : 0.f;
+
+    // ---- the A tile copy: one instruction per token row (45 lanes x 16 B =
+    // 720 B; the other lanes are masked off), token t of the window at LDS
+    // row t, its plane pixel (torch.roll's wrap at the plane edge) as the
+    // scalar offset; wave w copies tokens w, w + 4, ... ----
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(g.x, (size_t)g.hp * g.wp * C * 4);
+    auto copy_a = [&](int wi) __attribute__((always_inline)) {
+        const int wh = __builtin_amdgcn_readfirstlane(wi / g.nww);
+        const int ww = __builtin_amdgcn_readfirstlane(wi - wh * g.nww);
+        if (lane < C / 4) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                // (scalar: the token is the same for the whole wave)
+                const int t = __builtin_amdgcn_readfirstlane(tid >> 6) + 4 * u;
+                int y = 8 * wh + (t >> 3) + shift;
+                if (y >= g.hp) y -= g.hp;
+                int x = 8 * ww + (t & 7) + shift;
+                if (x >= g.wp) x -= g.wp;
+                dma16s(rx, buf + t * C, 16 * lane,
+                       __builtin_amdgcn_readfirstlane((y * g.wp + x) * C * 4));
+            }
+        }
+    };
+
+    // ---- attention state (k_wattn's) ----
+    const float ls = ATTN_LOG2E * __expf(fminf(g.logit_scale[head], 4.605170185988092f));
+    const float *cp = g.cpbt + ((size_t)head * 64 + qtok) * 64 + 4 * hh;
+    f16v s[2];
+    auto load_bias = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float4 b4 = *reinterpret_cast<const float4 *>(cp + 32 * kt + 8 * a);
+                s[kt][4 * a + 0] = b4.x;
+                s[kt][4 * a + 1] = b4.y;
+                s[kt][4 * a + 2] = b4.z;
+                s[kt][4 * a + 3] = b4.w;
+            }
+    };
+    // copy-out: 4 tokens per instruction, 16 lanes each (lane 16t + c takes
+    // float4 c of token 16u + 4w + t; 15 float4s a token, lane 15 repeats 14)
+    const int otq = lane >> 4;
+    const int oc4 = min(lane & 15, W2 / 4 - 1);
+    const int otj = 4 * (wave & 1) + otq;
+    const float *const ldso = buf + (4 * wave + otq) * RS + 4 * oc4;
+    const int colo = (hg * W2 + 4 * oc4) * 4;
+    const __amdgpu_buffer_rsrc_t ro = buf_rsrc(g.out, (size_t)g.hp * g.wp * C * 4);
+
+    int wi = xcd + 8 * ws;
+    if (wi < g.nw) copy_a(wi);
+    // as many dropped stores as a window's output has: the loop is entered
+    // with the same queue (the copy, then stores) as it loops back with
+    {
+        const __amdgpu_buffer_rsrc_t rnull = buf_rsrc(g.out, 0);
+#pragma unroll
+        for (int u = 0; u < NST; ++u) buf_store4(rnull, 16 * u, make_float4(0.f, 0.f, 0.f, 0.f));
+    }
+    while (wi < g.nw) {
+        // ---- the window's A tile has landed (outstanding: at most the
+        // previous window's stores) ----
+        WAIT_VMCNT(NST);
+        lds_sync();
+        const int wn = wi + wstep;
+        const int wh = wi / g.nww;
+        const int ww = wi - wh * g.nww;
+
+        // ---- q|k|v of the pair: 64 tokens x 180 unit columns ----
+        f4v acc[4][3];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                const float4 b4 = *reinterpret_cast<const float4 *>(&prm[48 * wave + 16 * t + 4 * q]);
+                acc[rb][t] = f4v{b4.x, b4.y, b4.z, b4.w};
+            }
+#pragma unroll
+        for (int gi = 0; gi < GK; ++gi) {
+            float av[4][4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const float4 a = *reinterpret_cast<const float4 *>(&buf[(16 * rb + j) * C + 16 * gi + 4 * q]);
+                av[rb][0] = a.x;
+                av[rb][1] = a.y;
+                av[rb][2] = a.z;
+                av[rb][3] = a.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                    for (int t = 0; t < 3; ++t) acc[rb][t] = MFMA16(bw[t][4 * gi + i], av[rb][i], acc[rb][t]);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const float a = buf[(16 * rb + j) * C + 16 * GK + q];
+#pragma unroll
+            for (int t = 0; t < 3; ++t) acc[rb][t] = MFMA16(bw[t][4 * GK], a, acc[rb][t]);
+        }
+        lds_sync();  // every wave has read the A tile
+        // ---- the unit over it: lane (j, q) holds token 16rb + j, unit
+        // columns 48w + 16t + 4q .. + 3; column 180 is the ones column ----
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                // (only wave 3's last tile runs past column 179: lanes q > 0)
+                const int col = 48 * wave + 16 * t + 4 * q;
+                if (t < 2 || col < C) {
+                    float *dst = &buf[(16 * rb + j) * RS + col];
+                    *reinterpret_cast<float2 *>(dst) = make_float2(acc[rb][t][0], acc[rb][t][1]);
+                    *reinterpret_cast<float2 *>(dst + 2) = make_float2(acc[rb][t][2], acc[rb][t][3]);
+                }
+            }
+        if (tid < 64) buf[tid * RS + 6 * HD] = 1.0f;
+        // S^T starts from the bias (the accumulators are free again)
+        load_bias();
+        lds_sync();
+
+        // ---- the attention of head 2hg + hl, queries 32qt .. 32qt + 31 ----
+        f16v o;
+        float inv;
+        {
+            float qop[NS];
+            {
+                const float *qrow = buf + qtok * RS + hl * HD;
+#pragma unroll
+                for (int s2 = 0; s2 < G4; ++s2) {
+                    const float2 v = *reinterpret_cast<const float2 *>(qrow + 4 * s2 + 2 * hh);
+                    qop[2 * s2] = v.x;
+                    qop[2 * s2 + 1] = v.y;
+                }
+                qop[NS - 1] = qrow[4 * G4 + hh];
+                float qs = 0.f;
+#pragma unroll
+                for (int k = 0; k < NS; ++k) qs += qop[k] * qop[k];
+                qs = half_sum(qs);
+                const float qsc = ls * __builtin_amdgcn_rsqf(fmaxf(qs, 1e-24f));
+#pragma unroll
+                for (int k = 0; k < NS; ++k) qop[k] *= qsc;
+            }
+            // one key tile at a time (the weights hold 135 registers
+            // throughout): S^T rows 32kt .. 32kt + 31
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                float kop[NS];
+                const float *krow = buf + (32 * kt + r) * RS + W2 + hl * HD;
+#pragma unroll
+                for (int s2 = 0; s2 < G4; ++s2) {
+                    const float2 v = *reinterpret_cast<const float2 *>(krow + 4 * s2 + 2 * hh);
+                    kop[2 * s2] = v.x;
+                    kop[2 * s2 + 1] = v.y;
+                }
+                kop[NS - 1] = krow[4 * G4 + hh];
+                float ks = 0.f;
+#pragma unroll
+                for (int k = 0; k < NS; ++k) ks += kop[k] * kop[k];
+                ks = half_sum(ks);
+                const float ksc = __builtin_amdgcn_rsqf(fmaxf(ks, 1e-24f));
+#pragma unroll
+                for (int k = 0; k < NS; ++k) kop[k] *= ksc;
+#pragma unroll
+                for (int k = 0; k < NS; ++k) s[kt] = MFMA32(kop[k], qop[k], s[kt]);
+            }
+            // shift mask (last window row / column of a shifted block), softmax
+            const bool ey = shift && (wh * 8 + 8 >= g.hp);
+            const bool ex = shift && (ww * 8 + 8 >= g.wp);
+            const bool qy = (qtok >> 3) < 8 - shift;
+            const bool qx = (qtok & 7) < 8 - shift;
+            if (ey || ex) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int krw = 4 * kt + (e >> 2);
+                        const int kcl = 4 * hh + (e & 3);
+                        const bool dy = ey && ((krw < 8 - shift) != qy);
+                        const bool dx = ex && ((kcl < 8 - shift) != qx);
+                        if (dy || dx) s[kt][e] -= 100.f * ATTN_LOG2E;
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
+            mx = half_max(mx);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[kt][e] = __builtin_amdgcn_exp2f(s[kt][e] - mx);
+            // O^T = V^T P^T; lane r = HD reads the ones column, so row HD of
+            // O^T is the softmax denominator
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[e] = 0.f;
+            const float *vcol = r == HD ? buf + 6 * HD : buf + 2 * W2 + hl * HD + min(r, HD - 1);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                float vv[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    vv[e] = vcol[(32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3)) * RS];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o = MFMA32(vv[e], s[kt][e], o);
+            }
+            float lo, hi;
+            halves(o[SUM_E], lo, hi);
+            inv = 1.0f / (SUM_HH ? hi : lo);
+        }
+        // into this wave's own q rows (the other head's waves read other
+        // columns of them)
+        {
+            float *orow = buf + qtok * RS + hl * HD;
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+                const int d = 8 * (e >> 2) + 4 * hh + (e & 3);
+                if (d < HD)
+                    *reinterpret_cast<float2 *>(orow + d) = make_float2(o[e] * inv, o[e + 1] * inv);
+            }
+        }
+        lds_sync();
+        float4 ov[NST];
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const float *src = ldso + 16 * u * RS;
+            const float2 a = *reinterpret_cast<const float2 *>(src);
+            const float2 b = *reinterpret_cast<const float2 *>(src + 2);
+            ov[u] = make_float4(a.x, a.y, b.x, b.y);
+        }
+        lds_sync();  // every wave has read the buffer: the next A tile may land
+        if (wn < g.nw) copy_a(wn);
+        {
+            int x = 8 * ww + otj + shift;
+            if (x >= g.wp) x -= g.wp;
+            const int xo = x * C * 4 + colo;
+#pragma unroll
+            for (int u = 0; u < NST; ++u) {
+                int y = 8 * wh + 2 * u + (wave >> 1) + shift;
+                if (y >= g.hp) y -= g.hp;
+                buf_store4s(ro, xo, y * g.wp * C * 4, ov[u]);
+            }
+        }
+        wi = wn;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Streaming kernels.
 // ---------------------------------------------------------------------------
 
@@ -2725,6 +3049,42 @@ hipError_t launch_attention(const AttnArgs &g0, hipStream_t st, unsigned *grid_o
 unsigned attention_grid(const AttnArgs &g) {
     return wattn_eligible(g) ? (unsigned)(8 * ((g.heads + 1) / 2) * wattn_lanes(g))
                              : (unsigned)((g.nw * g.heads + 3) / 4);
+}
+
+void qkv_pair_weights(const float *w, const float *b, int heads, int hd, float *w_out,
+                      float *b_out) {
+    const int c = heads * hd;
+    for (int p = 0; p < heads / 2; ++p)
+        for (int u = 0; u < 6 * hd; ++u) {
+            // unit column u: segment u / (2hd) (q, k, v), head 2p + (u / hd) % 2, d
+            const int seg = u / (2 * hd), hp = (u / hd) & 1, d = u % hd;
+            const int src = seg * c + (2 * p + hp) * hd + d;
+            for (int k = 0; k < c; ++k) w_out[((size_t)p * 6 * hd + u) * c + k] = w[(size_t)src * c + k];
+            b_out[p * 6 * hd + u] = b[src];
+        }
+}
+
+// k_qkv_wattn's persistent grid: 8 XCDs x 3 head pairs x window lanes, two
+// workgroups per CU, never more lanes than an XCD has windows.
+static int qkv_attn_lanes(int nw) {
+    return std::max(1, std::min((nw + 7) / 8, 2 * cu_count() / (8 * 3)));
+}
+
+unsigned qkv_attention_grid(int hp, int wp) {
+    return (unsigned)(8 * 3 * qkv_attn_lanes((hp / 8) * (wp / 8)));
+}
+
+hipError_t launch_qkv_attention(const QkvAttnArgs &g0, hipStream_t st, unsigned *grid_out) {
+    if (g0.hp <= 0 || g0.wp <= 0 || g0.hp % 8 || g0.wp % 8 || g0.shift < 0 || g0.shift >= 8)
+        return hipErrorInvalidValue;
+    QkvAttnArgs g = g0;
+    g.nww = g.wp / 8;
+    g.nw = (g.hp / 8) * g.nww;
+    g.nws = qkv_attn_lanes(g.nw);
+    const unsigned grid = (unsigned)(8 * 3 * g.nws);
+    if (grid_out) *grid_out = grid;
+    hipLaunchKernelGGL(k_qkv_wattn, dim3(grid), dim3(256), 0, st, g);
+    return hipGetLastError();
 }
 
 hipError_t launch_pad_input(const float *in, float *out, int h, int w, int hp, int wp,

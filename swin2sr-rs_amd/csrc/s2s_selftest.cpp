@@ -350,6 +350,33 @@ extern "C" int s2s_selftest(const s2s_arch *arch, const s2s_tensor *tensors, siz
         }
     }
 
+    // the block's qkv projection and window attention as the forward runs
+    // them for 6 heads of 30 (one fused kernel): x -> x W^T + b -> attention
+    if (qkv_attn_fused(wheads, whd)) {
+        const int heads = wheads, hd = whd, c = heads * hd, hp = 16, wp = 24;
+        const size_t P = (size_t)hp * wp;
+        for (int shift : {0, 4}) {
+            std::vector<float> x = seq(P * c, 0.35f), w = seq((size_t)3 * c * c, 0.6f),
+                               b = seq((size_t)3 * c, 1.7f), ls(heads),
+                               cpb = seq((size_t)64 * 64 * heads, 0.15f), got(P * c);
+            for (float &v : w) v /= std::sqrt((float)c);
+            for (int i = c; i < 2 * c; ++i) b[i] = 0.f;  // k has no bias
+            for (int h = 0; h < heads; ++h) ls[h] = 1.3f - 0.2f * h;
+            std::vector<float> qkv(P * 3 * c);
+            for (size_t p = 0; p < P; ++p)
+                for (int o = 0; o < 3 * c; ++o) {
+                    double a = b[o];
+                    for (int i = 0; i < c; ++i) a += (double)w[(size_t)o * c + i] * x[p * c + i];
+                    qkv[p * 3 * c + o] = (float)a;
+                }
+            CHECK(s2s_test_block_attention(hp, wp, heads, hd, shift, x.data(), w.data(), b.data(),
+                                           ls.data(), cpb.data(), got.data()));
+            CHECK(cnt.ok(close("qkv + attention (fused) " + std::to_string(heads) + "x" +
+                                   std::to_string(hd) + " shift=" + std::to_string(shift),
+                               attention(qkv, hp, wp, heads, hd, shift, ls, cpb), got, tol)));
+        }
+    }
+
     // the qkv GEMM's shifted-window gather into the unit layout, exactly: an
     // identity weight carries each pixel's index into every q/k/v column
     {

@@ -203,12 +203,32 @@ int s2s_test_block_attention(int hp, int wp, int heads, int head_dim, int shift,
     float *dq = d.alloc<float>(nq), *dout = d.alloc<float>(P * c);
     if (!dx || !dw || !db || !dls || !dcp || !dq || !dout)
         return fail("hipMalloc failed: out of memory");
-    GemmArgs g;
-    const int epi = qkv_gemm_args(dx, dw, db, dq, hp, wp, shift, heads, head_dim, &g);
-    hipError_t e = launch_gemm(g, ALOAD_ROWS, epi, 0);
-    if (e == hipSuccess)
-        e = launch_attention(window_attn_args(dq, dcp, dls, dout, hp, wp, shift, heads, head_dim), 0,
-                             nullptr);
+    hipError_t e;
+    if (qkv_attn_fused(heads, head_dim)) {
+        // the forward's fused kernel, with the weights in its order
+        std::vector<float> wp_((size_t)3 * c * c), bp_((size_t)3 * c);
+        qkv_pair_weights(wqkv, bqkv, heads, head_dim, wp_.data(), bp_.data());
+        const float *dwp = d.up(wp_.data(), wp_.size()), *dbp = d.up(bp_.data(), bp_.size());
+        if (!dwp || !dbp) return fail("hipMalloc failed: out of memory");
+        QkvAttnArgs a{};
+        a.x = dx;
+        a.w = dwp;
+        a.bias = dbp;
+        a.cpbt = dcp;
+        a.logit_scale = dls;
+        a.out = dout;
+        a.hp = hp;
+        a.wp = wp;
+        a.shift = shift;
+        e = launch_qkv_attention(a, 0, nullptr);
+    } else {
+        GemmArgs g;
+        const int epi = qkv_gemm_args(dx, dw, db, dq, hp, wp, shift, heads, head_dim, &g);
+        e = launch_gemm(g, ALOAD_ROWS, epi, 0);
+        if (e == hipSuccess)
+            e = launch_attention(window_attn_args(dq, dcp, dls, dout, hp, wp, shift, heads, head_dim),
+                                 0, nullptr);
+    }
     if (int rc = finish(e, "qkv + window attention")) return rc;
     if (hipMemcpy(out, dout, P * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
         return fail("hipMemcpy failed");

@@ -194,6 +194,38 @@ def test_conv3x3(pkg, orc, h, w, cin, cout, epi):
     assert err < 5e-5, err
 
 
+@pytest.mark.parametrize("shift", [0, 4])
+@pytest.mark.parametrize("hp,wp", [(16, 16), (40, 72), (264, 264)])
+def test_block_attention_fused(pkg, orc, shift, hp, wp):
+    """6 heads of 30 (C = 180): the block's qkv projection and window
+    attention run as one kernel (the pair's q|k|v straight from the GEMM into
+    the attention's LDS unit). From x and the block's weights against the
+    qkv linear in float64 and the oracle's attention, at the attention test's
+    bars, up to the headline plane with its wrapped last window row and
+    column."""
+    abi = pkg.abi
+    heads, hd = 6, 30
+    c = heads * hd
+    r = rng(hp * wp + shift + 11)
+    P = hp * wp
+    x = r.standard_normal((P, c), dtype=np.float32)
+    w = (r.standard_normal((3 * c, c), dtype=np.float32) / np.sqrt(c)).astype(np.float32)
+    b = r.standard_normal(3 * c, dtype=np.float32)
+    b[c:2 * c] = 0.0  # k has no bias
+    ls = np.array([1.3 - 0.2 * i for i in range(heads)], np.float32)
+    ls[0] = np.log(300.0)  # above the log(100) clamp
+    cpb = (r.standard_normal((64 * 64, heads), dtype=np.float32) * 3.0).astype(np.float32)
+    qkv = (x.astype(np.float64) @ w.astype(np.float64).T + b).astype(np.float32)  # [P][3c]
+    p = orc.plan_explicit(hp, wp, 8, c)
+    planes = [hwc_to_nchw(np.ascontiguousarray(qkv[:, i * c:(i + 1) * c]), hp, wp) for i in range(3)]
+    qkv_tok = np.concatenate([orc.gather(p, t, shift) for t in planes], axis=0)
+    want = nchw_to_hwc(orc.scatter(p, orc.attention(p, heads, hd, ls, cpb, qkv_tok, shift), shift))
+    got = abi.test_block_attention(hp, wp, heads, hd, shift, x, w, b, ls, cpb)
+    vmax = max(1.0, float(np.abs(qkv[:, 2 * c:]).max()))
+    err = np.abs(got - want).max()
+    assert err < 2e-5 * vmax, err
+
+
 @pytest.mark.parametrize("h,w,c", [(2, 2, 180), (5, 7, 60), (6, 10, 60), (34, 40, 120),
                                    (33, 39, 180), (20, 70, 180), (72, 80, 180), (264, 264, 180),
                                    (72, 72, 60)])
