@@ -104,6 +104,11 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         work["up2_last_in"] = ("hbm", 0, f * (ho * wo * F + T5 * F))
         work["up2_last"] = ("mfma", 2 * T5 * 48 * F, f * (T5 * (F + 48) + 36 * 48 * F))
         work["up2_last_out"] = ("hbm", 0, f * (T5 * 48 + 3 * h * s * w * s))
+    if arch.upsampler == "pixelshuffle" and s >= 4 and F == 64:
+        # input row 0 and column 0 recomputed with the padding-aware variants:
+        # 48 outputs of a 5x5xF footprint per border pixel (VALU)
+        nb = -(-h * s // 4) + -(-w * s // 4) - 1
+        work["up2_last_edge"] = ("valu", 2 * nb * 48 * 25 * F, f * (nb * 25 * F + 4 * 48 * 25 * F))
     if C in (60, 120, 180) and F % 4 == 0 and F <= 64:
         # conv_before_upsample (C -> F, LeakyReLU) as Winograd F(4x4,3x3): the
         # same input transform, 36 GEMMs of T x F x C, the output transform

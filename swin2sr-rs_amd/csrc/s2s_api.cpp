@@ -779,7 +779,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
                 }))
                 return -1;
             const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
-            return run("up2_last_edge", dim3((nb + 3) / 4), dim3(256), [&] {
+            return run("up2_last_edge", dim3(nb), dim3(256), [&] {
                 return launch_up2_last_edge(src, u2_we, u2_be, d_out, H, W, feat, oh, ow,
                                             arch.img_range, arch.mean, stream);
             });
@@ -801,7 +801,7 @@ int s2s_ctx::head(int h, int w, float *d_out) {
             for (int i = 0; i < 3; ++i) g.mean[i] = arch.mean[i];
             if (gemm("up2_last", g, ALOAD_IM2COL5, EPI_SHUFFLE_FINISH)) return -1;
             const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
-            return run("up2_last_edge", dim3((nb + 3) / 4), dim3(256), [&] {
+            return run("up2_last_edge", dim3(nb), dim3(256), [&] {
                 return launch_up2_last_edge(fplanes[octaves - 2], u2_we, u2_be, d_out, H, W, feat,
                                             oh, ow, arch.img_range, arch.mean, stream);
             });

@@ -2518,14 +2518,14 @@ __global__ __launch_bounds__(256) void k_up_last_edge(const float *__restrict__ 
     }
 }
 
-// The two-octave composition's (ALOAD_IM2COL5 + EPI_SHUFFLE_FINISH) outputs
-// at input row 0 and column 0, where the middle plane's and conv_last's zero
-// padding drop terms the interior composition includes: recomputed with the
-// variant for the pixel (ey = row 0, ex = column 0), weights [4][48][25][64].
-// One wave per border pixel, lane = input channel: the lane's 25 tap values
-// stay in registers, each of the 48 outputs is 25 coalesced weight loads and
-// 25 FMAs per lane, and the 64 partial sums of an output meet through LDS
-// (lane s adds up output s) rather than through 48 chains of lane shuffles.
+// The two-octave composition's outputs at input row 0 and column 0, where the
+// middle plane's and conv_last's zero padding drop terms the interior
+// composition includes: recomputed with the variant for the pixel (ey = row
+// 0, ex = column 0), weights [4][48][25][64]. One workgroup per border pixel,
+// lane = input channel, wave w computing outputs 12w .. 12w + 11: the lane's
+// 25 tap values stay in registers, each output is 25 coalesced weight loads
+// and 25 FMAs per lane, and the 64 partial sums of an output meet through LDS
+// (thread s adds up output s) rather than through 48 chains of lane shuffles.
 #define U2E_FEAT 64
 __global__ __launch_bounds__(256) void k_up2_last_edge(const float *__restrict__ in,
                                                        const float *__restrict__ wv,
@@ -2533,35 +2533,34 @@ __global__ __launch_bounds__(256) void k_up2_last_edge(const float *__restrict__
                                                        float *__restrict__ out, int H, int W,
                                                        int oh, int ow, float inv_range,
                                                        float m0, float m1, float m2) {
-    __shared__ float part[4][48][U2E_FEAT + 1];
-    const int cw = (ow + 3) >> 2, chh = (oh + 3) >> 2;
+    __shared__ float part[48][U2E_FEAT + 1];
+    const int cw = (ow + 3) >> 2;
     const int wave = threadIdx.x >> 6;
-    const int b = blockIdx.x * 4 + wave;
+    const int b = blockIdx.x;  // the launch has exactly one workgroup per border pixel
     const int lane = threadIdx.x & 63;
-    const bool live = b < cw + chh - 1;  // (whole wave; no early return: a barrier follows)
-    const int y = !live ? 0 : (b < cw ? 0 : b - cw + 1), x = !live ? 0 : (b < cw ? b : 0);
+    const int y = b < cw ? 0 : b - cw + 1, x = b < cw ? b : 0;
     const int var = 2 * (y == 0) + (x == 0);
-    if (live) {
-        float xv[25];
+    float xv[25];
 #pragma unroll
-        for (int tap = 0; tap < 25; ++tap) {
-            const int yy = y + tap / 5 - 2, xx = x + tap % 5 - 2;
-            const bool ok = yy >= 0 && yy < H && xx >= 0 && xx < W;
-            xv[tap] = ok ? in[((size_t)yy * W + xx) * U2E_FEAT + lane] : 0.f;
-        }
-        for (int s = 0; s < 48; ++s) {
-            const float *w = wv + (size_t)(var * 48 + s) * 25 * U2E_FEAT + lane;
-            float acc = 0.f;
+    for (int tap = 0; tap < 25; ++tap) {
+        const int yy = y + tap / 5 - 2, xx = x + tap % 5 - 2;
+        const bool ok = yy >= 0 && yy < H && xx >= 0 && xx < W;
+        xv[tap] = ok ? in[((size_t)yy * W + xx) * U2E_FEAT + lane] : 0.f;
+    }
+#pragma unroll 2
+    for (int k = 0; k < 12; ++k) {
+        const int s = 12 * wave + k;
+        const float *w = wv + (size_t)(var * 48 + s) * 25 * U2E_FEAT + lane;
+        float acc = 0.f;
 #pragma unroll
-            for (int tap = 0; tap < 25; ++tap) acc = fmaf(w[tap * U2E_FEAT], xv[tap], acc);
-            part[wave][s][lane] = acc;
-        }
+        for (int tap = 0; tap < 25; ++tap) acc = fmaf(w[tap * U2E_FEAT], xv[tap], acc);
+        part[s][lane] = acc;
     }
     __syncthreads();
-    if (live && lane < 48) {
-        const int s = lane;
+    if (threadIdx.x < 48) {
+        const int s = threadIdx.x;
         float acc = 0.f;
-        for (int l = 0; l < U2E_FEAT; ++l) acc += part[wave][s][l];
+        for (int l = 0; l < U2E_FEAT; ++l) acc += part[s][l];
         const int kk = s >> 4, oy = 4 * y + ((s >> 2) & 3), ox = 4 * x + (s & 3);
         if (oy < oh && ox < ow) {
             const float mk = kk == 0 ? m0 : (kk == 1 ? m1 : m2);
@@ -3143,9 +3142,9 @@ hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float
                                int H, int W, int feat, int oh, int ow, float img_range,
                                const float *mean, hipStream_t st) {
     if (feat != U2E_FEAT || (oh + 3) / 4 > H || (ow + 3) / 4 > W) return hipErrorInvalidValue;
-    const int n = (ow + 3) / 4 + (oh + 3) / 4 - 1;  // border pixels, one wave each
-    hipLaunchKernelGGL(k_up2_last_edge, dim3((n + 3) / 4), dim3(256), 0, st, in, wedge, bedge, out,
-                       H, W, oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+    const int n = (ow + 3) / 4 + (oh + 3) / 4 - 1;  // border pixels, one workgroup each
+    hipLaunchKernelGGL(k_up2_last_edge, dim3(n), dim3(256), 0, st, in, wedge, bedge, out, H, W, oh,
+                       ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
 
