@@ -1,0 +1,78 @@
+"""The device forward's HIP-graph replay (s2s_forward_device called again with
+the same image size, pointers and buffer plan) against the same forward
+launched kernel by kernel, through the C ABI.
+
+The second identical call in a row captures the launches and the calls after
+it replay the graph, so every replay here gets a fresh input written into the
+same device buffer, with the program's own eager work (copies, other
+forwards, synchronisations) between replays, and each output must equal the
+eager context's output for that input bit for bit (the same kernels in the
+same order). The reference has no graph path: its CUDA backend launches
+kernel by kernel (src/gpu.rs:462-583); equality with the eager launches, whose
+parity with the oracle the other GPU tests establish, is the bar.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def make_backend(pkg, arch, wts, graphs):
+    old = os.environ.get("SWIN2SR_HIP_GRAPHS")
+    os.environ["SWIN2SR_HIP_GRAPHS"] = "1" if graphs else "0"
+    try:
+        return pkg.HipBackend(arch, wts)
+    finally:
+        if old is None:
+            del os.environ["SWIN2SR_HIP_GRAPHS"]
+        else:
+            os.environ["SWIN2SR_HIP_GRAPHS"] = old
+
+
+def test_graph_replays_match_eager_launches(pkg, orc):
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    wts = M.make_weights(arch, seed=5, perturb=True)
+    h, w = 24, 40
+    h2, w2 = 16, 24
+    inputs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=s))) for s in range(6)]
+    other = M.adjust(arch, M.to_unit(M.input_sinusoids(h2, w2, seed=9)))
+    eager = make_backend(pkg, arch, wts, graphs=False)
+    graph = make_backend(pkg, arch, wts, graphs=True)
+    try:
+        want = [eager.forward(h, w, x) for x in inputs]
+        want_other = eager.forward(h2, w2, other)
+        din = hip.DeviceBuffer(3 * h * w)
+        dout = hip.DeviceBuffer(3 * h * 4 * w * 4)
+        din2 = hip.DeviceBuffer.from_array(other)
+        dout2 = hip.DeviceBuffer(3 * h2 * 4 * w2 * 4)
+
+        def run(i):
+            din.upload(inputs[i])
+            graph.forward_device(h, w, din.ptr, dout.ptr)
+            hip.stream_synchronize(graph.stream())
+            got = dout.download((3, h * 4, w * 4))
+            assert np.array_equal(got, want[i]), (i, float(np.abs(got - want[i]).max()))
+
+        # eager (first sight), captured + launched, then replays
+        for i in (0, 1, 2, 3):
+            run(i)
+        # a host-path forward of the same size in between: other buffers, eager
+        assert np.array_equal(graph.forward(h, w, inputs[4]), want[4])
+        run(5)
+        run(0)
+        # another image size re-plans the buffers (the graph is dropped); back
+        # at the first size: eager, captured, replayed again
+        graph.forward_device(h2, w2, din2.ptr, dout2.ptr)
+        hip.stream_synchronize(graph.stream())
+        assert np.array_equal(dout2.download((3, h2 * 4, w2 * 4)), want_other)
+        for i in (1, 2, 3, 4):
+            run(i)
+    finally:
+        graph.close()
+        eager.close()
+    # and the eager context itself against the oracle on one of the inputs
+    ref, _ = orc.forward(arch, wts, h, w, inputs[2])
+    assert float(np.abs(want[2] - ref).max()) <= 1e-4
