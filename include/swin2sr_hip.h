@@ -135,7 +135,11 @@ int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out
  * `[3][h*scale][w*scale]` buffer. Enqueued on the context's stream and NOT
  * synchronised; `s2s_stream` / `s2s_sync` order it. No reference counterpart:
  * the crate always hands over host slices; this is the entry a caller with
- * inputs already in HBM (the throughput harness) uses. */
+ * inputs already in HBM (the throughput harness) uses. The second call in a
+ * row with the same (h, w, d_in, d_out) and buffer plan captures the pass's
+ * launches into a HIP graph, which later such calls replay (the same kernels;
+ * SWIN2SR_HIP_GRAPHS=0 at `s2s_create` turns this off; profiling launches
+ * eagerly). `s2s_forward` runs this pass on its own device copies. */
 int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
 
 /* `s2s_forward_device` without allocating anything: every intermediate
