@@ -1680,10 +1680,17 @@ __global__ __launch_bounds__(256, wattn_per_cu(HD)) void k_wattn(AttnArgs g) {
 //     per-window attention on it, its output stored through the plane's
 //     shifted-window pixels.
 // The A tile and the unit share one 48 KiB buffer, so two workgroups run per
-// CU and one's copy overlaps the other's arithmetic. Window assignment as in
-// k_wattn: workgroup b on XCD b % 8, its slot fixing the head pair and a
-// window lane, so the three head pairs of a window read its rows from the
-// same L2.
+// CU and one's copy overlaps the other's arithmetic. Workgroup b runs on XCD
+// x = b % 8 as slot s = b / 8, which fixes its head pair, (x + 2s) % 3, and its
+// window lane, s / 3. The whole rounds go as in k_wattn: lane ws takes
+// windows x + 8 ws + 8 nws k, so the three head pairs of a window read its
+// rows from the same L2. The T windows left over are dealt out item by item:
+// item i = 3 j + pair of leftover window j goes to slot i / 8 of XCD i % 8,
+// whose pair is the item's ((x + 2 s) % 3 = i % 3). The workgroups with one
+// window more are then slots 0, 1, ... of each XCD - one per CU while there
+// are at most 32 per XCD - instead of three whole lanes of one XCD, which put
+// two of them on one CU (at 264 x 264, 81 leftover windows: that CU ran 6 us
+// past the others).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
     constexpr int HD = 30, C = 180, HG = 3;
@@ -1703,9 +1710,17 @@ __global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
 
     const int xcd = blockIdx.x & 7;
     const int slot = blockIdx.x >> 3;
-    const int hg = slot % HG;
+    static_assert(HG == 3, "the pair of a slot cycles through three");
+    const int hg = (xcd + 2 * slot) % HG;
     const int ws = slot / HG;
     const int wstep = 8 * g.nws;
+    // window k of this workgroup: whole rounds, then at most one leftover
+    // window (its item's pair is hg: (xcd + 8 slot) % 3 == hg)
+    const int R0 = g.nw / wstep;
+    const int T = g.nw - R0 * wstep;
+    const int ti = xcd + 8 * slot;
+    const int wtail = ti < 3 * T ? R0 * wstep + ti / 3 : g.nw;
+    auto window_k = [&](int k) { return k < R0 ? xcd + 8 * ws + wstep * k : (k == R0 ? wtail : g.nw); };
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1788,7 +1803,8 @@ __global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
     const int colo = (hg * W2 + 4 * oc4) * 4;
     const __amdgpu_buffer_rsrc_t ro = buf_rsrc(g.out, (size_t)g.hp * g.wp * C * 4);
 
-    int wi = xcd + 8 * ws;
+    int kw = 0;
+    int wi = window_k(0);
     if (wi < g.nw) copy_a(wi);
     // as many dropped stores as a window's output has: the loop is entered
     // with the same queue (the copy, then stores) as it loops back with
@@ -1802,7 +1818,7 @@ __global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
         // previous window's stores) ----
         WAIT_VMCNT(NST);
         lds_sync();
-        const int wn = wi + wstep;
+        const int wn = window_k(kw + 1);
         const int wh = wi / g.nww;
         const int ww = wi - wh * g.nww;
 
@@ -1983,6 +1999,7 @@ __global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
             }
         }
         wi = wn;
+        ++kw;
     }
 }
 
