@@ -2971,14 +2971,17 @@ static hipError_t run_bs_e(const GemmArgs &g, int epi, hipStream_t st, bool laun
 
 // 32-row tasks (two row blocks) when several column groups or batches share
 // the machine and the epilogue keeps no per-row state; else 16-row tasks.
-// The GELU GEMM (fc1) keeps 16-row tasks: its plane rarely divides into whole
-// rounds of 32-row tasks, and the last, partial round of the finer tasks is
-// half as long (measured 2.8% faster at 264 x 264).
+// The GELU GEMM (fc1) and the Winograd batches at K = C keep 16-row tasks:
+// their planes rarely divide into whole rounds of 32-row tasks, and the last,
+// partial round of the finer tasks is half as long (measured at 264 x 264:
+// fc1 2.8%, the body convs' 36-batch GEMM 4.5% faster). The x4 head's K = 64
+// batches, bound by HBM rather than MFMA, keep 32-row tasks (16-row: 7% slower).
 static int bs_rb(const GemmArgs &g, int ks, int epi) {
     const int gw = 64 * bs_ntw(g, epi);
     const int ng = (g.N + gw - 1) / gw * std::max(g.nb, 1);  // column groups x batches
     const bool simple = epi == EPI_STORE || epi == EPI_LRELU || epi == EPI_QKV_WIN;
     (void)ks;
+    if (g.nb > 1 && g.K != 64) return 1;
     return (ng >= 2 && simple) ? 2 : 1;
 }
 
