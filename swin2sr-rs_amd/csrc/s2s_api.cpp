@@ -250,6 +250,27 @@ struct s2s_ctx {
 
 namespace {
 
+// Whether a weight of N rows of K multiplied under epilogue `epi` is stored
+// in k_bsgemm's register order (bs_pack_weights), and its floats as stored.
+// The x4 head's K = 64 Winograd products keep rows: their GEMM is bound by
+// HBM, not by its start, and measured 10% slower with packed weights.
+bool bs_packs(int N, int K, int epi) { return K != 64 && bs_weight_floats(N, K, epi) > 0; }
+size_t weight_floats(int N, int K, int epi) {
+    return bs_packs(N, K, epi) ? bs_weight_floats(N, K, epi) : (size_t)N * K;
+}
+
+// nb weights of rows [N][K], one after another, as the GEMM that multiplies
+// by them reads them: in register order when k_bsgemm takes the shape (each
+// batch weight_floats apart), else unchanged.
+std::vector<float> gemm_weights(const std::vector<float> &rows, int nb, int N, int K, int epi) {
+    if (!bs_packs(N, K, epi)) return rows;
+    const size_t pf = bs_weight_floats(N, K, epi);
+    std::vector<float> out(pf * nb);
+    for (int b = 0; b < nb; ++b)
+        bs_pack_weights(rows.data() + (size_t)b * N * K, K, N, K, epi, out.data() + b * pf);
+    return out;
+}
+
 void free_list(AllocList &l) {
     for (void *p : l.ptrs) (void)hipFree(p);
     l.ptrs.clear();
@@ -601,6 +622,7 @@ int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *
         // qkv straight into the window attention's unit layout where its
         // kernel takes the head shape, else the plane layout [P][3c]
         const int epi = qkv_gemm_args(x_in, b.wqkv, b.bqkv, qkv, hp, wp, shift, arch.heads, hd, &g);
+        g.b_packed = bs_packs(3 * c, c, EPI_STORE);
         if (gemm("qkv", g, ALOAD_ROWS, epi)) return -1;
         const AttnArgs a = window_attn_args(qkv, b.cpbt, b.ls, o, hp, wp, shift, arch.heads, hd);
         const unsigned ag = attention_grid(a);
@@ -610,6 +632,7 @@ int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *
     }
 
     g = rows_gemm(o, c, b.wproj, c, b.bproj, x_out, c, P, c, c);
+    g.b_packed = bs_packs(c, c, EPI_LN_RES);
     g.res = x_in;
     g.ldr = c;
     g.ln_w = b.n1w;
@@ -617,9 +640,11 @@ int s2s_ctx::block_fwd(const BlockW &b, int hp, int wp, int shift, const float *
     if (gemm("proj_ln_res", g, ALOAD_ROWS, EPI_LN_RES)) return -1;
 
     g = rows_gemm(x_out, c, b.w1, c, b.b1, hid, hidden, P, hidden, c);
+    g.b_packed = bs_packs(hidden, c, EPI_GELU);
     if (gemm("fc1_gelu", g, ALOAD_ROWS, EPI_GELU)) return -1;
 
     g = rows_gemm(hid, hidden, b.w2, hidden, b.b2, x_out, c, P, c, hidden);
+    g.b_packed = bs_packs(c, hidden, EPI_LN_RES);
     g.res = x_out;
     g.ldr = c;
     g.ln_w = b.n2w;
@@ -692,7 +717,8 @@ int s2s_ctx::conv_wino(const char *name, const float *in, int H, int W, int ci, 
     g.nb = WINO_POS;
     g.a_bstride = (size_t)T * ci;
     g.o_bstride = (size_t)T * co;
-    g.b_bstride = (size_t)co * ci;
+    g.b_packed = bs_packs(co, ci, EPI_STORE);
+    g.b_bstride = weight_floats(co, ci, EPI_STORE);
     if (gemm(name, g, ALOAD_ROWS, EPI_STORE)) return -1;
     return run(out_name.c_str(), dim3(wino_out_grid(H, W, co)), dim3(256), [&] {
         return launch_wino_out(mbuf, bias, res, res ? co : 0, out, co, H, W, co, lrelu, slope, stream);
@@ -844,7 +870,8 @@ int s2s_ctx::head(int h, int w, float *d_out) {
             g = rows_gemm(qkv, feat, u2_w, feat, nullptr, qkv, feat, T, 48, feat);
             g.nb = WINO_POS;
             g.a_bstride = g.o_bstride = (size_t)T * feat;
-            g.b_bstride = (size_t)48 * feat;
+            g.b_packed = bs_packs(48, feat, EPI_STORE);
+            g.b_bstride = weight_floats(48, feat, EPI_STORE);
             if (gemm("up2_last", g, ALOAD_ROWS, EPI_STORE)) return -1;
             if (run("up2_last_out", dim3(wino5_finish_grid(Ho, Wo)), dim3(256), [&] {
                     return launch_wino5_finish(qkv, feat, u2_b, d_out, Ho, Wo, oh, ow, arch.img_range,
@@ -971,13 +998,13 @@ std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vect
 }
 
 // A body C -> C conv's weights [co][ci][3][3] as its kernels read them: the
-// Winograd transform [36][C][C] for the released widths, else the implicit
-// GEMM's [co][tap][ci_pad4].
+// Winograd transform [36][C][C] for the released widths (in the batched
+// GEMM's order), else the implicit GEMM's [co][tap][ci_pad4].
 std::vector<float> body_conv_weights(const float *w, int C) {
     if (!wino_body(C)) return conv_relayout(w, C, C, nullptr);
     std::vector<float> u((size_t)WINO_POS * C * C);
     wino_weights(w, C, C, u.data());
-    return u;
+    return gemm_weights(u, WINO_POS, C, C, EPI_STORE);
 }
 
 // co = 4ch + 2dy + dx  ->  row (2dy+dx)*feat + ch, so a 32-column tile of the
@@ -1142,17 +1169,24 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
     f += C;                     // conv_first's bias (the body skip)
     f += 2 * 9 * 4 * C + C;     // k_embed's two weight sets, the folded bias
     f += 4 * C;                 // patch_embed's LayerNorm, the final LayerNorm
-    // the body's C -> C convs: Winograd weights [36][C][C] or direct [C][9][C4]
-    const uint64_t body_conv = wino_body(A.embed) ? WINO_POS * C * C : C * 9 * C4;
+    // the body's C -> C convs: Winograd weights [36][C][C] (in the batched
+    // GEMM's register order) or direct [C][9][C4]
+    const uint64_t body_conv = wino_body(A.embed) ? WINO_POS * weight_floats(C, C, EPI_STORE) : C * 9 * C4;
     f += body_conv + C;         // conv_after_body
     for (int s = 0; s < A.n_stages; ++s) {
         f += body_conv + C;     // the stage close (3x3 with the 1x1 folded in)
-        const uint64_t per_block = 3 * C * C + 3 * C  // fused qkv and its bias
-                                   + NH               // logit scale
-                                   + C * C + C        // proj
-                                   + 4 * C            // norm1, norm2
-                                   + H2 * C + H2 + C * H2 + C  // fc1, fc2
-                                   + NH * n * n;      // the CPB table
+        // the fused qkv (per head pair when the qkv + attention kernel takes
+        // the head shape), proj, fc1, fc2 in their GEMMs' layouts
+        const uint64_t wqkv = qkv_attn_fused(A.heads, A.embed / A.heads)
+                                  ? (uint64_t)(A.heads / 2) * weight_floats(C, C, EPI_STORE)
+                                  : weight_floats(3 * C, C, EPI_STORE);
+        const uint64_t per_block = wqkv + 3 * C                               // fused qkv, its bias
+                                   + NH                                       // logit scale
+                                   + weight_floats(C, C, EPI_LN_RES) + C      // proj
+                                   + 4 * C                                    // norm1, norm2
+                                   + weight_floats(H2, C, EPI_GELU) + H2      // fc1
+                                   + weight_floats(C, H2, EPI_LN_RES) + C     // fc2
+                                   + NH * n * n;                              // the CPB table
         f += per_block * (uint64_t)A.depths[s];
     }
     const int up = A.upsampler;
@@ -1161,7 +1195,7 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
         if (head_feat_of(ts, A.embed, &F)) return -1;
         const uint64_t F_ = F, F4 = round4(F);
         // conv_before_upsample: Winograd weights [36][F][C4] or direct [F][9][C4]
-        f += (wino_head(A.embed, F) ? WINO_POS * F_ * C4 : F_ * 9 * C4) + F_;
+        f += (wino_head(A.embed, F) ? WINO_POS * weight_floats(F, C4, EPI_STORE) : F_ * 9 * C4) + F_;
         f += 9 * F_ * 3 + 3;            // conv_last
         if (up == S2S_NEAREST_CONV) {
             f += 3 * (F_ * 9 * F4 + F_);  // conv_up1, conv_up2, conv_hr
@@ -1170,7 +1204,7 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
             f += (uint64_t)oct * (4 * F_ * 9 * F4 + 4 * F_);  // the octave convs
             if (up == S2S_PIXELSHUFFLE && F % 8 == 0) {
                 if (oct >= 2 && F == 64)     // two octaves and conv_last composed (the
-                    f += (wino_up2(oct, F) ? WINO_POS * 48 * F4 : 48 * 25 * F_)  // GEMM's,
+                    f += (wino_up2(oct, F) ? WINO_POS * weight_floats(48, F4, EPI_STORE) : 48 * 25 * F_)  // GEMM's,
                          + 4 * 48 * 25 * F_ + 5 * 48;                           // the edges')
                 else
                     f += 5 * 12 * 25 * F_ + 5 * 12;  // the last octave and conv_last composed
@@ -1262,7 +1296,7 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
         if (ts.get("conv_before_upsample.0.weight", {F, C, 3, 3}, &x)) return -1;
         std::vector<float> u((size_t)WINO_POS * F * round4(C));
         wino_weights(x->data, F, C, u.data());
-        return ctx->upload(u, &ctx->cbu_w);
+        return ctx->upload(gemm_weights(u, WINO_POS, F, round4(C), EPI_STORE), &ctx->cbu_w);
     };
 
     rc = rc || up("conv_first.bias", {C}, &ctx->cf_b);
@@ -1374,26 +1408,33 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             std::copy(vb->data, vb->data + C, bqkv.begin() + 2 * C);
             if (qkv_attn_fused(NH, C / NH)) {
                 // the fused qkv + attention kernel's order: each head pair's
-                // q|k|v rows as the attention unit's columns
+                // q|k|v rows as the attention unit's columns, each pair's
+                // C x C rows in register order
                 std::vector<float> wp(wqkv.size()), bp(bqkv.size());
                 qkv_pair_weights(wqkv.data(), bqkv.data(), NH, C / NH, wp.data(), bp.data());
-                wqkv.swap(wp);
+                wqkv = gemm_weights(wp, NH / 2, C, C, EPI_STORE);
                 bqkv.swap(bp);
+            } else {
+                wqkv = gemm_weights(wqkv, 1, 3 * C, C, EPI_STORE);
             }
             rc = rc || ctx->upload(wqkv, &bw.wqkv) || ctx->upload(bqkv, &bw.bqkv);
             const s2s_tensor *lsx;
             rc = rc || ts.get(p + "attn.logit_scale", {NH, 1, 1}, &lsx);
             if (rc) break;
             rc = ctx->upload(vec_of(lsx, NH), &bw.ls);
-            rc = rc || up(p + "attn.proj.weight", {C, C}, &bw.wproj);
+            auto up_gemm = [&](const std::string &name, int N, int K, int epi, float **dst) -> int {
+                if (ts.get(name, {N, K}, &x)) return -1;
+                return ctx->upload(gemm_weights(vec_of(x, ts.numel(x)), 1, N, K, epi), dst);
+            };
+            rc = rc || up_gemm(p + "attn.proj.weight", C, C, EPI_LN_RES, &bw.wproj);
             rc = rc || up(p + "attn.proj.bias", {C}, &bw.bproj);
             rc = rc || up(p + "norm1.weight", {C}, &bw.n1w);
             rc = rc || up(p + "norm1.bias", {C}, &bw.n1b);
             rc = rc || up(p + "norm2.weight", {C}, &bw.n2w);
             rc = rc || up(p + "norm2.bias", {C}, &bw.n2b);
-            rc = rc || up(p + "mlp.fc1.weight", {H2, C}, &bw.w1);
+            rc = rc || up_gemm(p + "mlp.fc1.weight", H2, C, EPI_GELU, &bw.w1);
             rc = rc || up(p + "mlp.fc1.bias", {H2}, &bw.b1);
-            rc = rc || up(p + "mlp.fc2.weight", {C, H2}, &bw.w2);
+            rc = rc || up_gemm(p + "mlp.fc2.weight", C, H2, EPI_LN_RES, &bw.w2);
             rc = rc || up(p + "mlp.fc2.bias", {C}, &bw.b2);
             if (rc) break;
             // The bias table, stored [head][query][key] and scaled by log2(e)
@@ -1503,7 +1544,8 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                             ctx->up2_wino = wino_up2(oct, F);
                             compose_up2_last(we, be, u0w->data, u0b->data, F, wg, bg, w48, b48,
                                              ctx->up2_wino ? &u5 : nullptr);
-                            rc = ctx->upload(ctx->up2_wino ? u5 : wg, &ctx->u2_w) ||
+                            rc = ctx->upload(ctx->up2_wino ? gemm_weights(u5, WINO_POS, 48, F, EPI_STORE) : wg,
+                                             &ctx->u2_w) ||
                                  ctx->upload(bg, &ctx->u2_b) || ctx->upload(w48, &ctx->u2_we) ||
                                  ctx->upload(b48, &ctx->u2_be);
                             ctx->fuse2 = true;

@@ -73,7 +73,24 @@ struct GemmArgs {
     // after that row has been read)
     int nb;
     size_t a_bstride, b_bstride, o_bstride;
+    // B in k_bsgemm's register order (bs_pack_weights, b_bstride counting that
+    // layout's floats) instead of rows [N][ldb]: only k_bsgemm reads that
+    // layout (it reads both)
+    int b_packed;
 };
+
+// k_bsgemm's weight layout, "register order": for each column group, K half,
+// column wave and 16-column MFMA tile, one block holding, for every k group of
+// 16, the 64 lanes' float4s lane after lane (1 KiB), then for the K tail of R
+// steps R dwords per lane, lane after lane; columns past the group are zeros.
+// Each weight load of the kernel then reads 1 KiB contiguous, where the rows
+// [N][K] layout has it read 64 bytes of each of 16 rows. bs_weight_floats is a
+// weight's size in that layout (0: no k_bsgemm shape; it depends on N, K and
+// the epilogue only); bs_pack_weights writes it from host rows w [N][ldb].
+size_t bs_weight_floats(int N, int K, int epi);
+void bs_pack_weights(const float *w, int ldb, int N, int K, int epi, float *dst);
+// the GEMM's shape is one k_bsgemm runs (with B packed)
+bool bs_takes(const GemmArgs &g, int aload, int epi);
 
 // The weight-stationary token GEMM (k_bsgemm): out = epi(A B^T + bias) with A
 // [M][lda] rows, B [N][ldb] rows. Set by the launcher: P (workgroups per
@@ -97,6 +114,7 @@ struct BsArgs {
     // batches (nb >= 1) and their strides in floats
     int nb;
     size_t a_bs, b_bs, o_bs;
+    int bpk;  // B in register order (bs_pack_weights), else rows [N][ldb]
 };
 
 // The attention kernels run the softmax in base 2: logits scaled by log2(e)

@@ -710,7 +710,11 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const int kbase = kq * KPW;
 
     const __amdgpu_buffer_rsrc_t ra_rs = buf_rsrc(g.A, (size_t)g.M * g.lda * 4);
-    const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
+    // B in register order (a block of TFL floats per group, K half, column
+    // wave and tile) or in rows
+    constexpr int TFL = G * 256 + R * 64;
+    const __amdgpu_buffer_rsrc_t rb_rs =
+        buf_rsrc(g.B, g.bpk ? (size_t)ngc * KS * 4 * NTW * TFL * 4 : (size_t)g.N * g.ldb * 4);
     // EPI_QKV_WIN: a unit is 64 rows of RSU floats, HG units per window
     const int RSU = WIN ? attn_unit_stride(g.hd) : 0;
     const int HGU = WIN ? ((g.heads + 1) >> 1) * 64 * RSU : 0;
@@ -750,22 +754,32 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const __amdgpu_buffer_rsrc_t rr_rs = buf_rsrc(HAS_RES ? g.res : g.out,
                                                   HAS_RES ? (size_t)g.M * g.ldr * 4 : 0);
 
-    // ---- the weight slice, once (columns outside the group read as zero) ----
+    // ---- the weight slice, once: register bw[t][4 gi + i] of lane (j, q) is
+    // column 16 NTW cg + 16 t + j of the group (the MFMA's A row l%16), k =
+    // kbase + 16 gi + 4 q + i, and the tail's bw[t][4 G + i] k = kbase + 16 G +
+    // R q + i (zeros past the group), in register order ----
     float bw[NTW][S];
+    // byte offsets of a lane's float4 of k group gi and its tail dword i:
+    // base + gi * ostep + odw, base + tail + i * tstep (rows: columns past the
+    // group out of range, reading zeros)
+    const int ostep = g.bpk ? 1024 : 64;
+    const int tstep = g.bpk ? 256 : 4;
 #pragma unroll
     for (int t = 0; t < NTW; ++t) {
-        const int cl = 16 * NTW * cg + 16 * t + j;  // (the MFMA's A row l%16: an output column)
-        const int boff = cl < gw ? ((gc0 + cl) * g.ldb + kbase) * 4 : BUF_OOB;
+        const int cl = 16 * NTW * cg + 16 * t + j;
+        const int base = g.bpk ? (((ng * KS + kq) * 4 + cg) * NTW + t) * TFL * 4 + lane * 16
+                               : (cl < gw ? ((gc0 + cl) * g.ldb + kbase + 4 * q) * 4 : BUF_OOB);
+        const int tail = g.bpk ? G * 1024 - lane * 12 : (16 * G - 4 * q + R * q) * 4;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
-            const float4 v = buf_load4(rb_rs, boff + (16 * gi + 4 * q) * 4);
+            const float4 v = buf_load4(rb_rs, base + gi * ostep);
             bw[t][4 * gi + 0] = v.x;
             bw[t][4 * gi + 1] = v.y;
             bw[t][4 * gi + 2] = v.z;
             bw[t][4 * gi + 3] = v.w;
         }
 #pragma unroll
-        for (int i = 0; i < R; ++i) bw[t][4 * G + i] = buf_load1(rb_rs, boff + (16 * G + R * q + i) * 4);
+        for (int i = 0; i < R; ++i) bw[t][4 * G + i] = buf_load1(rb_rs, base + tail + i * tstep);
     }
     if (tid < GW) {
         const bool ok = tid < gw;
@@ -1736,22 +1750,24 @@ __global__ __launch_bounds__(256, 2) void k_qkv_wattn(QkvAttnArgs g) {
 
     // ---- the pair's weights, once: wave w, column tile t, MFMA A row j is
     // unit column 48w + 16t + j; step 4gi + i takes k = 16gi + 4q + i, the
-    // tail step k = 176 + q ----
-    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(g.w + (size_t)hg * C * C, (size_t)C * C * 4);
+    // tail step k = 176 + q. Each pair's rows are stored in k_bsgemm's
+    // register order (bs_pack_weights of its 180 x 180 rows: 4 waves x 3
+    // tiles, blocks of TFL floats) ----
+    constexpr int TFL = GK * 256 + 64;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(g.w + (size_t)hg * 12 * TFL, (size_t)12 * TFL * 4);
     float bw[3][S];
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
-        const int cl = 48 * wave + 16 * t + j;
-        const int boff = cl < C ? cl * C * 4 : BUF_OOB;
+        const int boff = (wave * 3 + t) * TFL * 4;
 #pragma unroll
         for (int gi = 0; gi < GK; ++gi) {
-            const float4 v = buf_load4(rw, boff + (16 * gi + 4 * q) * 4);
+            const float4 v = buf_load4(rw, boff + (gi * 256 + lane * 4) * 4);
             bw[t][4 * gi + 0] = v.x;
             bw[t][4 * gi + 1] = v.y;
             bw[t][4 * gi + 2] = v.z;
             bw[t][4 * gi + 3] = v.w;
         }
-        bw[t][4 * GK] = buf_load1(rw, boff + (16 * GK + q) * 4);
+        bw[t][4 * GK] = buf_load1(rw, boff + (GK * 256 + lane) * 4);
     }
     if (tid < 192) prm[tid] = tid < C ? g.bias[hg * C + tid] : 0.f;
 
@@ -2836,13 +2852,71 @@ static int cu_count() {
     return n;
 }
 
+// K per wave and K halves of a weight shape k_bsgemm is built for (the embed
+// widths of the released checkpoints: 180 and 60, with K = 2*KPW split over
+// two wave sets, and the x4 head's 64-feature Winograd products), with its
+// tiles per wave
+static bool bs_weight_shape(int N, int K, int epi, int *kpw, int *ks, int *ntw) {
+    *ntw = (N <= 64 && (epi == EPI_STORE || epi == EPI_LN_RES)) ? 1 : 3;
+    if (N <= 0) return false;
+    if (K == 180 || K == 60) {
+        *kpw = K;
+        *ks = 1;
+    } else if (K == 64 && epi == EPI_STORE && *ntw == 1) {
+        *kpw = 64;
+        *ks = 1;
+    } else if (K == 360 || K == 120) {
+        *kpw = K / 2;
+        *ks = 2;
+    } else {
+        return false;
+    }
+    return true;
+}
+
 // k_bsgemm takes a row GEMM whose K per wave is one it is built for (the
 // embed widths of the released checkpoints: 180 and 60, with K = 2*KPW split
 // over two wave sets).
 // MFMA tiles of 16 columns per wave: one for a GEMM of at most 64 columns
 // whose epilogue has a narrow build (a column group of 64), else three (192).
 static int bs_ntw(const GemmArgs &g, int epi) {
-    return (g.N <= 64 && (epi == EPI_STORE || epi == EPI_LN_RES)) ? 1 : 3;
+    int kpw, ks, ntw;
+    (void)bs_weight_shape(g.N, g.K, epi, &kpw, &ks, &ntw);
+    return ntw;
+}
+
+size_t bs_weight_floats(int N, int K, int epi) {
+    int kpw, ks, ntw;
+    if (!bs_weight_shape(N, K, epi, &kpw, &ks, &ntw)) return 0;
+    const int ng = (N + 64 * ntw - 1) / (64 * ntw);
+    return (size_t)ng * ks * 4 * ntw * ((kpw / 16) * 256 + ((kpw % 16) / 4) * 64);
+}
+
+void bs_pack_weights(const float *w, int ldb, int N, int K, int epi, float *dst) {
+    int kpw, ks, ntw;
+    if (!bs_weight_shape(N, K, epi, &kpw, &ks, &ntw)) return;
+    const int ng = (N + 64 * ntw - 1) / (64 * ntw);
+    const int ngw = (N + ng - 1) / ng;  // columns per group, as the launch sets it
+    const int G = kpw / 16, R = (kpw % 16) / 4, tfl = G * 256 + R * 64;
+    size_t blk = 0;
+    for (int gp = 0; gp < ng; ++gp) {
+        const int gw = std::min(ngw, N - gp * ngw);
+        for (int kq = 0; kq < ks; ++kq)
+            for (int cg = 0; cg < 4; ++cg)
+                for (int t = 0; t < ntw; ++t, ++blk) {
+                    float *b = dst + blk * tfl;
+                    for (int lane = 0; lane < 64; ++lane) {
+                        const int j = lane & 15, q = lane >> 4;
+                        const int cl = 16 * ntw * cg + 16 * t + j;
+                        const float *row = cl < gw ? w + (size_t)(gp * ngw + cl) * ldb + kq * kpw : nullptr;
+                        for (int gi = 0; gi < G; ++gi)
+                            for (int i = 0; i < 4; ++i)
+                                b[gi * 256 + lane * 4 + i] = row ? row[16 * gi + 4 * q + i] : 0.f;
+                        for (int i = 0; i < R; ++i)
+                            b[G * 256 + i * 64 + lane] = row ? row[16 * G + R * q + i] : 0.f;
+                    }
+                }
+    }
 }
 
 static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks) {
@@ -2860,19 +2934,8 @@ static bool bs_eligible(const GemmArgs &g, int aload, int epi, int *kpw, int *ks
     // the A tile (and the residual tile) are copied as contiguous blocks
     if (g.lda != g.K) return false;
     if ((epi == EPI_RES || epi == EPI_LN_RES) && (g.ldr != g.N || g.N > 192)) return false;
-    if (g.K == 180 || g.K == 60) {
-        *kpw = g.K;
-        *ks = 1;
-    } else if (g.K == 64 && epi == EPI_STORE && bs_ntw(g, epi) == 1) {
-        // the x4 head's Winograd 5x5 products (64 features in, 48 out)
-        *kpw = 64;
-        *ks = 1;
-    } else if (g.K == 360 || g.K == 120) {
-        *kpw = g.K / 2;
-        *ks = 2;
-    } else {
-        return false;
-    }
+    int ntw;
+    if (!bs_weight_shape(g.N, g.K, epi, kpw, ks, &ntw)) return false;
     if ((epi == EPI_LN || epi == EPI_LN_RES) && g.N > 192) return false;
     if (epi == EPI_QKV_WIN) {
         // whole windows of the plane, three head-major column blocks
@@ -2936,6 +2999,7 @@ static hipError_t run_bs(const GemmArgs &g, hipStream_t st, bool launch, dim3 *g
     a.a_bs = g.a_bstride;
     a.b_bs = g.b_bstride;
     a.o_bs = g.o_bstride;
+    a.bpk = g.b_packed;
     hipLaunchKernelGGL((k_bsgemm<KPW, KS, RB, EPI, NTW>), grid, dim3(256 * KS), 0, st, a);
     return hipGetLastError();
 }
@@ -3005,6 +3069,11 @@ static hipError_t run_bs_any(const GemmArgs &g, int kpw, int ks, int epi, hipStr
                    : run_bs_e<60, 2, 2>(g, epi, st, launch, grid);
 }
 
+bool bs_takes(const GemmArgs &g, int aload, int epi) {
+    int kpw, ks;
+    return bs_eligible(g, aload, epi, &kpw, &ks);
+}
+
 void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *block) {
     int kpw, ks;
     if (bs_eligible(g, aload, epi, &kpw, &ks)) {
@@ -3021,7 +3090,9 @@ void gemm_geometry(const GemmArgs &g, int aload, int epi, dim3 *grid, dim3 *bloc
 hipError_t launch_gemm(const GemmArgs &g, int aload, int epi, hipStream_t st) {
     int kpw, ks;
     if (bs_eligible(g, aload, epi, &kpw, &ks)) return run_bs_any(g, kpw, ks, epi, st, true, nullptr);
-    if (g.nb > 1) return hipErrorInvalidValue;  // batches run on k_bsgemm only
+    // a packed B only k_bsgemm reads; batches and the unit-layout store only
+    // k_bsgemm runs
+    if (g.b_packed || g.nb > 1 || epi == EPI_QKV_WIN) return hipErrorInvalidValue;
     return launch_gemm_variant(g, aload, epi, gemm_pick(g, aload, epi), st);
 }
 

@@ -46,6 +46,20 @@ std::vector<float> pad_rows(const float *x, size_t rows, int c, int cp) {
     return o;
 }
 
+// nb weights of host rows [N][K] (each N*K apart) as the forward uploads
+// them: in k_bsgemm's register order when that kernel takes the GEMM `g`
+// (then g.b_packed and g.b_bstride are set), else unchanged.
+std::vector<float> gemm_weights(GemmArgs &g, int aload, int epi, const float *rows, int nb) {
+    const size_t raw = (size_t)g.N * g.K;
+    if (!bs_takes(g, aload, epi)) return std::vector<float>(rows, rows + raw * nb);
+    const size_t pf = bs_weight_floats(g.N, g.K, epi);
+    std::vector<float> out(pf * nb);
+    for (int b = 0; b < nb; ++b) bs_pack_weights(rows + b * raw, g.K, g.N, g.K, epi, out.data() + b * pf);
+    g.b_packed = 1;
+    if (nb > 1) g.b_bstride = pf;
+    return out;
+}
+
 std::vector<float> conv_relayout(const float *w, int co, int ci, const std::vector<int> *perm) {
     const int cp = round4(ci);
     std::vector<float> out((size_t)co * 9 * cp, 0.f);
@@ -162,13 +176,15 @@ int s2s_test_qkv_windows(int hp, int wp, int heads, int head_dim, int shift, con
     const size_t P = (size_t)hp * wp, nu = attn_unit_floats(hp, wp, heads, head_dim);
     if (unit_cap < nu) return fail("unit buffer too small: " + std::to_string(nu) + " floats needed");
     Dev d;
-    const float *dx = d.up(x, P * c), *dw = d.up(wqkv, (size_t)3 * c * c);
+    const float *dx = d.up(x, P * c);
     const float *db = d.up(bqkv, (size_t)3 * c);
     float *dq = d.alloc<float>(nu);
-    if (!dx || !dw || !db || !dq) return fail("hipMalloc failed: out of memory");
+    if (!dx || !db || !dq) return fail("hipMalloc failed: out of memory");
     if (hipMemset(dq, 0xff, nu * 4) != hipSuccess) return fail("hipMemset failed");
     GemmArgs g;
-    const int epi = qkv_gemm_args(dx, dw, db, dq, hp, wp, shift, heads, head_dim, &g);
+    const int epi = qkv_gemm_args(dx, nullptr, db, dq, hp, wp, shift, heads, head_dim, &g);
+    const std::vector<float> wg = gemm_weights(g, ALOAD_ROWS, epi, wqkv, 1);
+    if (!(g.B = d.up(wg.data(), wg.size()))) return fail("hipMalloc failed: out of memory");
     hipError_t e = launch_gemm(g, ALOAD_ROWS, epi, 0);
     if (int rc = finish(e, "k_bsgemm(qkv)")) return rc;
     if (hipMemcpy(unit, dq, nu * 4, hipMemcpyDeviceToHost) != hipSuccess) return fail("hipMemcpy failed");
@@ -197,18 +213,24 @@ int s2s_test_block_attention(int hp, int wp, int heads, int head_dim, int shift,
                           ? std::max(P * 3 * c, attn_unit_floats(hp, wp, heads, head_dim))
                           : P * 3 * c;
     Dev d;
-    const float *dx = d.up(x, P * c), *dw = d.up(wqkv, (size_t)3 * c * c);
+    const float *dx = d.up(x, P * c);
     const float *db = d.up(bqkv, (size_t)3 * c), *dls = d.up(logit_scale, heads);
     const float *dcp = d.up(cpbt.data(), cpbt.size());
     float *dq = d.alloc<float>(nq), *dout = d.alloc<float>(P * c);
-    if (!dx || !dw || !db || !dls || !dcp || !dq || !dout)
+    if (!dx || !db || !dls || !dcp || !dq || !dout)
         return fail("hipMalloc failed: out of memory");
     hipError_t e;
     if (qkv_attn_fused(heads, head_dim)) {
-        // the forward's fused kernel, with the weights in its order
+        // the forward's fused kernel, with the weights in its order: each head
+        // pair's q|k|v rows as the unit's columns, each pair's c x c rows in
+        // k_bsgemm's register order
         std::vector<float> wp_((size_t)3 * c * c), bp_((size_t)3 * c);
         qkv_pair_weights(wqkv, bqkv, heads, head_dim, wp_.data(), bp_.data());
-        const float *dwp = d.up(wp_.data(), wp_.size()), *dbp = d.up(bp_.data(), bp_.size());
+        const size_t pf = bs_weight_floats(c, c, EPI_STORE);
+        std::vector<float> wk((size_t)(heads / 2) * pf);
+        for (int pr = 0; pr < heads / 2; ++pr)
+            bs_pack_weights(wp_.data() + (size_t)pr * c * c, c, c, c, EPI_STORE, wk.data() + pr * pf);
+        const float *dwp = d.up(wk.data(), wk.size()), *dbp = d.up(bp_.data(), bp_.size());
         if (!dwp || !dbp) return fail("hipMalloc failed: out of memory");
         QkvAttnArgs a{};
         a.x = dx;
@@ -223,7 +245,9 @@ int s2s_test_block_attention(int hp, int wp, int heads, int head_dim, int shift,
         e = launch_qkv_attention(a, 0, nullptr);
     } else {
         GemmArgs g;
-        const int epi = qkv_gemm_args(dx, dw, db, dq, hp, wp, shift, heads, head_dim, &g);
+        const int epi = qkv_gemm_args(dx, nullptr, db, dq, hp, wp, shift, heads, head_dim, &g);
+        const std::vector<float> wg = gemm_weights(g, ALOAD_ROWS, epi, wqkv, 1);
+        if (!(g.B = d.up(wg.data(), wg.size()))) return fail("hipMalloc failed: out of memory");
         e = launch_gemm(g, ALOAD_ROWS, epi, 0);
         if (e == hipSuccess)
             e = launch_attention(window_attn_args(dq, dcp, dls, dout, hp, wp, shift, heads, head_dim),
@@ -272,7 +296,6 @@ int s2s_test_linear(int rows, int c_in, int c_out, const float *x, const float *
     GemmArgs g{};
     g.A = d.up(xp.data(), xp.size());
     g.lda = kp;
-    g.B = d.up(wp.data(), wp.size());
     g.ldb = kp;
     g.bias = bias ? d.up(bias, c_out) : nullptr;
     float *dout = d.alloc<float>((size_t)rows * c_out);
@@ -286,6 +309,9 @@ int s2s_test_linear(int rows, int c_in, int c_out, const float *x, const float *
     g.M = rows;
     g.N = c_out;
     g.K = kp;
+    // the weights as the forward holds them (register order for k_bsgemm)
+    const std::vector<float> wg = gemm_weights(g, ALOAD_ROWS, epi, wp.data(), 1);
+    g.B = d.up(wg.data(), wg.size());
     if (!g.A || !g.B || !dout) return fail("hipMalloc failed: out of memory");
     hipError_t e = launch_gemm(g, ALOAD_ROWS, epi, 0);
     if (int rc = finish(e, "k_gemm")) return rc;
@@ -360,8 +386,21 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
     const size_t P = (size_t)h * w, T = wino_tiles(h, w);
     std::vector<float> u((size_t)WINO_POS * c_out * c_in);
     wino_weights(wgt, c_out, c_in, u.data());
+    GemmArgs g{};
+    g.lda = c_in;
+    g.ldb = c_in;
+    g.ldo = c_out;
+    g.M = (int)T;
+    g.N = c_out;
+    g.K = c_in;
+    g.nb = WINO_POS;
+    g.a_bstride = T * c_in;
+    g.o_bstride = T * c_out;
+    g.b_bstride = (size_t)c_out * c_in;
+    // U in the batched GEMM's register order, as the forward uploads it
+    const std::vector<float> ug = gemm_weights(g, ALOAD_ROWS, EPI_STORE, u.data(), WINO_POS);
     Dev d;
-    const float *dx = d.up(x, P * c_in), *du = d.up(u.data(), u.size());
+    const float *dx = d.up(x, P * c_in), *du = d.up(ug.data(), ug.size());
     const float *db = bias ? d.up(bias, c_out) : nullptr;
     const float *dr = res ? d.up(res, P * c_out) : nullptr;
     // V [36][T][C_in], then M [36][T][C_out] - over V row for row for the
@@ -371,20 +410,9 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
     float *dm = body ? dv : d.alloc<float>(WINO_POS * T * c_out);
     if (!dx || !du || !dv || !dm || !dout || (bias && !db) || (res && !dr))
         return fail("hipMalloc failed: out of memory");
-    GemmArgs g{};
     g.A = dv;
-    g.lda = c_in;
     g.B = du;
-    g.ldb = c_in;
     g.out = dm;
-    g.ldo = c_out;
-    g.M = (int)T;
-    g.N = c_out;
-    g.K = c_in;
-    g.nb = WINO_POS;
-    g.a_bstride = T * c_in;
-    g.o_bstride = T * c_out;
-    g.b_bstride = (size_t)c_out * c_in;
     hipError_t e = launch_wino_in(dx, c_in, dv, h, w, c_in, 0);
     if (e == hipSuccess) e = launch_gemm(g, ALOAD_ROWS, EPI_STORE, 0);
     if (e == hipSuccess)
