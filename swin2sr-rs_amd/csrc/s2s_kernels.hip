@@ -754,38 +754,16 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
     const __amdgpu_buffer_rsrc_t rr_rs = buf_rsrc(HAS_RES ? g.res : g.out,
                                                   HAS_RES ? (size_t)g.M * g.ldr * 4 : 0);
 
-    // ---- the weight slice, once: register bw[t][4 gi + i] of lane (j, q) is
-    // column 16 NTW cg + 16 t + j of the group (the MFMA's A row l%16), k =
-    // kbase + 16 gi + 4 q + i, and the tail's bw[t][4 G + i] k = kbase + 16 G +
-    // R q + i (zeros past the group), in register order ----
+    // the weight slice (loaded after the first tiles are requested, below)
     float bw[NTW][S];
-    // byte offsets of a lane's float4 of k group gi and its tail dword i:
-    // base + gi * ostep + odw, base + tail + i * tstep (rows: columns past the
-    // group out of range, reading zeros)
-    const int ostep = g.bpk ? 1024 : 64;
-    const int tstep = g.bpk ? 256 : 4;
-#pragma unroll
-    for (int t = 0; t < NTW; ++t) {
-        const int cl = 16 * NTW * cg + 16 * t + j;
-        const int base = g.bpk ? (((ng * KS + kq) * 4 + cg) * NTW + t) * TFL * 4 + lane * 16
-                               : (cl < gw ? ((gc0 + cl) * g.ldb + kbase + 4 * q) * 4 : BUF_OOB);
-        const int tail = g.bpk ? G * 1024 - lane * 12 : (16 * G - 4 * q + R * q) * 4;
-#pragma unroll
-        for (int gi = 0; gi < G; ++gi) {
-            const float4 v = buf_load4(rb_rs, base + gi * ostep);
-            bw[t][4 * gi + 0] = v.x;
-            bw[t][4 * gi + 1] = v.y;
-            bw[t][4 * gi + 2] = v.z;
-            bw[t][4 * gi + 3] = v.w;
-        }
-#pragma unroll
-        for (int i = 0; i < R; ++i) bw[t][4 * G + i] = buf_load1(rb_rs, base + tail + i * tstep);
-    }
+    // bias and LayerNorm parameters of the group's columns: loaded first,
+    // stored to LDS once the tile copies and the weight loads are on their way
+    float pv[3] = {0.f, 0.f, 0.f};
     if (tid < GW) {
         const bool ok = tid < gw;
-        prm[0][tid] = (ok && g.bias) ? g.bias[gc0 + tid] : 0.f;
-        prm[1][tid] = (HAS_LN && ok) ? g.ln_w[gc0 + tid] : 0.f;
-        prm[2][tid] = (HAS_LN && ok) ? g.ln_b[gc0 + tid] : 0.f;
+        pv[0] = (ok && g.bias) ? g.bias[gc0 + tid] : 0.f;
+        pv[1] = (HAS_LN && ok) ? g.ln_w[gc0 + tid] : 0.f;
+        pv[2] = (HAS_LN && ok) ? g.ln_b[gc0 + tid] : 0.f;
     }
 
     const int ntask = (g.M + TR - 1) / TR;
@@ -1094,7 +1072,49 @@ __global__ __launch_bounds__(256 * KS, 2) void k_bsgemm(BsArgs g) {
         dma_a(task, As0);
         if (HAS_RES) dma_r(task, Rs0);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    // ---- the weight slice, once, requested after the first tiles and in the
+    // order the first task's MFMAs use it: the barrier below waits for the
+    // tiles alone, and each MFMA for its own weights (measured 0.5-1.6 us
+    // per launch). Register bw[t][4 gi + i] of lane (j, q) is column
+    // 16 NTW cg + 16 t + j of the group (the MFMA's A row l%16), k = kbase +
+    // 16 gi + 4 q + i, the tail's bw[t][4 G + i] k = kbase + 16 G + R q + i;
+    // B in register order (bs_pack_weights) or in rows (columns past the
+    // group then out of range, reading zeros) ----
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    {
+        const int ostep = g.bpk ? 1024 : 64;  // bytes between k groups
+        const int tstep = g.bpk ? 256 : 4;    // bytes between tail steps
+        int base[NTW], tail[NTW];
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) {
+            const int cl = 16 * NTW * cg + 16 * t + j;
+            base[t] = g.bpk ? (((ng * KS + kq) * 4 + cg) * NTW + t) * TFL * 4 + lane * 16
+                            : (cl < gw ? ((gc0 + cl) * g.ldb + kbase + 4 * q) * 4 : BUF_OOB);
+            tail[t] = g.bpk ? G * 1024 - lane * 12 : (16 * G - 4 * q + R * q) * 4;
+        }
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int t = 0; t < NTW; ++t) {
+                const float4 v = buf_load4(rb_rs, base[t] + gi * ostep);
+                bw[t][4 * gi + 0] = v.x;
+                bw[t][4 * gi + 1] = v.y;
+                bw[t][4 * gi + 2] = v.z;
+                bw[t][4 * gi + 3] = v.w;
+            }
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int t = 0; t < NTW; ++t) bw[t][4 * G + i] = buf_load1(rb_rs, base[t] + tail[t] + i * tstep);
+    }
+    if (tid < GW) {
+        prm[0][tid] = pv[0];
+        prm[1][tid] = pv[1];
+        prm[2][tid] = pv[2];
+    }
+    // (vmcnt counts in issue order: all but the weight loads done = the tiles)
+    static_assert(NTW * (G + R) <= 63, "the weight loads fit the vmcnt counter");
+    WAIT_VMCNT(NTW * (G + R));
     lds_sync();
     if (task < ntask) {
         // task k multiplies from As[k%2], writes its statistics to rst[k%2] and
