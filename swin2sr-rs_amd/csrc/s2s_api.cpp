@@ -176,7 +176,8 @@ struct s2s_ctx {
     // its launches are captured into a graph, which is then replayed while the
     // same call keeps coming (about 1.6 us less per kernel than stream
     // launches on MI355X); any other call launches eagerly. Off while
-    // profiling, for s2s_forward_device_noalloc, and with SWIN2SR_HIP_GRAPHS=0.
+    // profiling, for s2s_forward_device_noalloc, while a caller captures the
+    // context's stream itself, and with SWIN2SR_HIP_GRAPHS=0.
     struct GraphKey {
         int h = 0, w = 0;
         const float *in = nullptr;
@@ -735,6 +736,11 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out, bool 
                     "falls through to a different padding rule this engine does not implement.");
     if (plan_image(h, w)) return -1;
     if (!may_graph || prof || !graphs) return forward_launches(h, w, d_in, d_out);
+    // a caller capturing the context's stream into a graph of its own gets
+    // the launches recorded there
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIPCHK("hipStreamIsCapturing", hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone) return forward_launches(h, w, d_in, d_out);
     const GraphKey k{h, w, d_in, d_out, plan_gen};
     if (gexec && k == gkey) {
         HIPCHK("hipGraphLaunch", hipGraphLaunch(gexec, stream));

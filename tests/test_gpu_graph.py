@@ -76,3 +76,57 @@ def test_graph_replays_match_eager_launches(pkg, orc):
     # and the eager context itself against the oracle on one of the inputs
     ref, _ = orc.forward(arch, wts, h, w, inputs[2])
     assert float(np.abs(want[2] - ref).max()) <= 1e-4
+
+
+def test_caller_capture_records_the_launches(pkg):
+    """A caller that captures the context's stream (s2s_stream) into a graph of
+    its own gets the forward's launches in it, not the library's graph: its
+    graph, replayed on new inputs, equals the eager context bit for bit."""
+    import ctypes as C
+
+    M, hip = pkg.model, pkg.hip
+    h_ = hip.rt()
+    vp = C.c_void_p
+    for name, args in {"hipStreamBeginCapture": [vp, C.c_int], "hipStreamEndCapture": [vp, C.POINTER(vp)],
+                       "hipGraphInstantiate": [C.POINTER(vp), vp, vp, vp, C.c_size_t],
+                       "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp],
+                       "hipGraphDestroy": [vp]}.items():
+        getattr(h_, name).argtypes = args
+        getattr(h_, name).restype = C.c_int
+    arch = M.classical(4)
+    wts = M.make_weights(arch, seed=6, perturb=True)
+    h, w = 16, 24
+    inputs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=s))) for s in range(3)]
+    eager = make_backend(pkg, arch, wts, graphs=False)
+    graph = make_backend(pkg, arch, wts, graphs=True)
+    g = vp()
+    ge = vp()
+    try:
+        want = [eager.forward(h, w, x) for x in inputs]
+        din = hip.DeviceBuffer(3 * h * w)
+        dout = hip.DeviceBuffer(3 * h * 4 * w * 4)
+        st = vp(graph.stream())
+        # the same call twice first: the library has captured a graph of its own
+        din.upload(inputs[0])
+        for _ in range(2):
+            graph.forward_device(h, w, din.ptr, dout.ptr)
+        hip.stream_synchronize(graph.stream())
+        assert np.array_equal(dout.download((3, h * 4, w * 4)), want[0])
+        # now the caller captures the stream (relaxed mode) around the same call
+        assert h_.hipStreamBeginCapture(st, 2) == 0
+        graph.forward_device(h, w, din.ptr, dout.ptr)
+        assert h_.hipStreamEndCapture(st, C.byref(g)) == 0
+        assert h_.hipGraphInstantiate(C.byref(ge), g, None, None, 0) == 0
+        for i in (1, 2, 0):
+            din.upload(inputs[i])
+            assert h_.hipGraphLaunch(ge, st) == 0
+            hip.stream_synchronize(graph.stream())
+            got = dout.download((3, h * 4, w * 4))
+            assert np.array_equal(got, want[i]), (i, float(np.abs(got - want[i]).max()))
+    finally:
+        if ge.value:
+            h_.hipGraphExecDestroy(ge)
+        if g.value:
+            h_.hipGraphDestroy(g)
+        graph.close()
+        eager.close()
