@@ -130,3 +130,31 @@ def test_caller_capture_records_the_launches(pkg):
             h_.hipGraphDestroy(g)
         graph.close()
         eager.close()
+
+
+@pytest.mark.parametrize("name", ["lightweight", "realworld", "compressed"])
+def test_graph_replays_other_models(pkg, name):
+    """The released models' other shapes (lightweight: 6 heads of 10, the
+    two-kernel attention on packed K = 60 weights, pixelshuffledirect;
+    real-world: nearest+conv; compressed: the aux head) replay bit-exact too."""
+    M, hip = pkg.model, pkg.hip
+    arch = {"lightweight": M.lightweight(2), "realworld": M.realworld(), "compressed": M.compressed()}[name]
+    wts = M.make_weights(arch, seed=7, perturb=True)
+    h, w = 16, 24
+    s = arch.scale
+    inputs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=sd))) for sd in range(4)]
+    eager = make_backend(pkg, arch, wts, graphs=False)
+    graph = make_backend(pkg, arch, wts, graphs=True)
+    try:
+        want = [eager.forward(h, w, x) for x in inputs]
+        din = hip.DeviceBuffer(3 * h * w)
+        dout = hip.DeviceBuffer(3 * h * s * w * s)
+        for i in (0, 1, 2, 3, 0):  # eager, captured + launched, replays
+            din.upload(inputs[i])
+            graph.forward_device(h, w, din.ptr, dout.ptr)
+            hip.stream_synchronize(graph.stream())
+            got = dout.download((3, h * s, w * s))
+            assert np.array_equal(got, want[i]), (name, i, float(np.abs(got - want[i]).max()))
+    finally:
+        graph.close()
+        eager.close()
