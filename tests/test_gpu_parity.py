@@ -157,7 +157,7 @@ def test_linear_layernorm(pkg, orc, rows, cin, cout, with_res):
     assert err < 5e-5, err
 
 
-@pytest.mark.parametrize("hw,c", [(100, 180), (1000, 60), (77, 64)])
+@pytest.mark.parametrize("hw,c", [(100, 180), (1000, 60), (77, 64), (1, 180), (4099, 180), (9, 60)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_layernorm(pkg, orc, hw, c, with_res):
     r = rng(hw + c)
