@@ -60,3 +60,37 @@ def test_noalloc_refuses_a_plane_past_the_workspace(pkg):
         assert np.array_equal(got, want)
     finally:
         be.close()
+
+
+def test_noalloc_between_graph_replays(pkg):
+    """The allocation-free entry carves its buffers out of the workspace for
+    the call and puts the context's own plan back, so a graph the context
+    captured before the call replays unchanged after it (and the entry itself
+    launches eagerly, never into that graph)."""
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    be = pkg.HipBackend(arch, M.make_weights(arch, seed=4, perturb=True))
+    h, w = 40, 56
+    shape = (3, h * 4, w * 4)
+    xs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=s))) for s in (4, 5, 6)]
+    din = hip.DeviceBuffer(3 * h * w)
+    dout = hip.DeviceBuffer(3 * h * 4 * w * 4)
+    dna = hip.DeviceBuffer(3 * h * 4 * w * 4)
+    try:
+        want = [be.forward(h, w, x) for x in xs]  # the host path: other buffers
+        din.upload(xs[0])
+        for _ in range(3):  # eager, captured and launched, replayed
+            be.forward_device(h, w, din.ptr, dout.ptr)
+        hip.stream_synchronize(be.stream())
+        assert np.array_equal(dout.download(shape), want[0])
+        for i in (1, 2):
+            din.upload(xs[i])
+            be.forward_device_noalloc(h, w, din.ptr, dna.ptr)
+            be.forward_device(h, w, din.ptr, dout.ptr)  # a replay
+            hip.stream_synchronize(be.stream())
+            assert np.array_equal(dna.download(shape), want[i]), i
+            assert np.array_equal(dout.download(shape), want[i]), i
+    finally:
+        for b in (din, dout, dna):
+            b.free()
+        be.close()
