@@ -9,19 +9,32 @@
 // attention writes its output back through it.
 //
 // Dense contractions run on fp32 MFMA (fp32 in, fp32 accumulate):
-//   - k_bsgemm: the token GEMMs (qkv, proj, fc1, fc2), weights
-//     stationary in registers, with the elementwise work fused into the
-//     epilogue: bias, erf-GELU, residual, LeakyReLU, LayerNorm (+ residual)
-//     over the full row, and the qkv store in the attention's unit layout;
-//   - k_gemm: the 3x3 convolutions as implicit GEMMs (im2col done by the
-//     operand loader), with the same epilogues and the pixel-shuffle store of
-//     the head's octaves;
+//   - k_qkv_wattn: a Swin block's qkv projection and window attention in one
+//     kernel for 6 heads of 30 (every released 180-wide checkpoint): a
+//     workgroup per (window, head pair) multiplies the window's 64 gathered
+//     token rows by the pair's q|k|v weights held in registers, and runs the
+//     scaled-cosine attention of both heads on the products in LDS;
+//   - k_bsgemm: the other token GEMMs (proj, fc1, fc2, and qkv for other head
+//     shapes), weights stationary in registers, with the elementwise work
+//     fused into the epilogue: bias, erf-GELU, residual, LeakyReLU, LayerNorm
+//     (+ residual) over the full row, and the qkv store in the attention's
+//     unit layout; batched, the transform-domain products of the Winograd
+//     convolutions;
+//   - k_wino_in / k_wino_out: the Winograd F(4x4,3x3) input and output
+//     transforms of the body's 3x3 convolutions (bias, residual or LeakyReLU
+//     in the output pass), and, with k_wino5_finish, the F(2x2,5x5) form of the
+//     x4 head's composed last stage;
+//   - k_gemm: 3x3 convolutions as implicit GEMMs (im2col done by the operand
+//     loader) for the widths the Winograd path does not take, with the same
+//     epilogues and the pixel-shuffle store of the head's octaves;
 //   - k_wattn (k_attention for other head shapes): S^T = K Q^T and
 //     O^T = V^T P^T per (window, head) with the softmax in registers between.
-// The classical head's last octave and conv_last run composed on the VALU
-// (k_up_last, 12 outputs per input pixel); the memory-bound leftovers (input
-// padding, the standalone final LayerNorm, the other heads' 64->3 conv_last
-// with the crop/denormalisation) are plain streaming kernels.
+// The x2 head's last octave and conv_last run composed on the VALU
+// (k_up_last), and the composed heads' padded edge outputs in their own small
+// kernels; the memory-bound leftovers (input padding, conv_first with the
+// folded patch_embed and its LayerNorm, the standalone final LayerNorm, the
+// other heads' 64->3 conv_last with the crop/denormalisation) are plain
+// streaming kernels.
 //
 // MFMA 32x32x2 f32 lane layout (checked on the device): lane l supplies
 // A[l%32][l/32] and B[l/32][l%32]; accumulator register r of lane l holds
