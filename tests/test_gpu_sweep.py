@@ -8,7 +8,8 @@ every run: widths and heights from 8 to 71, which covers planes that are exact
 window multiples (the reference then pads a whole window), planes one pixel
 past one, and aspect ratios far from square. Each family runs at its released
 width (C = 180, or 60 for the lightweight model) with one stage of two blocks,
-so both the plain and the shifted-window attention run. Every case is
+so both the plain and the shifted-window attention run, and four strips
+narrower than two windows (up to 517 pixels long) follow. Every case is
 forwarded three times on one context: the plan is reused on the second call,
 the third replays the forward as a captured graph, and all three must be
 equal bit for bit.
@@ -33,6 +34,9 @@ def _cases():
         hi = 33 if scale == 8 else 72  # the x8 head's planes grow 64-fold
         h, w = (int(v) for v in rng.integers(8, hi, size=2))
         out.append((up, scale, c, h, w, 100 + i))
+    # and strips narrower than two windows
+    out += [("pixelshuffle", 4, 180, 8, 517, 200), ("pixelshuffle", 2, 180, 301, 9, 201),
+            ("pixelshuffledirect", 3, 60, 13, 401, 202), ("nearest+conv", 4, 180, 260, 11, 203)]
     return out
 
 
