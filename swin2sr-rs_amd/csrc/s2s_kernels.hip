@@ -2157,120 +2157,141 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x,
 
 // conv_first (3 -> C, 3x3) and patch_embed (its 1x1 conv folded into a second
 // set of conv_first weights, then LayerNorm) in one pass over the padded
-// input (reference src/gpu.rs:474-478): both read the same 3x3 x 3 taps, and
-// at K = 27 neither fills an MFMA tile. VALU: a 16-lane group takes EMB_PX
-// consecutive pixels, lane l the channel float4s q = l + 16i (q < C/4); both
-// weight sets [set][tap][ci][C] sit in LDS as float4s over channels, each
-// read serving the group's EMB_PX pixels. The LayerNorm statistics sum the
-// lane's values and then the 16 lanes by DPP, as k_layernorm does.
-#define EMB_PX 4
-__global__ __launch_bounds__(256) void k_embed(const float *__restrict__ in4,
-                                               const float *__restrict__ wts,
-                                               const float *__restrict__ b0,
-                                               const float *__restrict__ b1,
-                                               const float *__restrict__ lnw,
-                                               const float *__restrict__ lnb,
-                                               float *__restrict__ body, float *__restrict__ cur,
-                                               int H, int W, int C) {
-    __shared__ float4 ws[2 * 9 * 3 * 48];  // [set][tap][ci < 3][C/4 <= 48]
-    const int nq = C >> 2;
-    for (int i = threadIdx.x; i < 2 * 9 * 3 * nq; i += 256) {
-        const int r = i / nq, q = i - r * nq;   // r = (set * 9 + tap) * 3 + ci
-        const int set = r / 27, tc = r - 27 * set;
-        ws[r * 48 + q] = *reinterpret_cast<const float4 *>(wts + ((size_t)set * 36 + tc + tc / 3) * C + 4 * q);
-    }
-    __syncthreads();
-    const int l = threadIdx.x & 15;
-    const int p0 = (blockIdx.x * 16 + (threadIdx.x >> 4)) * EMB_PX;
+// input (reference src/gpu.rs:474-478): both read the same 3x3 x 3 taps. On
+// fp32 MFMA as 16x16x4 products with K = 36 (tap-major, the input's zero
+// fourth channel as the fourth k of each tap): a task is 16 consecutive
+// pixels; wave w holds channels 48w .. 48w + 47 of both weight sets in
+// registers (A operand: lane (j, q) the weight of channel 48w + 16t + j for
+// input channel q of tap s), and each lane gathers its pixel's tap-s input
+// channel q as the B operand, so lane (j, q) ends with channels
+// 48w + 16t + 4q .. + 3 of pixel j. Set 0 (conv_first, the body's long skip)
+// is stored as it is; set 1 gets its LayerNorm: the row sums over the lane's
+// values, the four lane rows (xrow_sum2) and the four waves (through LDS),
+// single-pass statistics as the reference's channel LayerNorm. Channels past
+// C have zero weights and bias, so they add nothing to the sums. A persistent
+// grid walks the tasks; each task's gathers are issued during the one before.
+// C <= 192, C % 4 == 0.
+__global__ __launch_bounds__(256, 2) void k_embed(const float *__restrict__ in4,
+                                                  const float *__restrict__ wts,
+                                                  const float *__restrict__ b0,
+                                                  const float *__restrict__ b1,
+                                                  const float *__restrict__ lnw,
+                                                  const float *__restrict__ lnb,
+                                                  float *__restrict__ body, float *__restrict__ cur,
+                                                  int H, int W, int C) {
+    __shared__ float rst[2][4][16][2];  // [task parity][wave][pixel][sum, sum of squares]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int j = lane & 15;
+    const int q = lane >> 4;
     const int P = H * W;
-    int py[EMB_PX], px[EMB_PX];
+    const int ntask = (P + 15) / 16;
+    // the wave's weights, biases and LayerNorm parameters (zeros past C: the
+    // loads past a resource's end read zero)
+    float wa[2][3][9];
+    float4 bs[2][3], gw[3], gb[3];
+    bool cok[3];
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wts, (size_t)2 * 9 * 4 * C * 4);
+    const __amdgpu_buffer_rsrc_t rb0 = buf_rsrc(b0, (size_t)C * 4), rb1 = buf_rsrc(b1, (size_t)C * 4);
+    const __amdgpu_buffer_rsrc_t rlw = buf_rsrc(lnw, (size_t)C * 4), rlb = buf_rsrc(lnb, (size_t)C * 4);
 #pragma unroll
-    for (int p = 0; p < EMB_PX; ++p) {
-        py[p] = (p0 + p) / W;
-        px[p] = p0 + p - py[p] * W;
+    for (int t = 0; t < 3; ++t) {
+        const int ch = 48 * wave + 16 * t + j;  // the A row this lane supplies
+        const int c4 = 48 * wave + 16 * t + 4 * q;  // the output channels it finishes
+        cok[t] = c4 < C;
+#pragma unroll
+        for (int set = 0; set < 2; ++set)
+#pragma unroll
+            for (int st = 0; st < 9; ++st)
+                wa[set][t][st] = buf_load1(rw, ch < C ? (((set * 9 + st) * 4 + q) * C + ch) * 4 : BUF_OOB);
+        const int o4 = cok[t] ? c4 * 4 : BUF_OOB;
+        bs[0][t] = buf_load4(rb0, o4);
+        bs[1][t] = buf_load4(rb1, o4);
+        gw[t] = buf_load4(rlw, o4);
+        gb[t] = buf_load4(rlb, o4);
     }
-    int qc[3];
-    float4 a0[EMB_PX][3], a1[EMB_PX][3];
+    const __amdgpu_buffer_rsrc_t rin = buf_rsrc(in4, (size_t)P * 16);
+    const __amdgpu_buffer_rsrc_t rbody = buf_rsrc(body, (size_t)P * C * 4);
+    const __amdgpu_buffer_rsrc_t rcur = buf_rsrc(cur, (size_t)P * C * 4);
+    // the B operand of task k: input channel q of each tap around pixel 16k + j
+    // (zero outside the plane: the conv's zero padding)
+    auto gather = [&](int task, float *xb) __attribute__((always_inline)) {
+        // (selects, not branches: every lane issues the same nine loads)
+        const int pj = 16 * task + j;
+        const int y = pj / W, x = pj - y * W;
+        const int base = (pj * 4 + q) * 4;
+        const unsigned in_p = pj < P ? ~0u : 0u;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        qc[i] = min(l + 16 * i, nq - 1);
-        const float4 c0 = *reinterpret_cast<const float4 *>(b0 + 4 * qc[i]);
-        const float4 c1 = *reinterpret_cast<const float4 *>(b1 + 4 * qc[i]);
-#pragma unroll
-        for (int p = 0; p < EMB_PX; ++p) {
-            a0[p][i] = c0;
-            a1[p][i] = c1;
+        for (int st = 0; st < 9; ++st) {
+            const int dy = st / 3 - 1, dx = st % 3 - 1;
+            const unsigned ok = in_p & ((unsigned)(y + dy) < (unsigned)H ? ~0u : 0u) &
+                                ((unsigned)(x + dx) < (unsigned)W ? ~0u : 0u);
+            xb[st] = buf_load1(rin, ok ? base + (dy * W + dx) * 16 : BUF_OOB);
         }
-    }
-#pragma unroll 1
-    for (int tap = 0; tap < 9; ++tap) {
-        const int dy = tap / 3 - 1, dx = tap - 3 * (tap / 3) - 1;
-        float4 xv[EMB_PX];
+    };
+    float xb[9];
+    int task = blockIdx.x;
+    if (task < ntask) gather(task, xb);
+    for (int k = 0; task < ntask; ++k, task += gridDim.x) {
+        float xn[9];
+        const int nxt = task + gridDim.x;
+        gather(nxt < ntask ? nxt : task, xn);
+        // (the next task's loads stay ahead of this task's MFMAs)
+        __builtin_amdgcn_sched_barrier(0);
+        f4v acc[2][3];
 #pragma unroll
-        for (int p = 0; p < EMB_PX; ++p) {
-            const int yy = py[p] + dy, xx = px[p] + dx;
-            const bool ok = p0 + p < P && yy >= 0 && yy < H && xx >= 0 && xx < W;
-            xv[p] = ok ? *reinterpret_cast<const float4 *>(in4 + ((size_t)yy * W + xx) * 4)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int set = 0; set < 2; ++set)
+#pragma unroll
+            for (int t = 0; t < 3; ++t) acc[set][t] = f4v{bs[set][t].x, bs[set][t].y, bs[set][t].z, bs[set][t].w};
+#pragma unroll
+        for (int st = 0; st < 9; ++st)
+#pragma unroll
+            for (int set = 0; set < 2; ++set)
+#pragma unroll
+                for (int t = 0; t < 3; ++t) acc[set][t] = MFMA16(wa[set][t][st], xb[st], acc[set][t]);
+        const int pj = 16 * task + j;
+        // conv_first: the long skip
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const int c4 = 48 * wave + 16 * t + 4 * q;
+            buf_store4(rbody, (pj < P && cok[t]) ? (pj * C + c4) * 4 : BUF_OOB,
+                       make_float4(acc[0][t][0], acc[0][t][1], acc[0][t][2], acc[0][t][3]));
         }
-#pragma unroll
-        for (int ci = 0; ci < 3; ++ci)
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const float4 w0 = ws[(tap * 3 + ci) * 48 + qc[i]];
-                const float4 w1 = ws[((9 + tap) * 3 + ci) * 48 + qc[i]];
-#pragma unroll
-                for (int p = 0; p < EMB_PX; ++p) {
-                    const float xc = ci == 0 ? xv[p].x : (ci == 1 ? xv[p].y : xv[p].z);
-                    a0[p][i].x = fmaf(w0.x, xc, a0[p][i].x);
-                    a0[p][i].y = fmaf(w0.y, xc, a0[p][i].y);
-                    a0[p][i].z = fmaf(w0.z, xc, a0[p][i].z);
-                    a0[p][i].w = fmaf(w0.w, xc, a0[p][i].w);
-                    a1[p][i].x = fmaf(w1.x, xc, a1[p][i].x);
-                    a1[p][i].y = fmaf(w1.y, xc, a1[p][i].y);
-                    a1[p][i].z = fmaf(w1.z, xc, a1[p][i].z);
-                    a1[p][i].w = fmaf(w1.w, xc, a1[p][i].w);
-                }
-            }
-    }
-    float4 gw[3], gb[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        gw[i] = *reinterpret_cast<const float4 *>(lnw + 4 * qc[i]);
-        gb[i] = *reinterpret_cast<const float4 *>(lnb + 4 * qc[i]);
-    }
-    const float invc = 1.0f / (float)C;
-#pragma unroll
-    for (int p = 0; p < EMB_PX; ++p) {
+        // patch_embed's LayerNorm
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            if (l + 16 * i >= nq) continue;
-            const float4 v = a1[p][i];
-            s1 += (v.x + v.y) + (v.z + v.w);
-            s2 += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s1 += acc[1][t][r];
+                s2 = fmaf(acc[1][t][r], acc[1][t][r], s2);
+            }
+        const float tot = xrow_sum2(s1, s2);
+        if (q < 2) rst[k & 1][wave][j][q] = tot;
+        lds_sync();
+        float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            a1 += rst[k & 1][w][j][0];
+            a2 += rst[k & 1][w][j][1];
         }
-        s1 = row16_sum(s1);
-        s2 = row16_sum(s2);
-        const int pix = p0 + p;
-        if (pix >= P) continue;
-        const float mean = s1 * invc;
-        float var = s2 * invc - mean * mean;
+        const float invc = 1.0f / (float)C;
+        const float mean = a1 * invc;
+        float var = a2 * invc - mean * mean;
         var = var > 0.f ? var : 0.f;
         const float rstd = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int q = l + 16 * i;
-            if (q >= nq) continue;
-            *reinterpret_cast<float4 *>(body + (size_t)pix * C + 4 * q) = a0[p][i];
-            const float4 v = a1[p][i];
+        for (int t = 0; t < 3; ++t) {
+            const int c4 = 48 * wave + 16 * t + 4 * q;
             float4 y;
-            y.x = (v.x - mean) * rstd * gw[i].x + gb[i].x;
-            y.y = (v.y - mean) * rstd * gw[i].y + gb[i].y;
-            y.z = (v.z - mean) * rstd * gw[i].z + gb[i].z;
-            y.w = (v.w - mean) * rstd * gw[i].w + gb[i].w;
-            *reinterpret_cast<float4 *>(cur + (size_t)pix * C + 4 * q) = y;
+            y.x = (acc[1][t][0] - mean) * rstd * gw[t].x + gb[t].x;
+            y.y = (acc[1][t][1] - mean) * rstd * gw[t].y + gb[t].y;
+            y.z = (acc[1][t][2] - mean) * rstd * gw[t].z + gb[t].z;
+            y.w = (acc[1][t][3] - mean) * rstd * gw[t].w + gb[t].w;
+            buf_store4(rcur, (pj < P && cok[t]) ? (pj * C + c4) * 4 : BUF_OOB, y);
         }
+#pragma unroll
+        for (int st = 0; st < 9; ++st) xb[st] = xn[st];
     }
 }
 
@@ -3296,10 +3317,21 @@ hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float
 hipError_t launch_embed(const float *in4, const float *wts, const float *b0, const float *b1,
                         const float *lnw, const float *lnb, float *body, float *cur, int H, int W,
                         int C, hipStream_t st) {
-    if (C % 4 || C > 192) return hipErrorInvalidValue;
-    const int P = H * W;
-    hipLaunchKernelGGL(k_embed, dim3((P + 16 * EMB_PX - 1) / (16 * EMB_PX)), dim3(256), 0, st, in4,
-                       wts, b0, b1, lnw, lnb, body, cur, H, W, C);
+    if (C % 4 || C > 192 || W < 1 || H < 1 || (long long)H * W * C * 4 >= BUF_MAX_BYTES)
+        return hipErrorInvalidValue;
+    static int per_cu = 0;  // resident workgroups per CU, from the occupancy query
+    if (!per_cu) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_embed, 256, 0) != hipSuccess || nb < 1) {
+            (void)hipGetLastError();
+            nb = 1;
+        }
+        per_cu = nb;
+    }
+    const int ntask = (H * W + 15) / 16;
+    const int grid = std::max(1, std::min(ntask, per_cu * cu_count()));
+    hipLaunchKernelGGL(k_embed, dim3(grid), dim3(256), 0, st, in4, wts, b0, b1, lnw, lnb, body, cur,
+                       H, W, C);
     return hipGetLastError();
 }
 
