@@ -28,13 +28,13 @@
 //     loader) for the widths the Winograd path does not take, with the same
 //     epilogues and the pixel-shuffle store of the head's octaves;
 //   - k_wattn (k_attention for other head shapes): S^T = K Q^T and
-//     O^T = V^T P^T per (window, head) with the softmax in registers between.
+//     O^T = V^T P^T per (window, head) with the softmax in registers between;
+//   - k_embed: conv_first and the folded patch_embed with its LayerNorm.
 // The x2 head's last octave and conv_last run composed on the VALU
 // (k_up_last), and the composed heads' padded edge outputs in their own small
-// kernels; the memory-bound leftovers (input padding, conv_first with the
-// folded patch_embed and its LayerNorm, the standalone final LayerNorm, the
-// other heads' 64->3 conv_last with the crop/denormalisation) are plain
-// streaming kernels.
+// kernels; the memory-bound leftovers (input padding, the standalone final
+// LayerNorm, the other heads' 64->3 conv_last with the crop/denormalisation)
+// are plain streaming kernels.
 //
 // MFMA 32x32x2 f32 lane layout (checked on the device): lane l supplies
 // A[l%32][l/32] and B[l/32][l%32]; accumulator register r of lane l holds
