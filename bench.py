@@ -80,8 +80,8 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "conv_after_body": ("mfma", 2 * VT * C * C, f * (2 * VT * C + 36 * C * C)),
         "conv_after_body_out": ("hbm", 0, f * (VT * C + 2 * P * C)),
         # conv_first and patch_embed (its 1x1 folded into conv_first) + LayerNorm
-        # in one VALU pass: two K = 27 convs
-        "embed": ("valu", 2 * 2 * P * C * 27, f * P * (4 + 2 * C)),
+        # in one pass on fp32 MFMA: two K = 27 convs
+        "embed": ("mfma", 2 * 2 * P * C * 27, f * P * (4 + 2 * C)),
         "layernorm": ("hbm", 10 * P * C, f * P * 2 * C),
         "pad_input": ("hbm", 0, f * (3 * h * w + 4 * P)),
         "conv_last_finish": ("hbm", 2 * (h * s) * (w * s) * 3 * 9 * F,
