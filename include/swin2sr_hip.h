@@ -295,6 +295,18 @@ int s2s_test_linear(int rows, int c_in, int c_out, const float *x, const float *
 int s2s_test_ln_residual(int hw, int c, const float *x, const float *ln_w, const float *ln_b,
                          const float *res, float *out);
 
+/* The forward's first kernel as it runs it (reference src/gpu.rs:474-478):
+ * conv_first (3 -> c, 3x3, zero pad) of a channel-last `[h*w][3]` image, and
+ * the same image through a second set of 3x3 weights (patch_embed's 1x1 conv
+ * folded into conv_first, as s2s_create forms it) followed by the channel
+ * LayerNorm (reference cpu::channel_layer_norm, src/cpu.rs:1019-1073).
+ * Weights `[c][3][3][3]`, biases and LayerNorm parameters `[c]`; outputs
+ * `body` (conv_first) and `cur` (the LayerNorm's), both `[h*w][c]`.
+ * c % 4 == 0, c <= 192. */
+int s2s_test_embed(int h, int w, int c, const float *x, const float *w_first, const float *b_first,
+                   const float *w_fold, const float *b_fold, const float *ln_w, const float *ln_b,
+                   float *body, float *cur);
+
 /* 3x3 stride-1 zero-pad-1 convolution (reference cpu::conv3x3, src/cpu.rs:
  * 400-414) on a channel-last `[h*w][c_in]` plane, weights `[c_out][c_in][3][3]`,
  * output `[h*w][c_out]`. epilogue: 0 store, 2 += res, 5 LeakyReLU(slope). */

@@ -81,6 +81,7 @@ EXPORTS = {
     "s2s_test_linear": (C.c_int, [C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_int, FP, FP, FP,
                                   C.c_float, FP]),
     "s2s_test_ln_residual": (C.c_int, [C.c_int, C.c_int, FP, FP, FP, FP, FP]),
+    "s2s_test_embed": (C.c_int, [C.c_int, C.c_int, C.c_int, FP, FP, FP, FP, FP, FP, FP, FP, FP]),
     "s2s_test_conv3x3": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_int, FP,
                                    C.c_float, FP]),
     "s2s_test_conv3x3_winograd": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP,
@@ -378,6 +379,21 @@ def test_ln_residual(x, ln_w, ln_b, res=None):
     check(lib.s2s_test_ln_residual(hw, c, fptr(c32(x)), fptr(c32(ln_w)), fptr(c32(ln_b)),
                                    fptr(c32(res)), fptr(out)), "s2s_test_ln_residual")
     return out
+
+
+def test_embed(x_hwc, h, w, w_first, b_first, w_fold, b_fold, ln_w, ln_b):
+    """conv_first and the folded patch_embed + LayerNorm through the forward's
+    kernel: `x_hwc` [h*w][3], weights [c][3][3][3]; returns (body, cur), each
+    [h*w][c]."""
+    lib = load_library()
+    c = w_first.shape[0]
+    body = np.empty((h * w, c), np.float32)
+    cur = np.empty((h * w, c), np.float32)
+    c32 = lambda a: np.ascontiguousarray(a, np.float32)
+    check(lib.s2s_test_embed(h, w, c, fptr(c32(x_hwc)), fptr(c32(w_first)), fptr(c32(b_first)),
+                             fptr(c32(w_fold)), fptr(c32(b_fold)), fptr(c32(ln_w)), fptr(c32(ln_b)),
+                             fptr(body), fptr(cur)), "s2s_test_embed")
+    return body, cur
 
 
 def test_conv3x3(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):

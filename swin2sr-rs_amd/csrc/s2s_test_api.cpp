@@ -335,6 +335,36 @@ int s2s_test_ln_residual(int hw, int c, const float *x, const float *ln_w, const
     return 0;
 }
 
+int s2s_test_embed(int h, int w, int c, const float *x, const float *w_first, const float *b_first,
+                   const float *w_fold, const float *b_fold, const float *ln_w, const float *ln_b,
+                   float *body, float *cur) {
+    if (c % 4 || c > 192 || c <= 0) return fail("the embed kernel needs c % 4 == 0 and c <= 192");
+    if (h < 1 || w < 1) return fail("empty plane");
+    const size_t P = (size_t)h * w;
+    // the kernel's operands as s2s_create lays them out: the input with a
+    // zero fourth channel, the weights [set][tap][ci < 4][c]
+    std::vector<float> in4(P * 4, 0.f), wt((size_t)2 * 9 * 4 * c, 0.f);
+    for (size_t i = 0; i < P; ++i)
+        for (int ci = 0; ci < 3; ++ci) in4[i * 4 + ci] = x[i * 3 + ci];
+    for (int o = 0; o < c; ++o)
+        for (int ci = 0; ci < 3; ++ci)
+            for (int t = 0; t < 9; ++t) {
+                wt[((size_t)t * 4 + ci) * c + o] = w_first[(size_t)o * 27 + ci * 9 + t];
+                wt[((size_t)(9 + t) * 4 + ci) * c + o] = w_fold[(size_t)o * 27 + ci * 9 + t];
+            }
+    Dev d;
+    const float *di = d.up(in4.data(), in4.size()), *dw = d.up(wt.data(), wt.size());
+    const float *b0 = d.up(b_first, c), *b1 = d.up(b_fold, c), *lw = d.up(ln_w, c), *lb = d.up(ln_b, c);
+    float *db = d.alloc<float>(P * c), *dc = d.alloc<float>(P * c);
+    if (!di || !dw || !b0 || !b1 || !lw || !lb || !db || !dc) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_embed(di, dw, b0, b1, lw, lb, db, dc, h, w, c, 0);
+    if (int rc = finish(e, "k_embed")) return rc;
+    if (hipMemcpy(body, db, P * c * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(cur, dc, P * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
 int s2s_test_conv3x3(int h, int w, int c_in, int c_out, const float *x, const float *wgt,
                      const float *bias, int epilogue, const float *res, float slope, float *out) {
     int epi;

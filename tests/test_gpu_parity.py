@@ -172,6 +172,29 @@ def test_layernorm(pkg, orc, hw, c, with_res):
     assert np.abs(got - want).max() < 3e-5
 
 
+@pytest.mark.parametrize("h,w,c", [(16, 16, 180), (24, 40, 180), (19, 23, 60), (5, 33, 24),
+                                   (1, 17, 192), (72, 80, 180)])
+def test_embed(pkg, orc, h, w, c):
+    """The forward's first kernel (conv_first, and the folded patch_embed +
+    LayerNorm, on fp32 MFMA) against the oracle's direct conv3x3 and channel
+    LayerNorm: planes ending in a partial 16-pixel task, one pixel high, the
+    released widths, and widths whose channels leave waves with no columns."""
+    r = rng(h * w + c)
+    x = (0.5 * r.standard_normal((3, h, w))).astype(np.float32)
+    w1 = (r.standard_normal((c, 3, 3, 3)) / np.sqrt(27)).astype(np.float32)
+    b1 = (0.1 * r.standard_normal(c)).astype(np.float32)
+    w2 = (r.standard_normal((c, 3, 3, 3)) / np.sqrt(27)).astype(np.float32)
+    b2 = (0.1 * r.standard_normal(c)).astype(np.float32)
+    g = (1 + 0.2 * r.standard_normal(c)).astype(np.float32)
+    be = (0.1 * r.standard_normal(c)).astype(np.float32)
+    x_hwc = np.ascontiguousarray(x.reshape(3, h * w).T)
+    body, cur = pkg.abi.test_embed(x_hwc, h, w, w1, b1, w2, b2, g, be)
+    want_body = orc.conv3x3(x, w1, b1).reshape(c, h * w)
+    want_cur = orc.channel_layer_norm(np.ascontiguousarray(orc.conv3x3(x, w2, b2).reshape(c, h * w)), g, be)
+    assert np.abs(body - want_body.T).max() < 2e-6
+    assert np.abs(cur - want_cur.T).max() < 2e-5
+
+
 @pytest.mark.parametrize("h,w,cin,cout", [(5, 7, 3, 4), (7, 9, 4, 12), (33, 39, 16, 20),
                                           (20, 70, 180, 180), (9, 11, 180, 64), (16, 16, 64, 3)])
 @pytest.mark.parametrize("epi", [0, 2, 5])
