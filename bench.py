@@ -1,6 +1,6 @@
 """Throughput of the MI355X swin2sr backend on the north-star workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload W]
 
 Workload (BASELINE.json metric): Swin2SR classical x4, fp32, a 256x256 RGB
 input upscaled to 1024x1024, whole image, one GPU. Weights are random-init by
@@ -16,9 +16,17 @@ One JSON line on stdout. `roofline` is for the kernel with the largest share
 of device time per step, its launches timed with HIP events on the library's
 own stream over K more forwards launched kernel by kernel; `cpu_baseline` is
 this repository's C restatement of the crate's CPU path (oracle/, OpenMP over
-the host cores) on a bounded sample.
+the host cores) on a bounded sample. The replayed output is checked bit for
+bit against an eager forward of the same input; a mismatch fails the run.
+
+Other workloads (--workload), each one JSON line of the same shape: rstb
+(config 1, one RSTB on an unpadded 256x256x180 plane), lightweight-x2,
+classical-x2 and realworld-x4 (configs 0, 2, 3, whole image, HBM-resident),
+compressed-x4-tiled (config 4: 1024x1024 in 256-pixel tiles with 64 of
+context through the crate's tile loop over the host-buffer entry).
 """
 import argparse
+import hashlib
 import json
 import os
 import re
@@ -123,6 +131,23 @@ def kernel_work(arch, h, w, hp=None, wp=None):
     for o in range(arch.octaves):
         work[f"conv3x3_shuffle2_o{o}"] = ("mfma", 2 * px * 4 * F * 9 * F, f * px * 5 * F)
         px *= 4
+    # pixelshuffledirect: one 3x3 conv C -> 3 s^2 stored through pixel_shuffle(s)
+    # into the denormalised, cropped image
+    work["conv_shuffle_finish"] = ("mfma", 2 * P * 3 * s * s * 9 * C, f * (P * C + 3 * h * s * w * s))
+    # nearest+conv: two nearest-2x steps, each read by the next 3x3 conv's
+    # loader (F -> F at 4P and 16P), then conv_hr at 16P
+    work["conv_up1"] = ("mfma", 2 * 4 * P * F * 9 * F, f * (P * F + 4 * P * F))
+    work["conv_up2"] = ("mfma", 2 * 16 * P * F * 9 * F, f * (4 * P * F + 16 * P * F))
+    work["conv_hr"] = ("mfma", 2 * 16 * P * F * 9 * F, f * 2 * 16 * P * F)
+    # pixelshuffle_aux: bicubic of the padded input to s x the plane (4
+    # channels), conv_bicubic 3 -> F there, conv_aux F -> 3, conv_after_aux
+    # 3 -> F, and the aux image's denormalisation
+    Q = (hp * s) * (wp * s)
+    work["bicubic"] = ("hbm", 0, f * (4 * P + 4 * Q))
+    work["conv_bicubic"] = ("mfma", 2 * Q * F * 27, f * (4 * Q + Q * F))
+    work["conv_aux"] = ("mfma", 2 * P * 3 * 9 * F, f * (P * F + 4 * P))
+    work["conv_after_aux"] = ("mfma", 2 * P * F * 27, f * (4 * P + P * F))
+    work["aux_finish"] = ("hbm", 0, f * (4 * P + 3 * P))
     return work
 
 
@@ -278,47 +303,56 @@ def bench_rstb(args, pkg):
         "roofline": roofline, "kernels": table}), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--size", type=int, default=256)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=256)
-    ap.add_argument("--cpu-passes", type=int, default=3)
-    ap.add_argument("--workload", choices=["classical-x4", "rstb"], default="classical-x4",
-                    help="classical-x4: the BASELINE metric (default); rstb: config 1's "
-                         "single-RSTB micro-bench")
-    ap.add_argument("--copy-probe-mb", type=int, default=0,
-                    help="before the warm-up, one device-to-device copy of this many MiB: the "
-                         "plain copy kernel of known size that scales rocprofv3's FETCH_SIZE / "
-                         "WRITE_SIZE counters to bytes")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this backend runs a whole image on one device and has "
-              "no multi-GPU path (see DESIGN.md for how it would shard); run with --gpus 1.",
-              file=sys.stderr)
-        sys.exit(2)
+def image_workload(M, name, size):
+    """(arch, weights, h, w, mean-adjusted input, label, data) of a whole-image
+    workload: the headline or BASELINE.json's configs 0, 2 and 3, at their
+    sizes, seeds and input generators."""
+    if name == "classical-x4":
+        arch, seed, h, w = M.classical(4), 3, size, size
+        img = M.input_sinusoids(h, w, seed=3)
+        data = "synthetic (random-init weights seed 3, config-2 sinusoid input seed 3)"
+    elif name == "lightweight-x2":  # config 0
+        arch, seed, h, w = M.lightweight(2), 0, 64, 64
+        img = M.input_uniform(h, w, seed=1)
+        data = "synthetic (random-init weights seed 0, uniform u8 input seed 1)"
+    elif name == "classical-x2":  # config 2
+        arch, seed, h, w = M.classical(2), 3, 256, 256
+        img = M.input_sinusoids(h, w, seed=3)
+        data = "synthetic (random-init weights seed 3, sinusoid input seed 3)"
+    elif name == "realworld-x4":  # config 3
+        arch, seed, h, w = M.realworld(), 4, 480, 640
+        img = M.input_texture_dct(h, w, seed=4)
+        data = "synthetic (random-init weights seed 4, DCT-quantised texture input seed 4)"
+    else:
+        raise ValueError(name)
+    s = arch.scale
+    label = f"{name} {h}x{w}->{h * s}x{w * s}"
+    return arch, M.make_weights(arch, seed=seed), h, w, M.adjust(arch, M.to_unit(img)), label, data
 
-    pkg = ge.load_package()
-    if args.workload == "rstb":
-        bench_rstb(args, pkg)
-        return
+
+TIMING_NOTE = ("kernels: one HIP event pair around each launch on the library's stream, over "
+               "forwards launched kernel by kernel; the pair adds about 2 us to each figure, "
+               "which is 10-15% of the shortest kernels (profiles/ holds rocprofv3 durations)")
+
+
+def bench_image(args, pkg, name):
+    """A whole-image workload from HBM-resident input to HBM-resident output:
+    warm-up, a per-kernel pass (events around every launch), the timed graph
+    replays, the replayed output checked bit for bit against an eager forward,
+    the dominant kernel's launches timed with events; for the headline also
+    the host-buffer path and the CPU baseline. One JSON line."""
     M, hip = pkg.model, pkg.hip
-    arch = M.classical(4)
-    h = w = args.size
+    headline = name == "classical-x4"
     t0 = time.perf_counter()
-    weights = M.make_weights(arch, seed=3)
-    img = M.to_unit(M.input_sinusoids(h, w, seed=3))
-    x = M.adjust(arch, img)
-    log(f"bench: weights + input generated in {time.perf_counter() - t0:.1f} s")
+    arch, weights, h, w, x, label, data = image_workload(M, name, args.size)
+    log(f"bench: {label}: weights + input generated in {time.perf_counter() - t0:.1f} s")
 
     be = pkg.HipBackend(arch, weights)
-    name, gfx = pkg.device_info()
-    log(f"bench: device {name} {gfx}; uploaded {be.uploaded_bytes() / 2**20:.1f} MiB")
+    dev_name, gfx = pkg.device_info()
+    log(f"bench: device {dev_name} {gfx}; uploaded {be.uploaded_bytes() / 2**20:.1f} MiB")
     din = hip.DeviceBuffer.from_array(x)
     s = arch.scale
+    shape = (3, h * s, w * s)
     dout = hip.DeviceBuffer(3 * h * s * w * s)
     stream = be.stream()
 
@@ -337,7 +371,7 @@ def main():
     log(f"bench: {args.warmup} warm-up steps done")
 
     # per-kernel pass: K forwards with an event pair around every launch on the
-    # library stream (the events cost ~3 us per launch, so this pass is not the
+    # library stream (the events cost ~2 us per launch, so this pass is not the
     # one `value` is read from); it names the dominant kernel
     work = kernel_work(arch, h, w)
     be.profile(True)
@@ -354,9 +388,8 @@ def main():
 
     # timed region: K whole-image forwards as the library runs a repeated
     # call: its launches replayed from the HIP graph it captures the second
-    # time the same call comes (the warm-up and the untimed call below make
-    # sure it has; no events: an event pair cannot bracket one kernel of a
-    # graph)
+    # time the same call comes (the two untimed calls below make sure it has;
+    # no events: an event pair cannot bracket one kernel of a graph)
     be.profile(False)
     be.forward_device(h, w, din.ptr, dout.ptr)
     be.forward_device(h, w, din.ptr, dout.ptr)
@@ -367,11 +400,26 @@ def main():
     hip.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
-    out = dout.download((3, h * s, w * s))
-    assert np.isfinite(out).all(), "non-finite output"
+    out = dout.download(shape)
     value = (h * s) * (w * s) / 1e6 / (ms_per_step / 1e3)
     log(f"bench: {args.steps} timed steps (graph replays), {ms_per_step:.3f} ms/step, "
         f"{value:.3f} output Mpix/s")
+
+    # the timed output, checked: the same input forwarded kernel by kernel into
+    # another buffer (a different call, so no graph) must give the replays'
+    # output bit for bit; a mismatch fails the run (no JSON line)
+    deager = hip.DeviceBuffer(3 * h * s * w * s)
+    be.forward_device(h, w, din.ptr, deager.ptr)
+    hip.stream_synchronize(stream)
+    eager = deager.download(shape)
+    deager.free()
+    digest = hashlib.sha256(out.tobytes()).hexdigest()[:16]
+    if not (np.isfinite(out).all() and np.array_equal(out, eager)):
+        log(f"bench: FAILED: the replayed output differs from the eager forward's "
+            f"(max |diff| {float(np.nanmax(np.abs(out - eager))):.3e})")
+        be.close()
+        sys.exit(1)
+    log(f"bench: replayed output equals the eager forward's bit for bit (sha256 {digest})")
 
     # the dominant kernel's launch duration, for its roofline: the same K
     # forwards launched kernel by kernel on the library's stream, an event
@@ -385,49 +433,54 @@ def main():
     for _ in range(args.steps):
         be.forward_device(h, w, din.ptr, dout.ptr)
     hip.synchronize()
-    roofline = roofline_of(work, dom, *profile_rows(be, {dom: work[dom]})[dom])
+    roofline = roofline_of(work, dom, *profile_rows(be, {dom: work[dom]})[dom], traffic=headline)
     roofline["device_ms_per_step"] = roofline_all["device_ms_per_step"]
     log(f"bench: {dom}: {roofline['avg_ms']:.4f} ms avg, "
         f"{roofline['achieved']} {roofline['unit']} ({100 * roofline['frac']:.1f}% of peak)")
     be.profile_only(None)
     be.profile(False)
 
-    # the crate's own boundary hands over host slices: s2s_forward uploads the
-    # input, runs, downloads the output (PCIe included); reported, never `value`.
-    # The crate's backend returns a new Vec per forward, so the first figure
-    # takes a fresh output array per call (its first-touch cost included); the
-    # second reuses one.
-    xh = np.ascontiguousarray(x)
-    be.forward(h, w, xh)
-    host_ms = {}
-    for mode in ("fresh", "reused"):
-        keep = np.empty((3, h * s, w * s), np.float32) if mode == "reused" else None
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            be.forward(h, w, xh, out=keep)
-        host_ms[mode] = (time.perf_counter() - t0) * 1e3 / args.steps
-    log(f"bench: host-buffer path (s2s_forward, PCIe included): {host_ms['fresh']:.3f} ms "
-        f"({(h * s) * (w * s) / 1e3 / host_ms['fresh']:.3f} output Mpix/s, "
-        f"{100 * (host_ms['fresh'] / ms_per_step - 1):.1f}% over the device-resident step) with a "
-        f"fresh output per call; {host_ms['reused']:.3f} ms into a reused one")
-
+    win = arch.window
     result = {
-        "metric": METRIC, "value": round(value, 4), "unit": "Mpix/s", "n_gpus": 1,
+        "metric": METRIC if headline else f"output Mpix/s {label} fp32 @1 GPU",
+        "value": round(value, 4), "unit": "Mpix/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (random-init weights seed 3, config-2 sinusoid input seed 3)",
-        "config": {"workload": f"classical-x4 {h}x{w}->{h * s}x{w * s} whole-image forward",
+        "data": data,
+        "config": {"workload": f"{label} whole-image forward",
                    "embed": arch.embed, "depths": arch.depths, "heads": arch.heads,
-                   "window": arch.window, "padded_plane": [(h // 8 + 1) * 8, (w // 8 + 1) * 8],
+                   "upsampler": arch.upsampler, "window": win,
+                   "padded_plane": [(h // win + 1) * win, (w // win + 1) * win],
                    "parallelism": "1 GPU"},
         "roofline": roofline,
         "kernels": table,
-        "host_path_mpix_s": round((h * s) * (w * s) / 1e3 / host_ms["fresh"], 3),
-        "host_path_ms": round(host_ms["fresh"], 4),
-        "host_path_reused_out_ms": round(host_ms["reused"], 4),
+        "kernel_timing": TIMING_NOTE,
+        "output_check": {"replay_equals_eager": True, "sha256_16": digest},
     }
+    if headline:
+        # the crate's own boundary hands over host slices: s2s_forward uploads
+        # the input, runs, downloads the output (PCIe included); reported, never
+        # `value`. The crate's backend returns a new Vec per forward, so the
+        # first figure takes a fresh output array per call (its first-touch
+        # cost included); the second reuses one.
+        xh = np.ascontiguousarray(x)
+        be.forward(h, w, xh)
+        host_ms = {}
+        for mode in ("fresh", "reused"):
+            keep = np.empty(shape, np.float32) if mode == "reused" else None
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                be.forward(h, w, xh, out=keep)
+            host_ms[mode] = (time.perf_counter() - t0) * 1e3 / args.steps
+        log(f"bench: host-buffer path (s2s_forward, PCIe included): {host_ms['fresh']:.3f} ms "
+            f"({(h * s) * (w * s) / 1e3 / host_ms['fresh']:.3f} output Mpix/s, "
+            f"{100 * (host_ms['fresh'] / ms_per_step - 1):.1f}% over the device-resident step) with a "
+            f"fresh output per call; {host_ms['reused']:.3f} ms into a reused one")
+        result["host_path_mpix_s"] = round((h * s) * (w * s) / 1e3 / host_ms["fresh"], 3)
+        result["host_path_ms"] = round(host_ms["fresh"], 4)
+        result["host_path_reused_out_ms"] = round(host_ms["reused"], 4)
     be.close()
-    if not args.no_cpu:
+    if headline and not args.no_cpu:
         orc = ge._load_oracle()
         log(f"bench: cpu baseline on {orc.lib().orc_threads()} threads ...")
         result["cpu_baseline"] = cpu_baseline(M, orc, arch, weights, args.cpu_sample,
@@ -436,6 +489,120 @@ def main():
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
+
+
+class _TimedBackend:
+    """`Backend` over the HIP context for the tile loop, adding each call's
+    wall time."""
+
+    def __init__(self, be):
+        self.be, self.ms = be, 0.0
+
+    def forward(self, h, w, x):
+        t0 = time.perf_counter()
+        out = self.be.forward(h, w, x)
+        self.ms += (time.perf_counter() - t0) * 1e3
+        return out
+
+
+def bench_tiled(args, pkg):
+    """Config 4: compressed x4 (pixelshuffle_aux), 1024x1024 -> 4096x4096 in
+    256-pixel tiles with 64 of context, through the crate's tile loop
+    (run_tiled) over the host-buffer entry s2s_forward, one tile after another
+    on one GPU, as the crate's --tile path runs it (PCIe included per tile).
+    `value` is output Mpix/s of whole tiled images. One JSON line, with the
+    per-kernel table of one profiled tiled run (work averaged over the tiles'
+    planes)."""
+    M, T = pkg.model, pkg.tiling
+    arch = M.compressed()
+    size, tile, pad = 1024, 256, 64
+    t0 = time.perf_counter()
+    weights = M.make_weights(arch, seed=5)
+    img = M.to_unit(M.input_texture_dct(size, size, seed=5))
+    log(f"bench: weights + input generated in {time.perf_counter() - t0:.1f} s")
+    be = pkg.HipBackend(arch, weights)
+    rec = []
+
+    class Rec:
+        def forward(self, h, w, x):
+            rec.append((h, w))
+            return be.forward(h, w, x)
+
+    for _ in range(max(args.warmup, 1)):
+        T.run_tiled(arch, Rec(), img, tile, pad)
+    tiles = rec[:len(rec) // max(args.warmup, 1)]
+    log(f"bench: {args.warmup} warm-up tiled runs done ({len(tiles)} tiles)")
+    # per-kernel pass: one tiled run with events around every launch; each
+    # kernel's work per launch is the average over the tiles' planes
+    work = {}
+    for h, w in tiles:
+        for k, (bound, fl, by) in kernel_work(arch, h, w).items():
+            b0, f0, y0 = work.get(k, (bound, 0, 0))
+            work[k] = (bound, f0 + fl / len(tiles), y0 + by / len(tiles))
+    be.profile(True)
+    be.profile_reset()
+    T.run_tiled(arch, be, img, tile, pad)
+    table, roofline = kernel_table(be, work, 1)
+    be.profile(False)
+    tb = _TimedBackend(be)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = T.run_tiled(arch, tb, img, tile, pad)
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    be.close()
+    assert out.shape == (3, size * 4, size * 4) and np.isfinite(out).all()
+    value = (size * 4) ** 2 / 1e6 / (ms / 1e3)
+    log(f"bench: {args.steps} tiled runs, {ms:.2f} ms per image ({tb.ms / args.steps:.2f} ms in "
+        f"s2s_forward), {value:.3f} output Mpix/s")
+    print(json.dumps({
+        "metric": "output Mpix/s compressed-x4 1024x1024->4096x4096 tiled (256 + 64 context) fp32 @1 GPU",
+        "value": round(value, 4), "unit": "Mpix/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init weights seed 5, DCT-quantised texture input seed 5)",
+        "config": {"workload": "config 4: compressed x4 1024x1024 in 16 tiles of 256 + 64 context "
+                               "through run_tiled over s2s_forward (host buffers, PCIe included)",
+                   "tiles": [list(t) for t in tiles], "parallelism": "1 GPU"},
+        "ms_in_forward_per_step": round(tb.ms / args.steps, 3),
+        "roofline": roofline, "kernels": table, "kernel_timing": TIMING_NOTE,
+        "cpu_baseline": None}), flush=True)
+
+
+WORKLOADS = ["classical-x4", "rstb", "lightweight-x2", "classical-x2", "realworld-x4",
+             "compressed-x4-tiled"]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--size", type=int, default=256, help="classical-x4 input side")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=256)
+    ap.add_argument("--cpu-passes", type=int, default=3)
+    ap.add_argument("--workload", choices=WORKLOADS, default="classical-x4",
+                    help="classical-x4: the BASELINE metric (default); rstb: config 1's "
+                         "single-RSTB micro-bench; lightweight-x2, classical-x2, realworld-x4: "
+                         "configs 0, 2, 3 whole-image; compressed-x4-tiled: config 4")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="before the warm-up, one device-to-device copy of this many MiB: the "
+                         "plain copy kernel of known size that scales rocprofv3's FETCH_SIZE / "
+                         "WRITE_SIZE counters to bytes")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this backend runs a whole image on one device and has "
+              "no multi-GPU path (see DESIGN.md for how it would shard); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    pkg = ge.load_package()
+    if args.workload == "rstb":
+        bench_rstb(args, pkg)
+    elif args.workload == "compressed-x4-tiled":
+        bench_tiled(args, pkg)
+    else:
+        bench_image(args, pkg, args.workload)
 
 
 if __name__ == "__main__":

@@ -139,7 +139,12 @@ int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out
  * row with the same (h, w, d_in, d_out) and buffer plan captures the pass's
  * launches into a HIP graph, which later such calls replay (the same kernels;
  * SWIN2SR_HIP_GRAPHS=0 at `s2s_create` turns this off; profiling launches
- * eagerly). `s2s_forward` runs this pass on its own device copies. */
+ * eagerly). A caller may capture the context's stream around this call: the
+ * launches are then recorded in the caller's graph, provided the buffers for
+ * (h, w) are already planned (one call of that size before the capture);
+ * otherwise the call is refused with an error, since planning allocates and
+ * synchronises the stream, and the context is left as it was.
+ * `s2s_forward` runs this pass on its own device copies. */
 int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
 
 /* `s2s_forward_device` without allocating anything: every intermediate
@@ -154,8 +159,13 @@ int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_o
  * with an error (classical x4 at C = 180: padded planes up to ~38,900 pixels,
  * i.e. images up to 191 x 191; `s2s_plan_bytes` less the two host-path copies
  * is the figure). Every call on one GPU shares that GPU's workspace, which
- * keeps the last call's contents: calls that overlap on one GPU (other
- * contexts or streams) race. */
+ * keeps the last call's contents. Eager calls are ordered on the device: each
+ * makes its stream wait for the workspace's previous user (an event the
+ * library creates per GPU at `s2s_create`) and records itself as the last, so
+ * contexts on different streams take the workspace in the order their calls
+ * were made. A call captured into a caller's graph is not ordered that way:
+ * its replays run when the caller launches them, so a replay that overlaps
+ * another call or replay on the same GPU races on the workspace. */
 int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
 
 /* `Backend::aux` (reference src/gpu.rs:756-758): the last forward's secondary

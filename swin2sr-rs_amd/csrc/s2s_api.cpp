@@ -231,6 +231,11 @@ struct s2s_ctx {
     void image_specs(int h, int w, bool io, bool bind, std::vector<BufSpec> &v);
     int plan_body(int hp, int wp);
     int plan_image(int h, int w);
+    // whether plan_image(h, w) would keep the current buffers
+    bool plan_fits(int h, int w) const {
+        const int hp = (h / arch.window + 1) * arch.window, wp = (w / arch.window + 1) * arch.window;
+        return h == ih && w == iw && hp == bhp && wp == bwp;
+    }
     int stage_buffers(int h, int w);
     hipEvent_t event();
     int drain();
@@ -280,8 +285,14 @@ void free_list(AllocList &l) {
 
 }  // namespace
 
+// The exec graph's last launch may still be queued on the stream: HIP does not
+// promise to defer the destruction of an exec graph in flight, so the stream
+// drains first (this runs only when a graph is replaced or a plan changes).
 void s2s_ctx::drop_graph() {
-    if (gexec) (void)hipGraphExecDestroy(gexec);
+    if (gexec) {
+        if (stream) (void)hipStreamSynchronize(stream);
+        (void)hipGraphExecDestroy(gexec);
+    }
     gexec = nullptr;
     gkey = GraphKey{};
 }
@@ -339,18 +350,34 @@ static __device__ __align__(256) unsigned char scratch[S2S_NOALLOC_SCRATCH_BYTES
 static constexpr int kMaxDevices = 64;
 static void *g_scratch[kMaxDevices];
 static std::mutex g_scratch_mu;
+// The workspace's last user on each device: every eager allocation-free call
+// makes its stream wait for this event before its first launch and records it
+// after its last, under g_ws_mu[device], so calls from different contexts
+// (different streams) take the workspace one after the other instead of
+// racing on it. Created with the address, at s2s_create (an event, not an
+// allocation on the call's path).
+static hipEvent_t g_ws_event[kMaxDevices];
+static std::mutex g_ws_mu[kMaxDevices];
 
-// Looks up the current device's address of `scratch`, once per device.
+// Looks up the current device's address of `scratch`, and creates its
+// ordering event, once per device.
 static int scratch_init(int dev) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (dev < 0 || dev >= kMaxDevices) return fail("device index out of range for the workspace table");
     if (g_scratch[dev]) return 0;
     void *p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
         (void)hipGetLastError();
         return fail(hip_msg("hipGetSymbolAddress(scratch)", e == hipSuccess ? hipErrorInvalidSymbol : e));
     }
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(hip_msg("hipEventCreate(workspace order)", e));
+    }
+    g_ws_event[dev] = ev;
     g_scratch[dev] = p;
     return 0;
 }
@@ -453,7 +480,7 @@ int s2s_ctx::plan_body(int hp, int wp) {
 int s2s_ctx::plan_image(int h, int w) {
     const int win = arch.window;
     const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
-    if (h == ih && w == iw && hp == bhp && wp == bwp) return 0;
+    if (plan_fits(h, w)) return 0;
     if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
     drop_graph();
     ++plan_gen;
@@ -734,13 +761,30 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out, bool 
                     " window. The reference pads to the NEXT window multiple by concatenating "
                     "the image with its own mirror, which for an image shorter than a window "
                     "falls through to a different padding rule this engine does not implement.");
-    if (plan_image(h, w)) return -1;
-    if (!may_graph || prof || !graphs) return forward_launches(h, w, d_in, d_out);
-    // a caller capturing the context's stream into a graph of its own gets
-    // the launches recorded there
+    // A caller capturing the context's stream into a graph of its own gets
+    // the launches recorded there. A new buffer plan cannot be made then:
+    // planning synchronises the stream and allocates, which would end the
+    // caller's capture in an error; the call is refused instead and the
+    // context stays as it was.
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIPCHK("hipStreamIsCapturing", hipStreamIsCapturing(stream, &cs));
-    if (cs != hipStreamCaptureStatusNone) return forward_launches(h, w, d_in, d_out);
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (capturing && !plan_fits(h, w))
+        return fail("s2s_forward_device: the context's stream is being captured into a graph and a " +
+                    std::to_string(h) + "x" + std::to_string(w) +
+                    " image needs a new buffer plan (planning allocates and synchronises the "
+                    "stream, which a capture does not allow); run one call of this size before "
+                    "capturing, or capture s2s_forward_device_noalloc");
+    if (plan_image(h, w)) return -1;
+    if (capturing) {
+        // the launches go into the caller's graph; no profiler events there
+        const bool p = prof;
+        prof = false;
+        const int rc = forward_launches(h, w, d_in, d_out);
+        prof = p;
+        return rc;
+    }
+    if (!may_graph || prof || !graphs) return forward_launches(h, w, d_in, d_out);
     const GraphKey k{h, w, d_in, d_out, plan_gen};
     if (gexec && k == gkey) {
         HIPCHK("hipGraphLaunch", hipGraphLaunch(gexec, stream));
@@ -1719,7 +1763,21 @@ int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, fl
     ctx->ih = h;
     ctx->iw = w;
     ctx->prof = false;
-    return ctx->forward_device(h, w, d_in, d_out, false);
+    // An eager call waits on the stream for the workspace's previous user
+    // (any context on this GPU) and marks itself its last. A call captured
+    // into a caller's graph is not ordered here: its replays run when the
+    // caller launches them, so overlapping replays and calls still race.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIPCHK("hipStreamIsCapturing", hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone) return ctx->forward_device(h, w, d_in, d_out, false);
+    std::lock_guard<std::mutex> lock(g_ws_mu[ctx->device]);
+    HIPCHK("hipStreamWaitEvent(workspace)", hipStreamWaitEvent(ctx->stream, g_ws_event[ctx->device], 0));
+    const int rc = ctx->forward_device(h, w, d_in, d_out, false);
+    // recorded after a failed call too: whatever it launched is then waited for
+    const hipError_t e = hipEventRecord(g_ws_event[ctx->device], ctx->stream);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(hip_msg("hipEventRecord(workspace)", e));
+    return 0;
 }
 
 // Host copy out of the pinned staging image into the caller's buffer with

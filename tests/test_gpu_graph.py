@@ -158,3 +158,103 @@ def test_graph_replays_other_models(pkg, name):
     finally:
         graph.close()
         eager.close()
+
+
+def _async_copy(hip, stream, dst, src, nbytes):
+    """A device-to-device copy ordered on `stream` (hipMemcpyAsync)."""
+    import ctypes as C
+
+    h_ = hip.rt()
+    h_.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    h_.hipMemcpyAsync.restype = C.c_int
+    assert h_.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), nbytes, hip.D2D, C.c_void_p(stream)) == 0
+
+
+def test_graph_replaced_while_a_replay_is_in_flight(pkg):
+    """Calls A, A, A, B, B, A (two input/output pairs of one size) enqueued
+    with no synchronisation between them: the third A is a replay still queued
+    when the second B captures a new graph and the library destroys A's. Each
+    call's output, snapshotted by a copy ordered on the stream right after it,
+    equals the eager context's bit for bit."""
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    wts = M.make_weights(arch, seed=8, perturb=True)
+    h, w = 40, 56
+    n_out = 3 * h * 4 * w * 4
+    xa = M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=11)))
+    xb = M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=12)))
+    eager = make_backend(pkg, arch, wts, graphs=False)
+    graph = make_backend(pkg, arch, wts, graphs=True)
+    bufs = []
+    try:
+        want = {"A": eager.forward(h, w, xa), "B": eager.forward(h, w, xb)}
+        pairs = {"A": (hip.DeviceBuffer.from_array(xa), hip.DeviceBuffer(n_out)),
+                 "B": (hip.DeviceBuffer.from_array(xb), hip.DeviceBuffer(n_out))}
+        bufs = [b for p in pairs.values() for b in p]
+        seq = ["A", "A", "A", "B", "B", "A"]
+        snaps = [hip.DeviceBuffer(n_out) for _ in seq]
+        bufs += snaps
+        st = graph.stream()
+        for k, snap in zip(seq, snaps):
+            din, dout = pairs[k]
+            graph.forward_device(h, w, din.ptr, dout.ptr)
+            _async_copy(hip, st, snap.ptr, dout.ptr, n_out * 4)
+        hip.stream_synchronize(st)
+        for i, (k, snap) in enumerate(zip(seq, snaps)):
+            got = snap.download((3, h * 4, w * 4))
+            assert np.array_equal(got, want[k]), (i, k, float(np.abs(got - want[k]).max()))
+    finally:
+        for b in bufs:
+            b.free()
+        graph.close()
+        eager.close()
+
+
+def test_capture_around_a_new_size_is_refused(pkg):
+    """A caller capturing the context's stream around a call whose image size
+    needs a new buffer plan gets an error naming the cause (planning would
+    allocate and synchronise the captured stream); its capture ends cleanly,
+    and the context still runs both sizes afterwards, bit-exact against an
+    eager context."""
+    import ctypes as C
+
+    M, hip = pkg.model, pkg.hip
+    h_ = hip.rt()
+    vp = C.c_void_p
+    for name, args in {"hipStreamBeginCapture": [vp, C.c_int], "hipStreamEndCapture": [vp, C.POINTER(vp)],
+                       "hipGraphDestroy": [vp]}.items():
+        getattr(h_, name).argtypes = args
+        getattr(h_, name).restype = C.c_int
+    arch = M.classical(4)
+    wts = M.make_weights(arch, seed=9, perturb=True)
+    (h, w), (h2, w2) = (16, 24), (24, 40)
+    x = M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=1)))
+    x2 = M.adjust(arch, M.to_unit(M.input_sinusoids(h2, w2, seed=2)))
+    eager = make_backend(pkg, arch, wts, graphs=False)
+    graph = make_backend(pkg, arch, wts, graphs=True)
+    g = vp()
+    try:
+        want, want2 = eager.forward(h, w, x), eager.forward(h2, w2, x2)
+        din, dout = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer(3 * h * 4 * w * 4)
+        din2, dout2 = hip.DeviceBuffer.from_array(x2), hip.DeviceBuffer(3 * h2 * 4 * w2 * 4)
+        graph.forward_device(h, w, din.ptr, dout.ptr)
+        hip.stream_synchronize(graph.stream())
+        st = vp(graph.stream())
+        assert h_.hipStreamBeginCapture(st, 2) == 0
+        with pytest.raises(pkg.abi.S2SError, match="needs a new buffer plan"):
+            graph.forward_device(h2, w2, din2.ptr, dout2.ptr)
+        assert h_.hipStreamEndCapture(st, C.byref(g)) == 0
+        for _ in range(3):  # eager, captured + launched, replayed
+            graph.forward_device(h, w, din.ptr, dout.ptr)
+            hip.stream_synchronize(graph.stream())
+            assert np.array_equal(dout.download((3, h * 4, w * 4)), want)
+        graph.forward_device(h2, w2, din2.ptr, dout2.ptr)
+        hip.stream_synchronize(graph.stream())
+        assert np.array_equal(dout2.download((3, h2 * 4, w2 * 4)), want2)
+        for b in (din, dout, din2, dout2):
+            b.free()
+    finally:
+        if g.value:
+            h_.hipGraphDestroy(g)
+        graph.close()
+        eager.close()

@@ -42,12 +42,16 @@ def test_headline_workload(pkg, orc):
         got = be.forward(h, w, x)
         din = hip.DeviceBuffer.from_array(x)
         dout = hip.DeviceBuffer(3 * 1024 * 1024)
-        be.forward_device(h, w, din.ptr, dout.ptr)
-        hip.stream_synchronize(be.stream())
-        got_dev = dout.download((3, 1024, 1024))
+        # three identical calls, as the bench makes them: launched kernel by
+        # kernel, captured into the library's graph and launched, replayed
+        for i in range(3):
+            dout.upload(np.zeros(3 * 1024 * 1024, np.float32))
+            be.forward_device(h, w, din.ptr, dout.ptr)
+            hip.stream_synchronize(be.stream())
+            got_dev = dout.download((3, 1024, 1024))
+            assert np.array_equal(got, got_dev), (i, float(np.abs(got - got_dev).max()))
     finally:
         be.close()
-    assert np.array_equal(got, got_dev)
     want, _ = orc.forward(arch, wts, h, w, x)
     check_image(M, got, want)
 
@@ -144,9 +148,10 @@ def test_config4_compressed_tiled(pkg, orc):
     """Config 4: compressed x4 (pixelshuffle_aux), 6x6 layers, 1024x1024 in
     256-pixel tiles with 64 of context (16 tiles on 392x392 planes) -> 4096 x
     4096, weights seed 5, config 3's input generator at seed 5. Parity per tile
-    against the oracle on the same crop (output and aux image) for a corner,
-    an edge and an interior tile; every tile of the assembled image is the
-    device tile's interior."""
+    against the oracle on the same crop (output and aux image) for one tile of
+    each of the four crop shapes - a corner (320x320), the two edges (320x384
+    and 384x320) and an interior tile (384x384) - and for the far corner; every
+    tile of the assembled image is the device tile's interior."""
     M = pkg.model
     arch = M.compressed()
     wts = M.make_weights(arch, seed=5)
@@ -160,8 +165,9 @@ def test_config4_compressed_tiled(pkg, orc):
     assert out.shape == (3, 4096, 4096) and np.isfinite(out).all()
     assert len(rec.calls) == 16
     assert {(h, w) for h, w, *_ in rec.calls} == {(320, 320), (320, 384), (384, 320), (384, 384)}
-    for i in (0, 6, 15):  # tile (0,0), (1,2), (3,3)
+    for i in (0, 1, 4, 6, 15):  # tiles (0,0), (0,1), (1,0), (1,2), (3,3)
         h, w, x, got, aux = rec.calls[i]
+        assert (h, w) == {0: (320, 320), 1: (320, 384), 4: (384, 320), 6: (384, 384), 15: (320, 320)}[i]
         want, want_aux = orc.forward(arch, wts, h, w, x)
         check_image(M, got, want, aux, want_aux)
         ty, tx = divmod(i, 4)

@@ -189,7 +189,58 @@ def test_the_pad_rounds_up_to_a_whole_window(pkg, orc):
     assert not np.array_equal(two, one)
 
 
+def seam_image():
+    """reference tests/tiling.rs:258-261: frac(0.618034 (3c + 11y + 29x)) on 32x32."""
+    c = np.arange(3)[:, None, None]
+    y = np.arange(32)[None, :, None]
+    x = np.arange(32)[None, None, :]
+    t = (c * 3 + y * 11 + x * 29).astype(np.float32) * np.float32(0.618034)
+    return (t - np.floor(t)).astype(np.float32)
+
+
+def seam_errors(pkg, a, be):
+    """(one window of context, two windows) around 16-pixel tiles: the largest
+    difference from the whole-image pass (reference tests/tiling.rs:262-265)."""
+    T, img = pkg.tiling, seam_image()
+    whole = T.run_tiled(a, be, img, 0, 0)
+    win = a.window
+    thin = float(np.abs(T.run_tiled(a, be, img, 2 * win, win) - whole).max())
+    thick = float(np.abs(T.run_tiled(a, be, img, 2 * win, 2 * win) - whole).max())
+    return thin, thick
+
+
+def test_context_reduces_the_tiling_error(pkg, orc):
+    """reference tests/tiling.rs:252-274 on the lightweight x2 model (random
+    weights by the benchmark's rules, seed 0; the reference uses the published
+    checkpoint): one window of context must leave more seam error than two,
+    and two at most 0.02 (here, as in the reference's comment, exactly 0)."""
+    M = pkg.model
+    a = M.lightweight(2)
+    thin, thick = seam_errors(pkg, a, OracleBackend(orc, a, M.make_weights(a, seed=0)))
+    assert thin > thick, (thin, thick)
+    assert thick <= 0.02, thick
+
+
 # ---- the HIP backend through the tile loop ---------------------------------------
+
+@pytest.mark.gpu
+def test_context_reduces_the_tiling_error_on_the_device(pkg, orc):
+    """The same property with the HIP backend behind the tile loop: one window
+    of context leaves more error than two, two leave at most 0.02, and both
+    figures equal the oracle's to 1e-4."""
+    M = pkg.model
+    a = M.lightweight(2)
+    wts = M.make_weights(a, seed=0)
+    be = pkg.abi.HipBackend(a, wts)
+    try:
+        thin, thick = seam_errors(pkg, a, be)
+    finally:
+        be.close()
+    assert thin > thick, (thin, thick)
+    assert thick <= 0.02, thick
+    o_thin, o_thick = seam_errors(pkg, a, OracleBackend(orc, a, wts))
+    assert abs(thin - o_thin) <= 1e-4 and abs(thick - o_thick) <= 1e-4, (thin, o_thin, thick, o_thick)
+
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("tile,pad", [(16, 8), (24, 16), (0, 0)])

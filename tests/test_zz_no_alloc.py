@@ -94,3 +94,41 @@ def test_noalloc_between_graph_replays(pkg):
         for b in (din, dout, dna):
             b.free()
         be.close()
+
+
+def test_noalloc_contexts_on_two_streams_take_turns(pkg):
+    """Two contexts (two streams) calling the allocation-free entry back to
+    back with no synchronisation between the calls share the GPU's one
+    workspace; the library orders them on the device (each call waits for the
+    workspace's previous user), so every output equals the same call run on
+    its own, bit for bit."""
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    bes = [pkg.HipBackend(arch, M.make_weights(arch, seed=s, perturb=True)) for s in (21, 22)]
+    h, w = 120, 96
+    n_out = 3 * h * 4 * w * 4
+    xs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=s))) for s in (31, 32, 33)]
+    dins = [hip.DeviceBuffer.from_array(x) for x in xs]
+    # (context, input) per call, interleaved between the two contexts
+    calls = [(0, 0), (1, 1), (0, 2), (1, 0), (0, 1), (1, 2)]
+    outs = [hip.DeviceBuffer(n_out) for _ in calls]
+    try:
+        want = {}
+        for b, i in set(calls):  # each call on its own, synchronised
+            d = hip.DeviceBuffer(n_out)
+            bes[b].forward_device_noalloc(h, w, dins[i].ptr, d.ptr)
+            hip.stream_synchronize(bes[b].stream())
+            want[(b, i)] = d.download((3, h * 4, w * 4))
+            d.free()
+        for (b, i), o in zip(calls, outs):
+            bes[b].forward_device_noalloc(h, w, dins[i].ptr, o.ptr)
+        for be in bes:
+            hip.stream_synchronize(be.stream())
+        for k, ((b, i), o) in enumerate(zip(calls, outs)):
+            got = o.download((3, h * 4, w * 4))
+            assert np.array_equal(got, want[(b, i)]), (k, b, i, float(np.abs(got - want[(b, i)]).max()))
+    finally:
+        for buf in dins + outs:
+            buf.free()
+        for be in bes:
+            be.close()
