@@ -106,8 +106,19 @@ struct BufSpec {
 // their total size.
 struct AllocList {
     std::vector<void *> ptrs;
+    std::vector<size_t> floats;  // each allocation's size, in the plan's order
     uint64_t bytes = 0;
 };
+
+// Whether the buffers of `v` fit the allocations of `l` one for one (the
+// same plan layout, each no larger than what is held).
+static bool fits_in(const AllocList &l, const std::vector<BufSpec> &v) {
+    if (l.floats.size() != v.size()) return false;
+    for (size_t i = 0; i < v.size(); ++i)
+        if (std::max<size_t>(v[i].floats, 1) > l.floats[i]) return false;
+    return true;
+}
+
 
 struct s2s_ctx {
     s2s_arch arch{};
@@ -166,7 +177,7 @@ struct s2s_ctx {
     float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr, *bicf = nullptr;
     // the host path's pinned staging copies of the input and output images
     float *pin_in = nullptr, *pin_out = nullptr;
-    int pin_h = 0, pin_w = 0;
+    size_t pin_in_floats = 0, pin_out_floats = 0;
     // a cap on the bytes of the body and image plans together (0 = none):
     // SWIN2SR_HIP_ALLOC_LIMIT at s2s_create, or s2s_set_alloc_limit
     uint64_t alloc_limit = 0;
@@ -231,10 +242,32 @@ struct s2s_ctx {
     void image_specs(int h, int w, bool io, bool bind, std::vector<BufSpec> &v);
     int plan_body(int hp, int wp);
     int plan_image(int h, int w);
-    // whether plan_image(h, w) would keep the current buffers
+    // whether the current plan is for (h, w)
     bool plan_fits(int h, int w) const {
         const int hp = (h / arch.window + 1) * arch.window, wp = (w / arch.window + 1) * arch.window;
         return h == ih && w == iw && hp == bhp && wp == bwp;
+    }
+    // whether the held buffers can serve a plane / an image of this size
+    // without allocating (within the allocation limit, if one is set)
+    bool held_within_limit() const {
+        return !alloc_limit || body_allocs.bytes + head_allocs.bytes <= alloc_limit;
+    }
+    bool body_reusable(int hp, int wp) {
+        if (!bhp || !held_within_limit()) return false;
+        std::vector<BufSpec> v;
+        body_specs(hp, wp, false, v);
+        return fits_in(body_allocs, v);
+    }
+    bool image_reusable(int h, int w) {
+        if (!ih || !held_within_limit()) return false;
+        std::vector<BufSpec> v;
+        image_specs(h, w, true, false, v);
+        return fits_in(head_allocs, v);
+    }
+    // whether plan_image(h, w) would allocate (or synchronise the stream)
+    bool plan_allocates(int h, int w) {
+        const int hp = (h / arch.window + 1) * arch.window, wp = (w / arch.window + 1) * arch.window;
+        return !plan_fits(h, w) && !(image_reusable(h, w) && body_reusable(hp, wp));
     }
     int stage_buffers(int h, int w);
     hipEvent_t event();
@@ -280,8 +313,10 @@ std::vector<float> gemm_weights(const std::vector<float> &rows, int nb, int N, i
 void free_list(AllocList &l) {
     for (void *p : l.ptrs) (void)hipFree(p);
     l.ptrs.clear();
+    l.floats.clear();
     l.bytes = 0;
 }
+
 
 }  // namespace
 
@@ -405,6 +440,7 @@ int s2s_ctx::alloc(AllocList &list, size_t floats, float **dev, const char *what
                     hipGetErrorString(e) + (e == hipErrorOutOfMemory ? " (out of memory)" : ""));
     }
     list.ptrs.push_back(p);
+    list.floats.push_back(std::max<size_t>(floats, 1));
     list.bytes += bytes;
     *dev = p;
     return 0;
@@ -457,9 +493,19 @@ void s2s_ctx::image_specs(int h, int w, bool io, bool bind, std::vector<BufSpec>
 }
 
 // Reused while the plane size repeats (reference Gpu::forward rebuilds Acts
-// only on a size change, src/gpu.rs:741-750).
+// only on a size change, src/gpu.rs:741-750), and also when a new plane's
+// buffers each fit the ones held (a smaller tile after a larger one, or the
+// same number of pixels transposed, as a tiled image alternates): the
+// buffers stay where they are, nothing is freed or allocated and the stream
+// is not synchronised. A plane that needs more is planned afresh at its own
+// size.
 int s2s_ctx::plan_body(int hp, int wp) {
     if (hp == bhp && wp == bwp) return 0;
+    if (body_reusable(hp, wp)) {
+        bhp = hp;
+        bwp = wp;
+        return 0;
+    }
     if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
     drop_graph();
     ++plan_gen;
@@ -481,6 +527,13 @@ int s2s_ctx::plan_image(int h, int w) {
     const int win = arch.window;
     const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
     if (plan_fits(h, w)) return 0;
+    if (image_reusable(h, w) && body_reusable(hp, wp)) {
+        bhp = hp;
+        bwp = wp;
+        ih = h;
+        iw = w;
+        return 0;
+    }
     if (stream) HIPCHK("hipStreamSynchronize", hipStreamSynchronize(stream));
     drop_graph();
     ++plan_gen;
@@ -510,23 +563,26 @@ int s2s_ctx::plan_image(int h, int w) {
 
 // The host path's pinned staging images for an h x w image (page-locked, so
 // the copies run as DMA at the link's rate and the host-side copies overlap
-// them). Only s2s_forward uses them.
+// them). Only s2s_forward uses them. Kept while an image fits them (pinning
+// a fresh buffer costs milliseconds, and a tiled image alternates sizes).
 int s2s_ctx::stage_buffers(int h, int w) {
-    if (h == pin_h && w == pin_w) return 0;
+    const int s = arch.scale;
+    const size_t nin = (size_t)3 * h * w, nout = nin * s * s;
+    if (pin_in && nin <= pin_in_floats && nout <= pin_out_floats) return 0;
     if (pin_in) (void)hipHostFree(pin_in);
     if (pin_out) (void)hipHostFree(pin_out);
     pin_in = pin_out = nullptr;
-    pin_h = pin_w = 0;
-    const int s = arch.scale;
-    hipError_t e = hipHostMalloc((void **)&pin_in, (size_t)3 * h * w * sizeof(float));
-    if (e == hipSuccess)
-        e = hipHostMalloc((void **)&pin_out, (size_t)3 * h * s * w * s * sizeof(float));
+    pin_in_floats = pin_out_floats = 0;
+    hipError_t e = hipHostMalloc((void **)&pin_in, nin * sizeof(float));
+    if (e == hipSuccess) e = hipHostMalloc((void **)&pin_out, nout * sizeof(float));
     if (e != hipSuccess) {
         (void)hipGetLastError();
+        if (pin_in) (void)hipHostFree(pin_in);
+        pin_in = nullptr;
         return fail(hip_msg("hipHostMalloc(staging)", e));
     }
-    pin_h = h;
-    pin_w = w;
+    pin_in_floats = nin;
+    pin_out_floats = nout;
     return 0;
 }
 
@@ -769,7 +825,7 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out, bool 
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIPCHK("hipStreamIsCapturing", hipStreamIsCapturing(stream, &cs));
     const bool capturing = cs != hipStreamCaptureStatusNone;
-    if (capturing && !plan_fits(h, w))
+    if (capturing && plan_allocates(h, w))
         return fail("s2s_forward_device: the context's stream is being captured into a graph and a " +
                     std::to_string(h) + "x" + std::to_string(w) +
                     " image needs a new buffer plan (planning allocates and synchronises the "

@@ -169,3 +169,43 @@ def test_head_planes_past_2gib(pkg, upsampler):
         assert np.array_equal(big[sl], small[sl])
     finally:
         be.close()
+
+
+@pytest.mark.parametrize("upsampler", ["pixelshuffle", "pixelshuffle_aux"])
+def test_held_buffers_serve_smaller_and_transposed_images(pkg, upsampler):
+    """A context keeps its buffers while a new image's plan fits them (a
+    smaller image after a larger one, the same pixel count transposed, as a
+    tiled image alternates), and plans afresh only for a larger one. Through a
+    sequence of sizes on one context, host and device entries and the graph
+    replays included, every output (and aux image) equals that of a fresh
+    context run at that size alone, bit for bit."""
+    M, hip = pkg.model, pkg.hip
+    arch = M.Arch(upsampler=upsampler, scale=4, embed=180, heads=6, depths=[1, 1])
+    wts = M.make_weights(arch, seed=12, perturb=True)
+    sizes = [(40, 56), (24, 40), (40, 24), (16, 16), (40, 56), (48, 64), (24, 40)]
+    xs = {hw: M.adjust(arch, M.to_unit(M.input_sinusoids(*hw, seed=hw[0] + hw[1]))) for hw in set(sizes)}
+    want = {}
+    for hw, x in xs.items():
+        fresh = pkg.HipBackend(arch, wts)
+        try:
+            want[hw] = (fresh.forward(*hw, x), fresh.aux())
+        finally:
+            fresh.close()
+    be = pkg.HipBackend(arch, wts)
+    try:
+        for h, w in sizes:
+            got = be.forward(h, w, xs[(h, w)])
+            assert np.array_equal(got, want[(h, w)][0]), (h, w)
+            if upsampler == "pixelshuffle_aux":
+                assert np.array_equal(be.aux(), want[(h, w)][1]), (h, w)
+            # the device entry three times (eager, captured, replayed)
+            din = hip.DeviceBuffer.from_array(xs[(h, w)])
+            dout = hip.DeviceBuffer(3 * h * 4 * w * 4)
+            for _ in range(3):
+                be.forward_device(h, w, din.ptr, dout.ptr)
+                hip.stream_synchronize(be.stream())
+                assert np.array_equal(dout.download((3, h * 4, w * 4)), want[(h, w)][0]), (h, w)
+            din.free()
+            dout.free()
+    finally:
+        be.close()
