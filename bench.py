@@ -14,7 +14,8 @@ repeated call.
 
 One JSON line on stdout. `roofline` is for the kernel with the largest share
 of device time per step, its launches timed with HIP events on the library's
-own stream over K more forwards launched kernel by kernel; `cpu_baseline` is
+own stream (a pair around every launch of K forwards launched kernel by
+kernel, before the timed replays); `cpu_baseline` is
 this repository's C restatement of the crate's CPU path (oracle/, OpenMP over
 the host cores) on a bounded sample. The replayed output is checked bit for
 bit against an eager forward of the same input; a mismatch fails the run.
@@ -226,7 +227,7 @@ def roofline_of(work, kernel, ms, n, traffic=True):
             "work_per_launch": fl if bound in FLOP_PEAK else by}
 
 
-def kernel_table(be, work, steps, rows=None):
+def kernel_table(be, work, steps, rows=None, traffic=True):
     """Per-kernel (launches, avg ms, share, rate) from the library's event
     profiler, logged; returns the rows and the dominant kernel's roofline."""
     if rows is None:
@@ -245,7 +246,7 @@ def kernel_table(be, work, steps, rows=None):
                     "frac": round(rate / (FLOP_PEAK[bound] / 1e12 if bound in FLOP_PEAK else HBM_PEAK / 1e9), 4),
                     "algorithmic_GBps": round(hbm, 1)}
     dom = max(rows, key=lambda k: rows[k][0])
-    roofline = roofline_of(work, dom, *rows[dom])
+    roofline = roofline_of(work, dom, *rows[dom], traffic=traffic)
     roofline["device_ms_per_step"] = round(total_dev / steps, 3)
     return table, roofline
 
@@ -267,18 +268,16 @@ def bench_rstb(args, pkg):
     for _ in range(args.warmup):
         be.rstb_device(0, hp, wp, din.ptr, dout.ptr)
     hip.synchronize()
-    # per-kernel pass (events around every launch), then the timed calls with
-    # events around the dominant kernel only
+    # per-kernel pass (events around every launch: the per-kernel table and
+    # the dominant kernel's roofline), then the timed calls without events
     work = kernel_work(arch, hp, wp, hp=hp, wp=wp)
     be.profile(True)
     be.profile_reset()
     for _ in range(args.steps):
         be.rstb_device(0, hp, wp, din.ptr, dout.ptr)
     hip.synchronize()
-    table, roofline_all = kernel_table(be, work, args.steps)
-    dom = roofline_all["kernel"]
-    be.profile_only(dom)
-    be.profile_reset()
+    table, roofline = kernel_table(be, work, args.steps, traffic=False)
+    be.profile(False)
     hip.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -287,10 +286,6 @@ def bench_rstb(args, pkg):
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     assert np.isfinite(dout.download()).all()
     log(f"bench: rstb {args.steps} calls, {ms:.3f} ms per RSTB")
-    roofline = roofline_of(work, dom, *profile_rows(be, {dom: work[dom]})[dom], traffic=False)
-    roofline["device_ms_per_step"] = roofline_all["device_ms_per_step"]
-    be.profile_only(None)
-    be.profile(False)
     be.close()
     print(json.dumps({
         "metric": "single-RSTB ms, 256x256x180 fp32 (6 Swin V2 layers + conv3x3 + 1x1 + residual)",
@@ -300,7 +295,7 @@ def bench_rstb(args, pkg):
         "data": "synthetic (N(0,1) activations seed 2, random-init weights seed 0)",
         "config": {"workload": "config 1: single RSTB on an unpadded 256x256x180 plane",
                    "windows": (hp // 8) * (wp // 8), "parallelism": "1 GPU"},
-        "roofline": roofline, "kernels": table}), flush=True)
+        "roofline": roofline, "kernels": table, "kernel_timing": TIMING_NOTE}), flush=True)
 
 
 def image_workload(M, name, size):
@@ -370,9 +365,14 @@ def bench_image(args, pkg, name):
     hip.stream_synchronize(stream)
     log(f"bench: {args.warmup} warm-up steps done")
 
-    # per-kernel pass: K forwards with an event pair around every launch on the
-    # library stream (the events cost ~2 us per launch, so this pass is not the
-    # one `value` is read from); it names the dominant kernel
+    # per-kernel pass: K forwards launched kernel by kernel with an event pair
+    # around every launch on the library stream (the events cost ~2 us per
+    # launch, so this pass is not the one `value` is read from). It names the
+    # dominant kernel and gives its launch duration for `roofline`: each launch
+    # bracketed by its own pair, as rocprofv3's trace of the same command
+    # brackets it (an event pair around that kernel's launches alone read
+    # 2-3% longer on the box: the first marker after the preceding kernel
+    # then carries that kernel's completion)
     work = kernel_work(arch, h, w)
     be.profile(True)
     be.profile_reset()
@@ -383,14 +383,16 @@ def bench_image(args, pkg, name):
     hip.synchronize()
     prof_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     log(f"bench: per-kernel pass (events around every launch): {prof_ms:.3f} ms/step")
-    table, roofline_all = kernel_table(be, work, args.steps)
-    dom = roofline_all["kernel"]
+    table, roofline = kernel_table(be, work, args.steps, traffic=headline)
+    be.profile(False)
+    dom = roofline["kernel"]
+    log(f"bench: {dom}: {roofline['avg_ms']:.4f} ms avg, "
+        f"{roofline['achieved']} {roofline['unit']} ({100 * roofline['frac']:.1f}% of peak)")
 
     # timed region: K whole-image forwards as the library runs a repeated
     # call: its launches replayed from the HIP graph it captures the second
     # time the same call comes (the two untimed calls below make sure it has;
     # no events: an event pair cannot bracket one kernel of a graph)
-    be.profile(False)
     be.forward_device(h, w, din.ptr, dout.ptr)
     be.forward_device(h, w, din.ptr, dout.ptr)
     hip.synchronize()
@@ -420,25 +422,6 @@ def bench_image(args, pkg, name):
         be.close()
         sys.exit(1)
     log(f"bench: replayed output equals the eager forward's bit for bit (sha256 {digest})")
-
-    # the dominant kernel's launch duration, for its roofline: the same K
-    # forwards launched kernel by kernel on the library's stream, an event
-    # pair around each of that kernel's launches only (a kernel runs the same
-    # whichever way it is launched; rocprofv3's trace of the graph replays
-    # agrees)
-    be.profile(True)
-    be.profile_only(dom)
-    be.profile_reset()
-    hip.synchronize()
-    for _ in range(args.steps):
-        be.forward_device(h, w, din.ptr, dout.ptr)
-    hip.synchronize()
-    roofline = roofline_of(work, dom, *profile_rows(be, {dom: work[dom]})[dom], traffic=headline)
-    roofline["device_ms_per_step"] = roofline_all["device_ms_per_step"]
-    log(f"bench: {dom}: {roofline['avg_ms']:.4f} ms avg, "
-        f"{roofline['achieved']} {roofline['unit']} ({100 * roofline['frac']:.1f}% of peak)")
-    be.profile_only(None)
-    be.profile(False)
 
     win = arch.window
     result = {
@@ -568,8 +551,46 @@ def bench_tiled(args, pkg):
         "cpu_baseline": None}), flush=True)
 
 
+def bench_copy_ceiling(args, pkg):
+    """The HBM streaming ceiling the memory-bound kernels are read against: the
+    runtime's own device-to-device copy kernel (hipMemcpy), timed with events
+    over `steps` copies enqueued back to back on the null stream at each size;
+    bytes moved = 2 x size (read + write).
+    The sizes span the memory-bound kernels' traffic at the headline workload
+    (50 MB planes to the 213 MB of the Winograd output transform) and a 1 GiB
+    copy, larger than the 256 MB last-level cache. One JSON line."""
+    hip = pkg.hip
+    res = {}
+    for mib in (16, 50, 100, 200, 400, 1024):
+        n = mib * 2**20 // 4
+        a, b = hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+        for _ in range(max(args.warmup, 1)):
+            hip.copy_device(b.ptr, a.ptr, n * 4)
+        hip.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(0)
+        for _ in range(args.steps):
+            hip.copy_device_async(b.ptr, a.ptr, n * 4, 0)
+        e1.record(0)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / args.steps
+        gbps = 2 * n * 4 / (ms / 1e3) / 1e9
+        res[f"{mib} MiB"] = {"avg_ms": round(ms, 4), "GBps": round(gbps, 1),
+                             "frac_of_8TBps": round(gbps / (HBM_PEAK / 1e9), 4)}
+        log(f"bench: copy {mib:5d} MiB: {ms:.4f} ms, {gbps:.1f} GB/s "
+            f"({100 * gbps / (HBM_PEAK / 1e9):.1f}% of 8 TB/s)")
+        a.free()
+        b.free()
+    print(json.dumps({"metric": "device-to-device copy GB/s (read + write bytes) @1 GPU",
+                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "higher_is_better": True, "dtype": "f32", "data": "uninitialised buffers",
+                      "config": {"workload": "hipMemcpyAsync device-to-device (the runtime's "
+                                             "copy kernel), null stream, event-timed"},
+                      "sizes": res}), flush=True)
+
+
 WORKLOADS = ["classical-x4", "rstb", "lightweight-x2", "classical-x2", "realworld-x4",
-             "compressed-x4-tiled"]
+             "compressed-x4-tiled", "copy-ceiling"]
 
 
 def main():
@@ -584,7 +605,8 @@ def main():
     ap.add_argument("--workload", choices=WORKLOADS, default="classical-x4",
                     help="classical-x4: the BASELINE metric (default); rstb: config 1's "
                          "single-RSTB micro-bench; lightweight-x2, classical-x2, realworld-x4: "
-                         "configs 0, 2, 3 whole-image; compressed-x4-tiled: config 4")
+                         "configs 0, 2, 3 whole-image; compressed-x4-tiled: config 4; "
+                         "copy-ceiling: the runtime's device copy at several sizes")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="before the warm-up, one device-to-device copy of this many MiB: the "
                          "plain copy kernel of known size that scales rocprofv3's FETCH_SIZE / "
@@ -601,6 +623,8 @@ def main():
         bench_rstb(args, pkg)
     elif args.workload == "compressed-x4-tiled":
         bench_tiled(args, pkg)
+    elif args.workload == "copy-ceiling":
+        bench_copy_ceiling(args, pkg)
     else:
         bench_image(args, pkg, args.workload)
 

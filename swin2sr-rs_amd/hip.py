@@ -27,6 +27,7 @@ def rt():
         for name, args in {
             "hipMalloc": [C.POINTER(vp), sz], "hipFree": [vp],
             "hipMemcpy": [vp, vp, sz, C.c_int], "hipMemset": [vp, C.c_int, sz],
+            "hipMemcpyAsync": [vp, vp, sz, C.c_int, vp],
             "hipDeviceSynchronize": [], "hipStreamSynchronize": [vp],
             "hipEventCreate": [C.POINTER(vp)], "hipEventDestroy": [vp],
             "hipEventRecord": [vp, vp], "hipEventSynchronize": [vp],
@@ -88,6 +89,12 @@ class DeviceBuffer:
 def copy_device(dst: int, src: int, nbytes: int):
     """Device-to-device hipMemcpy of `nbytes` (the runtime's plain copy kernel)."""
     _chk(rt().hipMemcpy(C.c_void_p(dst), C.c_void_p(src), nbytes, D2D), "hipMemcpy D2D")
+
+
+def copy_device_async(dst: int, src: int, nbytes: int, stream: int = 0):
+    """Device-to-device hipMemcpyAsync of `nbytes`, ordered on `stream`."""
+    _chk(rt().hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), nbytes, D2D, C.c_void_p(stream)),
+         "hipMemcpyAsync D2D")
 
 
 def synchronize():
