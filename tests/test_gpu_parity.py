@@ -391,9 +391,12 @@ def test_forward_rejects_tiny_image(pkg):
 
 
 def test_forward_with_buffers_past_2gib(pkg):
-    """A plane whose qkv buffer (1008^2 x 546 floats = 2.2 GB) and last head
-    plane (1008^2 x 16 x 64 floats = 4.2 GB) pass 2 GiB runs: those buffers are
-    reached through resources based per task, tile or window. The input repeats
+    """A plane whose qkv buffer passes 2 GiB runs: at 1008^2 it is 2.34 GB, set
+    by the x4 head's Winograd F(2x2,5x5) planes (36 x 504^2 tiles x 64 floats;
+    the attention units alone would be 1008^2 x 546 floats = 2.22 GB), and it
+    is reached through resources based per task, tile or window. (The composed
+    head allocates no plane past 2 GiB; test_gpu_boundary.py's
+    test_head_planes_past_2gib covers the heads that do.) The input repeats
     a random 16 x 16 patch, so away from the borders (the reflect padding and
     the shifted-window mask live there) every window, conv tap and pixel sees
     what it sees in a 200 x 200 image of the same pattern, and the outputs
