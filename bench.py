@@ -105,7 +105,8 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         "up2_last": ("mfma", 2 * min(hp * s // 4, -(-h * s // 4)) * (wp * s // 4) * 48 * 25 * F,
                      f * ((hp * s // 4) * (wp * s // 4) * F + 3 * h * s * w * s)),
     }
-    if arch.upsampler == "pixelshuffle" and s == 4 and F == 64:
+    shuffle = arch.upsampler in ("pixelshuffle", "pixelshuffle_aux")
+    if shuffle and s == 4 and F == 64:
         # the x4 head's composed 5x5 conv as Winograd F(2x2,5x5) over the
         # T5 2x2 tiles of the pixels whose outputs survive the crop: the input
         # transform (the plane in, 36 planes of T5 x F out), 36 GEMMs of
@@ -115,7 +116,7 @@ def kernel_work(arch, h, w, hp=None, wp=None):
         work["up2_last_in"] = ("hbm", 0, f * (ho * wo * F + T5 * F))
         work["up2_last"] = ("mfma", 2 * T5 * 48 * F, f * (T5 * (F + 48) + 36 * 48 * F))
         work["up2_last_out"] = ("hbm", 0, f * (T5 * 48 + 3 * h * s * w * s))
-    if arch.upsampler == "pixelshuffle" and s >= 4 and F == 64:
+    if shuffle and s >= 4 and F == 64:
         # input row 0 and column 0 recomputed with the padding-aware variants:
         # 48 outputs of a 5x5xF footprint per border pixel (VALU)
         nb = -(-h * s // 4) + -(-w * s // 4) - 1
@@ -140,15 +141,19 @@ def kernel_work(arch, h, w, hp=None, wp=None):
     work["conv_up1"] = ("mfma", 2 * 4 * P * F * 9 * F, f * (P * F + 4 * P * F))
     work["conv_up2"] = ("mfma", 2 * 16 * P * F * 9 * F, f * (4 * P * F + 16 * P * F))
     work["conv_hr"] = ("mfma", 2 * 16 * P * F * 9 * F, f * 2 * 16 * P * F)
-    # pixelshuffle_aux: bicubic of the padded input to s x the plane (4
-    # channels), conv_bicubic 3 -> F there, conv_aux F -> 3, conv_after_aux
-    # 3 -> F, and the aux image's denormalisation
+    # pixelshuffle_aux: conv_aux F -> 3, conv_after_aux 3 -> F, the aux image's
+    # denormalisation; the bicubic resample of the padded input to s x the
+    # plane (4 channels)
     Q = (hp * s) * (wp * s)
     work["bicubic"] = ("hbm", 0, f * (4 * P + 4 * Q))
-    work["conv_bicubic"] = ("mfma", 2 * Q * F * 27, f * (4 * Q + Q * F))
     work["conv_aux"] = ("mfma", 2 * P * 3 * 9 * F, f * (P * F + 4 * P))
     work["conv_after_aux"] = ("mfma", 2 * P * F * 27, f * (4 * P + P * F))
     work["aux_finish"] = ("hbm", 0, f * (4 * P + 3 * P))
+    # ... and its bicubic branch through conv_last, composed: a 5x5 conv of the
+    # 3 bicubic channels to the 3 outputs over the cropped image (VALU), added
+    # into it (the bicubic plane read, the image read and written)
+    work["bic_last_add"] = ("valu", 2 * (h * s) * (w * s) * 3 * 75,
+                            f * (4 * Q + 2 * 3 * h * s * w * s))
     return work
 
 

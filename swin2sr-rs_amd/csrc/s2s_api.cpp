@@ -154,7 +154,10 @@ struct s2s_ctx {
     // pixelshuffle_aux: conv_bicubic [F][9*4], conv_aux [4][9*F] (its fourth
     // output row zero, so the conv writes channel 3 of the aux plane as 0),
     // conv_after_aux [F][9*4]
-    float *bc_w = nullptr, *bc_b = nullptr, *ax_w = nullptr, *ax_b = nullptr;
+    float *ax_w = nullptr, *ax_b = nullptr;
+    // the compressed head's bicubic branch through conv_last, composed:
+    // [4][25][3][4], [4][3]
+    float *bl_w = nullptr, *bl_b = nullptr;
     float *caa_w = nullptr, *caa_b = nullptr;
     // pixelshuffledirect: upsample.0 [3*s*s][9*C]
     float *psd_w = nullptr, *psd_b = nullptr;
@@ -174,7 +177,7 @@ struct s2s_ctx {
     std::vector<float *> fplanes;  // the head's feature planes
     // pixelshuffle_aux: aux conv output [P][4], its planar image [3][P], the
     // bicubic input [(hp*s)*(wp*s)][4] and its conv (= the last head plane)
-    float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr, *bicf = nullptr;
+    float *aux4 = nullptr, *auxp = nullptr, *bic4 = nullptr;
     // the host path's pinned staging copies of the input and output images
     float *pin_in = nullptr, *pin_out = nullptr;
     size_t pin_in_floats = 0, pin_out_floats = 0;
@@ -551,11 +554,6 @@ int s2s_ctx::plan_image(int h, int w) {
             fplanes.clear();
             return -1;
         }
-    if (arch.upsampler == S2S_PIXELSHUFFLE_AUX)
-        // the bicubic branch's conv lands in the last octave's plane, which the
-        // last shuffle then updates in place (each element read, added, written
-        // by one thread)
-        bicf = fplanes[octaves];
     ih = h;
     iw = w;
     return 0;
@@ -930,14 +928,8 @@ int s2s_ctx::head(int h, int w, float *d_out) {
         const bool aux = arch.upsampler == S2S_PIXELSHUFFLE_AUX;
         if (before_upsample()) return -1;
         if (aux) {
-            // the bicubic branch from the padded input, its conv; the aux image
-            // and its conv back to features (reference network_swin2sr.py:948-958)
-            const int qh = hp * s, qw = wp * s, Q = qh * qw;
-            if (run("bicubic", dim3((Q + 255) / 256), dim3(256),
-                    [&] { return launch_bicubic4(in4, bic4, hp, wp, qh, qw, stream); }))
-                return -1;
-            g = conv_gemm(bic4, qh, qw, 4, bc_w, bc_b, bicf, feat, feat);
-            if (gemm("conv_bicubic", g, ALOAD_IM2COL, EPI_STORE)) return -1;
+            // the aux image and its conv back to features (reference
+            // network_swin2sr.py:948-958)
             // four output channels, the fourth with zero weights and bias: the
             // aux plane's channel 3, which conv_after_aux reads as zero padding
             g = conv_gemm(fplanes[0], hp, wp, feat, ax_w, ax_b, aux4, 4, 4);
@@ -954,70 +946,84 @@ int s2s_ctx::head(int h, int w, float *d_out) {
         for (int oc = 0; oc < octaves - fused_octaves(); ++oc) {
             g = conv_gemm(fplanes[oc], H, W, feat, up_w[oc], up_b[oc], fplanes[oc + 1], 0, 4 * feat);
             g.feat = feat;
-            if (aux && oc == octaves - 1) g.res = bicf;  // + the bicubic branch
             const std::string nm = "conv3x3_shuffle2_o" + std::to_string(oc);
             if (gemm(nm.c_str(), g, ALOAD_IM2COL, EPI_SHUFFLE)) return -1;
             H *= 2;
             W *= 2;
         }
-        if (fuse2 && up2_wino) {
-            // the last two octaves and conv_last: one 5x5 conv to 48 channels
-            // as Winograd F(2x2,5x5) over the pixels whose outputs survive the
-            // crop (V, then M over it at a row stride of F, in the qkv
-            // buffer), stored through pixel_shuffle(4), denormalised and
-            // cropped by the output transform; then the input row 0 / column 0
-            // outputs recomputed
-            const int Ho = std::min(H, (oh + 3) / 4), Wo = std::min(W, (ow + 3) / 4);
-            const int T = (int)wino5_tiles(Ho, Wo);
-            const float *src = fplanes[octaves - 2];
-            if (run("up2_last_in", dim3(wino5_in_grid(Ho, Wo, feat)), dim3(256),
-                    [&] { return launch_wino5_in(src, feat, qkv, H, W, Ho, Wo, feat, stream); }))
-                return -1;
-            g = rows_gemm(qkv, feat, u2_w, feat, nullptr, qkv, feat, T, 48, feat);
-            g.nb = WINO_POS;
-            g.a_bstride = g.o_bstride = (size_t)T * feat;
-            g.b_packed = bs_packs(48, feat, EPI_STORE);
-            g.b_bstride = weight_floats(48, feat, EPI_STORE);
-            if (gemm("up2_last", g, ALOAD_ROWS, EPI_STORE)) return -1;
-            if (run("up2_last_out", dim3(wino5_finish_grid(Ho, Wo)), dim3(256), [&] {
-                    return launch_wino5_finish(qkv, feat, u2_b, d_out, Ho, Wo, oh, ow, arch.img_range,
-                                               arch.mean, stream);
-                }))
-                return -1;
-            const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
-            return run("up2_last_edge", dim3(nb), dim3(256), [&] {
-                return launch_up2_last_edge(src, u2_we, u2_be, d_out, H, W, feat, oh, ow,
-                                            arch.img_range, arch.mean, stream);
-            });
-        }
-        if (fuse2) {
-            // the last two octaves and conv_last: one 5x5 conv to 48 channels
-            // stored through pixel_shuffle(4), denormalised and cropped, then
-            // the input row 0 / column 0 outputs recomputed
-            g = conv_gemm(fplanes[octaves - 2], H, W, feat, u2_w, u2_b, d_out, 0, 48);
-            g.ldb = 25 * feat;
-            g.K = 25 * feat;
-            // only the rows whose outputs survive the crop (the loader still
-            // reads the rows below them as the footprint needs)
-            g.M = std::min(H, (oh + 3) / 4) * W;
-            g.scale = 4;
-            g.oh = oh;
-            g.ow = ow;
-            g.img_range = arch.img_range;
-            for (int i = 0; i < 3; ++i) g.mean[i] = arch.mean[i];
-            if (gemm("up2_last", g, ALOAD_IM2COL5, EPI_SHUFFLE_FINISH)) return -1;
-            const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
-            return run("up2_last_edge", dim3(nb), dim3(256), [&] {
-                return launch_up2_last_edge(fplanes[octaves - 2], u2_we, u2_be, d_out, H, W, feat,
-                                            oh, ow, arch.img_range, arch.mean, stream);
-            });
-        }
-        if (fuse_last)
+        // the composed tail (the last octaves and conv_last, with the finish),
+        // then for the compressed head its bicubic branch through conv_last,
+        // composed, added into the finished image
+        auto composed = [&]() -> int {
+            if (fuse2 && up2_wino) {
+                // the last two octaves and conv_last: one 5x5 conv to 48 channels
+                // as Winograd F(2x2,5x5) over the pixels whose outputs survive the
+                // crop (V, then M over it at a row stride of F, in the qkv
+                // buffer), stored through pixel_shuffle(4), denormalised and
+                // cropped by the output transform; then the input row 0 / column 0
+                // outputs recomputed
+                const int Ho = std::min(H, (oh + 3) / 4), Wo = std::min(W, (ow + 3) / 4);
+                const int T = (int)wino5_tiles(Ho, Wo);
+                const float *src = fplanes[octaves - 2];
+                if (run("up2_last_in", dim3(wino5_in_grid(Ho, Wo, feat)), dim3(256),
+                        [&] { return launch_wino5_in(src, feat, qkv, H, W, Ho, Wo, feat, stream); }))
+                    return -1;
+                g = rows_gemm(qkv, feat, u2_w, feat, nullptr, qkv, feat, T, 48, feat);
+                g.nb = WINO_POS;
+                g.a_bstride = g.o_bstride = (size_t)T * feat;
+                g.b_packed = bs_packs(48, feat, EPI_STORE);
+                g.b_bstride = weight_floats(48, feat, EPI_STORE);
+                if (gemm("up2_last", g, ALOAD_ROWS, EPI_STORE)) return -1;
+                if (run("up2_last_out", dim3(wino5_finish_grid(Ho, Wo)), dim3(256), [&] {
+                        return launch_wino5_finish(qkv, feat, u2_b, d_out, Ho, Wo, oh, ow, arch.img_range,
+                                                   arch.mean, stream);
+                    }))
+                    return -1;
+                const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
+                return run("up2_last_edge", dim3(nb), dim3(256), [&] {
+                    return launch_up2_last_edge(src, u2_we, u2_be, d_out, H, W, feat, oh, ow,
+                                                arch.img_range, arch.mean, stream);
+                });
+            }
+            if (fuse2) {
+                // the last two octaves and conv_last: one 5x5 conv to 48 channels
+                // stored through pixel_shuffle(4), denormalised and cropped, then
+                // the input row 0 / column 0 outputs recomputed
+                g = conv_gemm(fplanes[octaves - 2], H, W, feat, u2_w, u2_b, d_out, 0, 48);
+                g.ldb = 25 * feat;
+                g.K = 25 * feat;
+                // only the rows whose outputs survive the crop (the loader still
+                // reads the rows below them as the footprint needs)
+                g.M = std::min(H, (oh + 3) / 4) * W;
+                g.scale = 4;
+                g.oh = oh;
+                g.ow = ow;
+                g.img_range = arch.img_range;
+                for (int i = 0; i < 3; ++i) g.mean[i] = arch.mean[i];
+                if (gemm("up2_last", g, ALOAD_IM2COL5, EPI_SHUFFLE_FINISH)) return -1;
+                const int nb = (ow + 3) / 4 + (oh + 3) / 4 - 1;
+                return run("up2_last_edge", dim3(nb), dim3(256), [&] {
+                    return launch_up2_last_edge(fplanes[octaves - 2], u2_we, u2_be, d_out, H, W, feat,
+                                                oh, ow, arch.img_range, arch.mean, stream);
+                });
+            }
             return run("up_last", up_last_grid(oh, ow), dim3(256), [&] {
                 return launch_up_last(fplanes[octaves - 1], ul_w, ul_b, ul_we, ul_be, d_out, H, W,
                                       feat, oh, ow, arch.img_range, arch.mean, stream);
             });
-        return last(fplanes[octaves], H, W);
+        };
+        if (!fuse_last) return last(fplanes[octaves], H, W);
+        if (composed()) return -1;
+        if (!aux) return 0;
+        // the compressed head's bicubic branch: the padded input resampled to
+        // the output grid, then through conv_last o conv_bicubic into the image
+        const int qh = hp * s, qw = wp * s, Q = qh * qw;
+        if (run("bicubic", dim3((Q + 255) / 256), dim3(256),
+                [&] { return launch_bicubic4(in4, bic4, hp, wp, qh, qw, stream); }))
+            return -1;
+        return run("bic_last_add", dim3((ow + 63) / 64, (oh + 3) / 4), dim3(256), [&] {
+            return launch_bic_last_add(bic4, qh, qw, bl_w, bl_b, d_out, oh, ow, arch.img_range, stream);
+        });
     }
     case S2S_PIXELSHUFFLE_DIRECT: {
         // one conv to 3*s^2 channels, stored through pixel_shuffle(s) straight
@@ -1246,6 +1252,43 @@ void compose_up2_last(const std::vector<float> &ue, const std::vector<float> &ub
     b48.assign(B.begin(), B.end());
 }
 
+// The compressed head's bicubic branch through conv_last (reference
+// src/gpu.rs:678-730: conv_last(octaves(x) + conv_bicubic(B))): conv_last
+// (Wl [3][F][3][3], without its bias, which the octaves' composition carries)
+// after conv_bicubic (Wb [F][3][3][3], bb [F]) as one 5x5 conv of the bicubic
+// image B: output (Y, X), channel k reads conv_last's tap (ky, kx) at
+// (Y + ky - 1, X + kx - 1) of conv_bicubic's output, which reads B at a further
+// (dy - 1, dx - 1): tap t = (ky + dy) * 5 + (kx + dx) of the 5x5 footprint.
+// Variant (ey, ex) drops conv_last's kernel row 0 (ey) / column 0 (ex) - with
+// the bias they carry - for output row 0 / column 0, where those taps read
+// conv_last's zero padding. Accumulated in double, rounded once: w [4][25][3][4]
+// (input channel 3 zero), b [4][3].
+void compose_bic_last(const float *Wb, const float *bb, const float *Wl, int F,
+                      std::vector<float> &w, std::vector<float> &b) {
+    std::vector<double> W((size_t)4 * 25 * 3 * 4, 0.0), B(12, 0.0);
+    for (int var = 0; var < 4; ++var) {
+        const bool ey = var >> 1, ex = var & 1;
+        for (int k = 0; k < 3; ++k)
+            for (int ky = 0; ky < 3; ++ky)
+                for (int kx = 0; kx < 3; ++kx) {
+                    if ((ey && ky == 0) || (ex && kx == 0)) continue;
+                    for (int f = 0; f < F; ++f) {
+                        const double wl = Wl[(((size_t)k * F + f) * 3 + ky) * 3 + kx];
+                        B[var * 3 + k] += wl * bb[f];
+                        for (int c = 0; c < 3; ++c)
+                            for (int dy = 0; dy < 3; ++dy)
+                                for (int dx = 0; dx < 3; ++dx) {
+                                    const int t = (ky + dy) * 5 + (kx + dx);
+                                    W[((size_t)(var * 25 + t) * 3 + k) * 4 + c] +=
+                                        wl * Wb[(((size_t)f * 3 + c) * 3 + dy) * 3 + dx];
+                                }
+                    }
+                }
+    }
+    w.assign(W.begin(), W.end());
+    b.assign(B.begin(), B.end());
+}
+
 // The head's feature width: conv_before_upsample's output channels.
 int head_feat_of(const TensorSet &ts, int C, int *F) {
     const s2s_tensor *cb = ts.find("conv_before_upsample.0.weight");
@@ -1308,7 +1351,7 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
         } else {
             const int oct = octaves_of(A.scale);
             f += (uint64_t)oct * (4 * F_ * 9 * F4 + 4 * F_);  // the octave convs
-            if (up == S2S_PIXELSHUFFLE && F % 8 == 0) {
+            if (F % 8 == 0) {
                 if (oct >= 2 && F == 64)     // two octaves and conv_last composed (the
                     f += (wino_up2(oct, F) ? WINO_POS * weight_floats(48, F4, EPI_STORE) : 48 * 25 * F_)  // GEMM's,
                          + 4 * 48 * 25 * F_ + 5 * 48;                           // the edges')
@@ -1316,7 +1359,8 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
                     f += 5 * 12 * 25 * F_ + 5 * 12;  // the last octave and conv_last composed
             }
             if (up == S2S_PIXELSHUFFLE_AUX)
-                f += (F_ * 9 * 4 + F_) + (4 * 9 * F4 + 4) + (F_ * 9 * 4 + F_);  // bicubic, aux, after_aux
+                f += (4 * 25 * 3 * 4 + 12)                     // conv_last o conv_bicubic composed,
+                     + (4 * 9 * F4 + 4) + (F_ * 9 * 4 + F_);  // aux, after_aux
         }
     } else if (up == S2S_PIXELSHUFFLE_DIRECT) {
         const uint64_t n3 = 3 * (uint64_t)A.scale * A.scale;
@@ -1613,9 +1657,11 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             rc = rc || up_before_upsample(F);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
             const std::vector<int> perm = shuffle_perm(F);
-            // the plain pixel-shuffle head composes its last octave with
-            // conv_last (not with the bicubic branch, which is added between)
-            ctx->fuse_last = A.upsampler == S2S_PIXELSHUFFLE && F % 8 == 0;
+            // the head's last octave (two, at x4 and above) composed with
+            // conv_last; the compressed head's bicubic branch, which the
+            // reference adds before conv_last, then goes through its own
+            // composition with conv_last (compose_bic_last)
+            ctx->fuse_last = F % 8 == 0;
             for (int o = 0; !rc && o < oct; ++o) {
                 const s2s_tensor *uw, *ub;
                 const std::string base = "upsample." + std::to_string(2 * o);
@@ -1662,9 +1708,20 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                     }
                 }
             }
+            if (A.upsampler == S2S_PIXELSHUFFLE_AUX && !ctx->fuse_last)
+                rc = rc || fail("internal: the compressed head composes its octaves with conv_last");
+            if (!rc && A.upsampler == S2S_PIXELSHUFFLE_AUX) {
+                const s2s_tensor *bw, *bb, *lw;
+                rc = rc || ts.get("conv_bicubic.weight", {F, 3, 3, 3}, &bw);
+                rc = rc || ts.get("conv_bicubic.bias", {F}, &bb);
+                rc = rc || ts.get("conv_last.weight", {3, F, 3, 3}, &lw);
+                if (!rc) {
+                    std::vector<float> w, b;
+                    compose_bic_last(bw->data, bb->data, lw->data, F, w, b);
+                    rc = ctx->upload(w, &ctx->bl_w) || ctx->upload(b, &ctx->bl_b);
+                }
+            }
             if (A.upsampler == S2S_PIXELSHUFFLE_AUX) {
-                rc = rc || upconv("conv_bicubic.weight", F, 3, &ctx->bc_w, nullptr);
-                rc = rc || up("conv_bicubic.bias", {F}, &ctx->bc_b);
                 // conv_aux with a fourth, zero output row (it writes the aux
                 // plane's zero channel 3 itself)
                 const s2s_tensor *aw, *ab;
@@ -1783,18 +1840,18 @@ int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, fl
         int bhp, bwp, ih, iw;
         bool prof;
         float *cur, *wk, *body, *qkv, *o, *hid, *in_dev, *in4, *out_dev;
-        float *aux4, *auxp, *bic4, *bicf;
+        float *aux4, *auxp, *bic4;
         std::vector<float *> fplanes;
         ~Saved() {
             c->bhp = bhp; c->bwp = bwp; c->ih = ih; c->iw = iw; c->prof = prof;
             c->cur = cur; c->wk = wk; c->body = body; c->qkv = qkv; c->o = o;
             c->hid = hid; c->in_dev = in_dev; c->in4 = in4; c->out_dev = out_dev;
-            c->aux4 = aux4; c->auxp = auxp; c->bic4 = bic4; c->bicf = bicf;
+            c->aux4 = aux4; c->auxp = auxp; c->bic4 = bic4;
             c->fplanes.swap(fplanes);
         }
     } saved{ctx, ctx->bhp, ctx->bwp, ctx->ih, ctx->iw, ctx->prof, ctx->cur, ctx->wk,
             ctx->body, ctx->qkv, ctx->o, ctx->hid, ctx->in_dev, ctx->in4, ctx->out_dev,
-            ctx->aux4, ctx->auxp, ctx->bic4, ctx->bicf, {}};
+            ctx->aux4, ctx->auxp, ctx->bic4, {}};
     saved.fplanes.swap(ctx->fplanes);
 
     std::vector<BufSpec> v;
@@ -1812,7 +1869,6 @@ int s2s_forward_device_noalloc(s2s_ctx *ctx, int h, int w, const float *d_in, fl
         *b.dst = (float *)(base + off);
         off += (std::max<size_t>(b.floats, 1) * sizeof(float) + 255) / 256 * 256;
     }
-    if (ctx->arch.upsampler == S2S_PIXELSHUFFLE_AUX) ctx->bicf = ctx->fplanes[ctx->octaves];
     // the carved plan is the current one for this call (plan_image keeps it)
     ctx->bhp = hp;
     ctx->bwp = wp;

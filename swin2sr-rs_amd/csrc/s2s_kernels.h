@@ -301,6 +301,14 @@ hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float
 // channel-last [h*w][4] plane to [oh*ow][4] (channel 3 stays 0).
 hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,
                            hipStream_t st);
+// The compressed head's bicubic branch through conv_last, added into the
+// finished output: out[k][Y][X] += (bias[v][k] + sum over the 5x5 taps t and
+// the 3 channels c of w[v][t][k][c] * bic[Y + t/5 - 2][X + t%5 - 2][c]) /
+// img_range over the cropped oh x ow image, bic the [qh*qw][4] bicubic plane
+// (zero outside), v = 2 (Y == 0) + (X == 0) the edge variant; weights
+// [4][25][3][4] (c = 3 unused), biases [4][3].
+hipError_t launch_bic_last_add(const float *bic, int qh, int qw, const float *w, const float *bias,
+                               float *out, int oh, int ow, float img_range, hipStream_t st);
 // [P][4] -> planar [3][P], v / img_range + mean (the compressed head's aux image).
 hipError_t launch_aux_finish(const float *in, float *out, int P, float img_range,
                              const float *mean, hipStream_t st);

@@ -2727,6 +2727,75 @@ __global__ void k_bicubic4(const float *__restrict__ in, float *__restrict__ out
     *reinterpret_cast<float4 *>(out + (size_t)i * 4) = make_float4(acc[0], acc[1], acc[2], 0.f);
 }
 
+// The compressed head (reference src/gpu.rs:678-730) adds its bicubic branch,
+// conv_bicubic (3 -> F) of the bicubic-resized input, to the last octave's
+// output just before conv_last; conv_last being linear, conv_last(octaves(x) +
+// Bc) = conv_last(octaves(x)) + conv_last(Bc), and the first term is the
+// classical head's composition (up2_last / up_last). The second is
+// conv_last o conv_bicubic composed on the host into one 5x5 conv from the 3
+// bicubic channels to the 3 outputs (the inner conv's bias folded in), with
+// edge variants for output row 0 / column 0, where conv_last's zero padding
+// drops taps (the bottom and right edges are cropped away). This kernel adds
+// it to the finished output (divided by img_range, the denormalisation's
+// scale), so neither the F-channel bicubic plane (16 P x F floats) nor the
+// octaves' planes exist. A workgroup owns 4 x 64 output pixels (lane = column,
+// wave = row); the 8 x 68 halo of the bicubic plane and the weights sit in
+// LDS; one thread computes the 3 channels of its pixel.
+#define BL_ROWS 4
+#define BL_COLS 64
+__global__ __launch_bounds__(256) void k_bic_last_add(const float *__restrict__ bic, int qh, int qw,
+                                                      const float *__restrict__ wt,
+                                                      const float *__restrict__ bias,
+                                                      float *__restrict__ out, int oh, int ow,
+                                                      float inv_range) {
+    constexpr int HR = BL_ROWS + 4, HC = BL_COLS + 4;
+    constexpr int NW = 4 * 25 * 3 * 4;
+    __shared__ float4 halo[HR * HC];
+    __shared__ float4 ws[NW / 4];
+    __shared__ float bs[12];
+    const int tid = threadIdx.x;
+    const int x0 = blockIdx.x * BL_COLS, y0 = blockIdx.y * BL_ROWS;
+    for (int i = tid; i < NW / 4; i += 256) ws[i] = reinterpret_cast<const float4 *>(wt)[i];
+    if (tid < 12) bs[tid] = bias[tid];
+    for (int i = tid; i < HR * HC; i += 256) {
+        const int r = i / HC, c = i - (i / HC) * HC;
+        const int y = y0 - 2 + r, x = x0 - 2 + c;
+        halo[i] = (y >= 0 && y < qh && x >= 0 && x < qw)
+                      ? *reinterpret_cast<const float4 *>(bic + ((size_t)y * qw + x) * 4)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+    const int lx = tid & 63, ly = tid >> 6;
+    const int X = x0 + lx, Y = y0 + ly;
+    if (X >= ow || Y >= oh) return;
+    const int v = 2 * (Y == 0) + (X == 0);
+    const float4 *w = ws + v * 75;
+    float a0 = bs[3 * v], a1 = bs[3 * v + 1], a2 = bs[3 * v + 2];
+#pragma unroll 5
+    for (int t = 0; t < 25; ++t) {
+        const float4 p = halo[(ly + t / 5) * HC + lx + t % 5];
+        const float4 w0 = w[3 * t], w1 = w[3 * t + 1], w2 = w[3 * t + 2];
+        a0 = fmaf(w0.z, p.z, fmaf(w0.y, p.y, fmaf(w0.x, p.x, a0)));
+        a1 = fmaf(w1.z, p.z, fmaf(w1.y, p.y, fmaf(w1.x, p.x, a1)));
+        a2 = fmaf(w2.z, p.z, fmaf(w2.y, p.y, fmaf(w2.x, p.x, a2)));
+    }
+    const size_t plane = (size_t)oh * ow, o = (size_t)Y * ow + X;
+    out[o] += a0 * inv_range;
+    out[plane + o] += a1 * inv_range;
+    out[2 * plane + o] += a2 * inv_range;
+}
+
+hipError_t launch_bic_last_add(const float *bic, int qh, int qw, const float *w, const float *bias,
+                               float *out, int oh, int ow, float img_range, hipStream_t st) {
+    // every output pixel's 5x5 footprint reads the bicubic plane at offsets
+    // -2..2 (zero outside); the output is the crop of that plane's grid
+    if (oh < 1 || ow < 1 || oh > qh || ow > qw) return hipErrorInvalidValue;
+    const dim3 grid((ow + BL_COLS - 1) / BL_COLS, (oh + BL_ROWS - 1) / BL_ROWS);
+    hipLaunchKernelGGL(k_bic_last_add, grid, dim3(256), 0, st, bic, qh, qw, w, bias, out, oh, ow,
+                       1.0f / img_range);
+    return hipGetLastError();
+}
+
 // reference cpu::finish_aux (src/cpu.rs:1925-1941): the aux image, denormalised,
 // planar at the padded geometry.
 __global__ void k_aux_finish(const float *__restrict__ in, float *__restrict__ out, int P,

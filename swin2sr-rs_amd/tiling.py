@@ -84,8 +84,9 @@ def _unit_layout(arch: M.Arch) -> bool:
 
 
 def _fused_octaves(arch: M.Arch) -> int:
-    """Octaves of the pixel-shuffle head composed into its last kernel."""
-    if arch.upsampler != "pixelshuffle" or arch.feat % 8:
+    """Octaves of the pixel-shuffle heads (the compressed one's too) composed
+    into their last kernel."""
+    if arch.upsampler not in ("pixelshuffle", "pixelshuffle_aux") or arch.feat % 8:
         return 0
     return 2 if arch.octaves >= 2 and arch.feat == 64 else 1
 
