@@ -136,10 +136,12 @@ def kernel_work(arch, h, w, hp=None, wp=None):
     # pixelshuffledirect: one 3x3 conv C -> 3 s^2 stored through pixel_shuffle(s)
     # into the denormalised, cropped image
     work["conv_shuffle_finish"] = ("mfma", 2 * P * 3 * s * s * 9 * C, f * (P * C + 3 * h * s * w * s))
-    # nearest+conv: two nearest-2x steps, each read by the next 3x3 conv's
-    # loader (F -> F at 4P and 16P), then conv_hr at 16P
-    work["conv_up1"] = ("mfma", 2 * 4 * P * F * 9 * F, f * (P * F + 4 * P * F))
-    work["conv_up2"] = ("mfma", 2 * 16 * P * F * 9 * F, f * (4 * P * F + 16 * P * F))
+    # nearest+conv: two nearest-2x steps, each with a 3x3 conv F -> F (to 4P
+    # and 16P pixels) run as the four output phases' 2x2 convs of the plane
+    # before the step (4 taps x F per output instead of 9 x F), then conv_hr
+    # at 16P
+    work["conv_up1"] = ("mfma", 2 * 4 * P * F * 4 * F, f * (P * F + 4 * P * F))
+    work["conv_up2"] = ("mfma", 2 * 16 * P * F * 4 * F, f * (4 * P * F + 16 * P * F))
     work["conv_hr"] = ("mfma", 2 * 16 * P * F * 9 * F, f * 2 * 16 * P * F)
     # pixelshuffle_aux: conv_aux F -> 3, conv_after_aux 3 -> F, the aux image's
     # denormalisation; the bicubic resample of the padded input to s x the

@@ -339,6 +339,15 @@ int s2s_test_conv3x3_winograd(int h, int w, int c_in, int c_out, const float *x,
                               const float *bias, int epilogue, const float *res, float slope,
                               float *out);
 
+/* The real-world head's conv_up1 / conv_up2 (reference src/gpu.rs:641-669:
+ * nearest-2x upsampling, conv3x3 c -> c, LeakyReLU(slope)) as the forward
+ * runs them: the four 2x2 convs of the plane itself, one per output phase,
+ * whose weights are sums of the 3x3 taps that land on the same plane pixel.
+ * Channel-last `[h*w][c]` in, weights `[c][c][3][3]`, channel-last
+ * `[(2h)*(2w)][c]` out; c a multiple of 4. */
+int s2s_test_conv3x3_nearest2(int h, int w, int c, const float *x, const float *wgt,
+                              const float *bias, float slope, float *out);
+
 /* The head's fused conv3x3 + pixel_shuffle(2) (reference cpu::conv3x3_shuffle2,
  * src/cpu.rs:502-542): weights `[4*feat][c_in][3][3]`, output channel-last
  * `[(2h)*(2w)][feat]`. */

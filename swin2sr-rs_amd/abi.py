@@ -87,6 +87,7 @@ EXPORTS = {
     "s2s_test_conv3x3_winograd": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP,
                                             C.c_int, FP, C.c_float, FP]),
     "s2s_test_conv3x3_shuffle2": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, FP]),
+    "s2s_test_conv3x3_nearest2": (C.c_int, [C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_float, FP]),
 }
 
 
@@ -403,6 +404,18 @@ def test_conv3x3(x_hwc, h, w, wgt, bias, epilogue=0, res=None, slope=0.0):
     c32 = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
     check(lib.s2s_test_conv3x3(h, w, cin, cout, fptr(c32(x_hwc)), fptr(c32(wgt)), fptr(c32(bias)),
                                epilogue, fptr(c32(res)), slope, fptr(out)), "s2s_test_conv3x3")
+    return out
+
+
+def test_conv3x3_nearest2(x_hwc, h, w, wgt, bias, slope):
+    """conv3x3 (c -> c) + LeakyReLU of the nearest-2x upsampling of an h x w
+    plane, as the four phases' 2x2 convs the real-world head runs."""
+    lib = load_library()
+    c = wgt.shape[0]
+    out = np.empty((4 * h * w, c), np.float32)
+    c32 = lambda a: np.ascontiguousarray(a, np.float32)
+    check(lib.s2s_test_conv3x3_nearest2(h, w, c, fptr(c32(x_hwc)), fptr(c32(wgt)), fptr(c32(bias)),
+                                        slope, fptr(out)), "s2s_test_conv3x3_nearest2")
     return out
 
 

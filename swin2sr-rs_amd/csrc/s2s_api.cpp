@@ -676,6 +676,17 @@ GemmArgs conv_gemm(const float *in, int H, int W, int cin, const float *wt, cons
     return g;
 }
 
+// A 3x3 conv (F -> F) of the nearest-2x upsampling of the H x W plane `in`
+// into the 2H x 2W plane `out`, as the ALOAD_SUB2 GEMM over its four phases
+// (weights from subpixel_weights).
+GemmArgs sub2_gemm(const float *in, int H, int W, int F, const float *wt, const float *bias,
+                   float *out) {
+    GemmArgs g = conv_gemm(in, H, W, F, wt, bias, out, F, F);
+    g.ldb = 4 * F;
+    g.K = 4 * F;
+    return g;
+}
+
 }  // namespace
 
 // One post-norm Swin V2 block (reference src/gpu.rs:485-522), x_in -> x_out
@@ -1039,12 +1050,12 @@ int s2s_ctx::head(int h, int w, float *d_out) {
     case S2S_NEAREST_CONV: {
         if (before_upsample()) return -1;
         // two nearest-2x steps, each read by the next conv's operand loader
-        g = conv_gemm(fplanes[0], 2 * hp, 2 * wp, feat, nu1_w, nu1_b, fplanes[1], feat, feat);
+        g = sub2_gemm(fplanes[0], hp, wp, feat, nu1_w, nu1_b, fplanes[1]);
         g.slope = 0.2f;
-        if (gemm("conv_up1", g, ALOAD_IM2COL_UP2, EPI_LRELU)) return -1;
-        g = conv_gemm(fplanes[1], 4 * hp, 4 * wp, feat, nu2_w, nu2_b, fplanes[2], feat, feat);
+        if (gemm("conv_up1", g, ALOAD_SUB2, EPI_LRELU)) return -1;
+        g = sub2_gemm(fplanes[1], 2 * hp, 2 * wp, feat, nu2_w, nu2_b, fplanes[2]);
         g.slope = 0.2f;
-        if (gemm("conv_up2", g, ALOAD_IM2COL_UP2, EPI_LRELU)) return -1;
+        if (gemm("conv_up2", g, ALOAD_SUB2, EPI_LRELU)) return -1;
         g = conv_gemm(fplanes[2], 4 * hp, 4 * wp, feat, hr_w, hr_b, fplanes[3], feat, feat);
         g.slope = 0.2f;
         if (gemm("conv_hr", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
@@ -1347,7 +1358,7 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
         f += (wino_head(A.embed, F) ? WINO_POS * weight_floats(F, C4, EPI_STORE) : F_ * 9 * C4) + F_;
         f += 9 * F_ * 3 + 3;            // conv_last
         if (up == S2S_NEAREST_CONV) {
-            f += 3 * (F_ * 9 * F4 + F_);  // conv_up1, conv_up2, conv_hr
+            f += 2 * (4 * F_ * 4 * F4 + F_) + (F_ * 9 * F4 + F_);  // conv_up1, conv_up2 (by phase), conv_hr
         } else {
             const int oct = octaves_of(A.scale);
             f += (uint64_t)oct * (4 * F_ * 9 * F4 + 4 * F_);  // the octave convs
@@ -1437,6 +1448,13 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                       const std::vector<int> *perm) -> int {
         if (ts.get(name, {co, ci, 3, 3}, &x)) return -1;
         return ctx->upload(conv_relayout(x->data, co, ci, perm), dst);
+    };
+    // a conv of a nearest-2x upsampling [F][F][3][3], as its four phases' 2x2 convs
+    auto up_sub2 = [&](const std::string &name, int F, float **dst) -> int {
+        if (ts.get(name, {F, F, 3, 3}, &x)) return -1;
+        std::vector<float> w((size_t)16 * F * round4(F));
+        subpixel_weights(x->data, F, F, w.data());
+        return ctx->upload(w, dst);
     };
     // conv_before_upsample [F][C][3][3]: the Winograd transform [36][F][C]
     // when wino_head takes it, else the implicit GEMM's layout
@@ -1751,9 +1769,9 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
             const int F = ctx->feat;
             rc = rc || up_before_upsample(F);
             rc = rc || up("conv_before_upsample.0.bias", {F}, &ctx->cbu_b);
-            rc = rc || upconv("conv_up1.weight", F, F, &ctx->nu1_w, nullptr);
+            rc = rc || up_sub2("conv_up1.weight", F, &ctx->nu1_w);
             rc = rc || up("conv_up1.bias", {F}, &ctx->nu1_b);
-            rc = rc || upconv("conv_up2.weight", F, F, &ctx->nu2_w, nullptr);
+            rc = rc || up_sub2("conv_up2.weight", F, &ctx->nu2_w);
             rc = rc || up("conv_up2.bias", {F}, &ctx->nu2_b);
             rc = rc || upconv("conv_hr.weight", F, F, &ctx->hr_w, nullptr);
             rc = rc || up("conv_hr.bias", {F}, &ctx->hr_b);

@@ -9,7 +9,13 @@ enum {
     ALOAD_ROWS = 0,       // A[m*lda + k]
     ALOAD_IM2COL = 1,     // 3x3 im2col of the channel-last H x W plane A[H*W][cin]
     ALOAD_IM2COL_UP2 = 2, // 3x3 im2col of the nearest-2x upsampling of A[(H/2)*(W/2)][cin]
-    ALOAD_IM2COL5 = 3     // 5x5 im2col of the channel-last H x W plane (k = tap*cin + ci)
+    ALOAD_IM2COL5 = 3,    // 5x5 im2col of the channel-last H x W plane (k = tap*cin + ci)
+    ALOAD_SUB2 = 4        // a 3x3 conv of the nearest-2x upsampling of the H x W plane A,
+                          // as four 2x2 convs of A, one per output phase (a, b): row m =
+                          // (y, x) of A, k = tap*cin + ci with tap (i, j) reading A at
+                          // (y + a - 1 + i, x + b - 1 + j); B = [4 phases][N][ldb]; the
+                          // epilogue stores output pixel (2y + a, 2x + b) of the 2H x 2W
+                          // plane. One launch covers the four phases.
 };
 enum {
     EPI_STORE = 0,   // out = acc + bias
@@ -297,6 +303,9 @@ hipError_t launch_up_last(const float *in, const float *wt, const float *bias, c
 hipError_t launch_up2_last_edge(const float *in, const float *wedge, const float *bedge, float *out,
                                int H, int W, int feat, int oh, int ow, float img_range,
                                const float *mean, hipStream_t st);
+// The four phases' 2x2 weights of a 3x3 conv w [co][ci][3][3] applied to a
+// nearest-2x upsampling (ALOAD_SUB2's B): [4][co][4][ci_pad4] at out.
+void subpixel_weights(const float *w, int co, int ci, float *out);
 // torch's bicubic resize (a = -0.75, align_corners = False, edge clamp) of a
 // channel-last [h*w][4] plane to [oh*ow][4] (channel 3 stays 0).
 hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,

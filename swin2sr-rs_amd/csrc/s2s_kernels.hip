@@ -164,9 +164,13 @@ __device__ __forceinline__ float gelu_erf(float v) {
 template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     static_assert(WM * WN == 4, "four wavefronts");
-    // IM2COL and IM2COL5 share the loader: a (2 RAD + 1)^2 footprint
-    constexpr bool IC = ALOAD == ALOAD_IM2COL || ALOAD == ALOAD_IM2COL5;
+    // IM2COL, IM2COL5 and SUB2 share the loader: an FS x FS footprint whose
+    // first tap is at (oy, ox) from the row's pixel: (-RAD, -RAD) for the
+    // centred 3x3 and 5x5, (a - 1, b - 1) for SUB2's phase (a, b)
+    constexpr bool SUB2 = ALOAD == ALOAD_SUB2;
+    constexpr bool IC = ALOAD == ALOAD_IM2COL || ALOAD == ALOAD_IM2COL5 || SUB2;
     constexpr int RAD = ALOAD == ALOAD_IM2COL5 ? 2 : 1;
+    constexpr int FS = SUB2 ? 2 : 2 * RAD + 1;
     constexpr int WTM = MT / WM / 32;
     constexpr int WTN = NT / WN / 32;
     static_assert(WTM * WM * 32 == MT && WTN * WN * 32 == NT, "tile shape");
@@ -190,9 +194,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // hardware's round-robin order over a 2-D grid every column tile pass and
     // every XCD re-read the whole plane from memory.
     const int ntn = (g.N + NT - 1) / NT;
-    const int ntiles = ((g.M + MT - 1) / MT) * ntn;
+    // SUB2: the four phases' tiles one after another (each phase's tiles
+    // contiguous, so an XCD's resident tiles share their rows of A)
+    const int ntp = ((g.M + MT - 1) / MT) * ntn;
+    const int ntiles = SUB2 ? 4 * ntp : ntp;
     const int xcd = blockIdx.x & 7;
-    const int lin = xcd * (ntiles >> 3) + min(xcd, ntiles & 7) + (int)(blockIdx.x >> 3);
+    int lin = xcd * (ntiles >> 3) + min(xcd, ntiles & 7) + (int)(blockIdx.x >> 3);
+    const int phase = SUB2 ? lin / ntp : 0;
+    lin -= phase * ntp;
+    const int oy = SUB2 ? (phase >> 1) - 1 : -RAD, ox = SUB2 ? (phase & 1) - 1 : -RAD;
+    if (SUB2) g.B += (size_t)phase * g.N * g.ldb;
     const int m0 = (lin / ntn) * MT;
     const int n0 = (lin - (lin / ntn) * ntn) * NT;
     const int lr = lane & 31;
@@ -241,10 +252,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         const int n = n0 + tid / KQ + KRP * i;
         bo[i] = n < g.N ? (n * g.ldb + kq) * 4 : -1;
     }
-    // IM2COL(5): each of the thread's rows as a byte offset from the resource
-    // base, and a mask of the taps (bit (2 RAD + 1)(dy + RAD) + dx + RAD) that read inside
-    // the plane (none for rows past M); a chunk then costs an add, a bit test
-    // and a select per row instead of the bounds checks and a multiply
+    // IM2COL(5), SUB2: each of the thread's rows as a byte offset from the
+    // resource base, and a mask of the taps (bit FS ty + tx for the tap at
+    // (oy + ty, ox + tx)) that read inside the plane (none for rows past M);
+    // a chunk then costs an add, a bit test and a select per row instead of
+    // the bounds checks and a multiply
     int aro[AV];
     unsigned tmask[AV];
     if (IC) {
@@ -254,12 +266,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             unsigned msk = 0;
             if (am[i] < g.M) {
 #pragma unroll
-                for (int ty = 0; ty < 2 * RAD + 1; ++ty)
+                for (int ty = 0; ty < FS; ++ty)
 #pragma unroll
-                    for (int tx = 0; tx < 2 * RAD + 1; ++tx)
-                        if ((unsigned)(ay[i] + ty - RAD) < (unsigned)g.H &&
-                            (unsigned)(ax[i] + tx - RAD) < (unsigned)g.W)
-                            msk |= 1u << ((2 * RAD + 1) * ty + tx);
+                    for (int tx = 0; tx < FS; ++tx)
+                        if ((unsigned)(ay[i] + oy + ty) < (unsigned)g.H &&
+                            (unsigned)(ax[i] + ox + tx) < (unsigned)g.W)
+                            msk |= 1u << (FS * ty + tx);
             }
             tmask[i] = msk;
         }
@@ -267,18 +279,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // (tap, ci) of k = k0 + kq for the chunk at k0, and the tap's shift; for
     // IM2COL also tapoff = ((dy * W + dx) * cin + ci) * 4, the byte offset of
     // that element from its row's pixel (unchanged when ci wraps into the
-    // next tap of the same kernel row; + (W - 3) * cin * 4 into the next row)
-    int tap = 0, ci = kq, dy = -RAD, dx = -RAD;
-    int tapoff = IC ? ((-RAD * g.W - RAD) * g.cin + kq) * 4 : 0;
+    // next tap of the same kernel row; + (W - FS) * cin * 4 into the next row)
+    int tap = 0, ci = kq, dy = oy, dx = ox;
+    int tapoff = IC ? ((oy * g.W + ox) * g.cin + kq) * 4 : 0;
     auto norm_k = [&]() __attribute__((always_inline)) {
         if (ALOAD == ALOAD_ROWS) return;
         while (ci >= g.cin) {
             ci -= g.cin;
             ++tap;
-            if (++dx > RAD) {
-                dx = -RAD;
+            if (++dx >= ox + FS) {
+                dx = ox;
                 ++dy;
-                tapoff += (g.W - 2 * RAD - 1) * g.cin * 4;
+                tapoff += (g.W - FS) * g.cin * 4;
             }
         }
     };
@@ -286,7 +298,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 
     auto load_chunk = [&](int k0) __attribute__((always_inline)) {
         const bool kok = k0 + kq < g.K;
-        // (tap < (2 RAD + 1)^2 <= 25 while k < K; bit 31 of a tap mask is never set)
+        // (tap < FS^2 <= 25 while k < K; bit 31 of a tap mask is never set)
         const int tsel = kok ? tap : 31;
 #pragma unroll
         for (int i = 0; i < AV; ++i) {
@@ -498,6 +510,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                     const int oy = g.scale * y + dy, ox = g.scale * x + dx;
                     if (oy < g.oh && ox < g.ow)
                         g.out[((size_t)c * g.oh + oy) * g.ow + ox] = v / g.img_range + g.mean[c];
+                } else if (SUB2) {
+                    // output pixel (2y + a, 2x + b) of the 2H x 2W plane
+                    const int y = m / g.W;
+                    const int x = m - y * g.W;
+                    const size_t px = (size_t)(2 * y + (phase >> 1)) * (2 * g.W) + 2 * x + (phase & 1);
+                    g.out[px * g.ldo + n] = v;
                 } else {
                     g.out[(size_t)m * g.ldo + n] = v;
                 }
@@ -2863,8 +2881,8 @@ __global__ void k_cpb_gather(const float *__restrict__ tab, float *__restrict__ 
 
 template <int MT, int NT, int WM, int WN, int ALOAD, int EPI>
 static hipError_t run_gemm_t(const GemmArgs &g, hipStream_t st) {
-    // one workgroup per tile, in k_gemm's XCD-aware order
-    const dim3 grid((unsigned)(((g.M + MT - 1) / MT) * ((g.N + NT - 1) / NT)));
+    // one workgroup per tile (per phase for SUB2), in k_gemm's XCD-aware order
+    const dim3 grid((unsigned)(((g.M + MT - 1) / MT) * ((g.N + NT - 1) / NT) * (ALOAD == ALOAD_SUB2 ? 4 : 1)));
     hipLaunchKernelGGL((k_gemm<MT, NT, WM, WN, ALOAD, EPI>), grid, dim3(256), 0, st, g);
     return hipGetLastError();
 }
@@ -2876,7 +2894,7 @@ static const int kVariants[GEMM_NVARIANTS][4] = {
 
 template <int MT, int NT, int WM, int WN, int ALOAD>
 static hipError_t run_gemm_e(const GemmArgs &g, int epi, hipStream_t st) {
-    if constexpr (ALOAD == ALOAD_IM2COL_UP2) {
+    if constexpr (ALOAD == ALOAD_IM2COL_UP2 || ALOAD == ALOAD_SUB2) {
         // the real-world head's conv_up1 / conv_up2 (+ LeakyReLU 0.2)
         if (epi == EPI_LRELU) return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
         return hipErrorInvalidValue;
@@ -2913,13 +2931,14 @@ static hipError_t run_gemm_v(const GemmArgs &g, int aload, int epi, hipStream_t 
     case ALOAD_IM2COL: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL>(g, epi, st);
     case ALOAD_IM2COL_UP2: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL_UP2>(g, epi, st);
     case ALOAD_IM2COL5: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL5>(g, epi, st);
+    case ALOAD_SUB2: return run_gemm_e<MT, NT, WM, WN, ALOAD_SUB2>(g, epi, st);
     default: return hipErrorInvalidValue;
     }
 }
 
 const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
     (void)g;
-    static const char *names[4][9] = {
+    static const char *names[5][9] = {
         {"gemm_rows_store", "gemm_rows_gelu", "gemm_rows_res", "gemm_rows_ln", "gemm_rows_ln_res",
          "gemm_rows_lrelu", "gemm_rows_shuffle", "gemm_rows_shuffle_finish", "gemm_rows_qkv_win"},
         {"conv3x3_store", "conv3x3_gelu", "conv3x3_res", "conv3x3_ln", "conv3x3_ln_res",
@@ -2928,8 +2947,10 @@ const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
          "conv3x3_up2_ln_res", "conv3x3_up2_lrelu", "conv3x3_up2_shuffle",
          "conv3x3_up2_shuffle_finish", "conv3x3_up2_qkv_win"},
         {"conv5x5_store", "conv5x5_gelu", "conv5x5_res", "conv5x5_ln", "conv5x5_ln_res",
-         "conv5x5_lrelu", "conv5x5_shuffle", "conv5x5_shuffle_finish", "conv5x5_qkv_win"}};
-    if (aload < 0 || aload > 3 || epi < 0 || epi > 8) return "gemm_unknown";
+         "conv5x5_lrelu", "conv5x5_shuffle", "conv5x5_shuffle_finish", "conv5x5_qkv_win"},
+        {"conv_sub2_store", "conv_sub2_gelu", "conv_sub2_res", "conv_sub2_ln", "conv_sub2_ln_res",
+         "conv_sub2_lrelu", "conv_sub2_shuffle", "conv_sub2_shuffle_finish", "conv_sub2_qkv_win"}};
+    if (aload < 0 || aload > 4 || epi < 0 || epi > 8) return "gemm_unknown";
     return names[aload][epi];
 }
 
@@ -2956,6 +2977,7 @@ void gemm_variant_grid(const GemmArgs &g, int variant, unsigned *gx, unsigned *g
 
 void gemm_grid(const GemmArgs &g, int aload, int epi, unsigned *gx, unsigned *gy) {
     gemm_variant_grid(g, gemm_pick(g, aload, epi), gx, gy);
+    if (aload == ALOAD_SUB2) *gx *= 4;  // the four phases
 }
 
 hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int variant,
@@ -3778,6 +3800,40 @@ void wino_weights(const float *w, int co, int ci, float *out) {
                     out[((size_t)(6 * xi + nu) * co + o) * cp + i] = (float)u;
                 }
         }
+}
+
+// A 3x3 conv (w [co][ci][3][3]) of the nearest-2x upsampling of a plane, as
+// the four 2x2 convs of the plane itself that the ALOAD_SUB2 GEMM runs, one
+// per output phase (a, b) (reference src/gpu.rs:641-669, the real-world head's
+// conv_up1 / conv_up2: nearest upsampling, then the conv). Output row
+// 2y + a, tap ky reads upsampled row 2y + a + ky - 1, i.e. plane row
+// floor((2y + a + ky - 1) / 2) = y + a - 1 + i with i = 0 for ky in S(a, 0)
+// and 1 for ky in S(a, 1): S(0, 0) = {0}, S(0, 1) = {1, 2}, S(1, 0) = {0, 1},
+// S(1, 1) = {2}; the same for the columns. The phase's 2x2 weights are the
+// sums of the 3x3 taps that land on the same plane pixel (in double, rounded
+// once); the upsampled plane's zero padding is the plane's. Layout [4 phases]
+// [co][4 taps (i, j)][ci_pad4], k = tap * ci_pad4 + ci: 16 co ci_pad4 floats at out.
+void subpixel_weights(const float *w, int co, int ci, float *out) {
+    const int cp = (ci + 3) / 4 * 4;
+    std::fill(out, out + (size_t)4 * co * 4 * cp, 0.f);
+    // whether tap k (0..2) of the 3x3 lands on tap i (0..1) of phase a's 2x2
+    auto in_set = [](int a, int i, int k) {
+        return a == 0 ? (i == 0 ? k == 0 : k >= 1) : (i == 0 ? k <= 1 : k == 2);
+    };
+    for (int ph = 0; ph < 4; ++ph) {
+        const int a = ph >> 1, b = ph & 1;
+        for (int o = 0; o < co; ++o)
+            for (int c = 0; c < ci; ++c)
+                for (int i = 0; i < 2; ++i)
+                    for (int j = 0; j < 2; ++j) {
+                        double sum = 0.0;
+                        for (int ky = 0; ky < 3; ++ky)
+                            for (int kx = 0; kx < 3; ++kx)
+                                if (in_set(a, i, ky) && in_set(b, j, kx))
+                                    sum += w[(((size_t)o * ci + c) * 3 + ky) * 3 + kx];
+                        out[(((size_t)ph * co + o) * 4 + 2 * i + j) * cp + c] = (float)sum;
+                    }
+    }
 }
 
 hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, int ow,

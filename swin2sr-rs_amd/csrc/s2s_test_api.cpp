@@ -487,4 +487,34 @@ int s2s_test_conv3x3_shuffle2(int h, int w, int c_in, int feat, const float *x,
     return 0;
 }
 
+int s2s_test_conv3x3_nearest2(int h, int w, int c, const float *x, const float *wgt,
+                              const float *bias, float slope, float *out) {
+    if (h < 1 || w < 1 || c < 4 || c % 4) return fail("s2s_test_conv3x3_nearest2: bad shape");
+    const size_t P = (size_t)h * w;
+    std::vector<float> wt((size_t)16 * c * c);
+    subpixel_weights(wgt, c, c, wt.data());
+    Dev d;
+    GemmArgs g{};
+    g.A = d.up(x, P * c);
+    g.H = h;
+    g.W = w;
+    g.cin = c;
+    g.B = d.up(wt.data(), wt.size());
+    g.ldb = 4 * c;
+    g.bias = d.up(bias, c);
+    float *dout = d.alloc<float>(4 * P * c);
+    g.out = dout;
+    g.ldo = c;
+    g.M = (int)P;
+    g.N = c;
+    g.K = 4 * c;
+    g.slope = slope;
+    if (!g.A || !g.B || !g.bias || !dout) return fail("hipMalloc failed: out of memory");
+    hipError_t e = launch_gemm(g, ALOAD_SUB2, EPI_LRELU, 0);
+    if (int rc = finish(e, "k_gemm(conv_sub2)")) return rc;
+    if (hipMemcpy(out, dout, 4 * P * c * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail("hipMemcpy failed");
+    return 0;
+}
+
 }  // extern "C"

@@ -310,6 +310,25 @@ def test_conv3x3_shuffle2(pkg, orc, cin, feat, h, w):
     assert err < 5e-5, err
 
 
+@pytest.mark.parametrize("c,h,w", [(4, 1, 1), (4, 3, 5), (8, 7, 2), (64, 9, 70), (64, 33, 17),
+                                   (64, 122, 162)])
+def test_conv3x3_nearest2(pkg, orc, c, h, w):
+    """The real-world head's conv of a nearest-2x upsampling (conv_up1 /
+    conv_up2, + LeakyReLU 0.2) as the device runs it, four phases of 2x2 convs
+    of the plane, against the oracle's nearest upsampling (reference
+    cpu::upsample2x_nearest) then its direct conv3x3, LeakyReLU in numpy; every
+    border (the upsampled plane's zero padding is the plane's) included."""
+    r = rng(c * 131 + h * w)
+    x = r.standard_normal((c, h, w), dtype=np.float32)
+    wt = (r.standard_normal((c, c, 3, 3), dtype=np.float32) / np.sqrt(9 * c)).astype(np.float32)
+    b = r.standard_normal(c, dtype=np.float32)
+    z = orc.conv3x3(orc.upsample2x_nearest(x), wt, b)
+    want = np.where(z < 0, z * np.float32(0.2), z)
+    got = pkg.abi.test_conv3x3_nearest2(nchw_to_hwc(x), h, w, wt, b, 0.2)
+    err = np.abs(hwc_to_nchw(got, 2 * h, 2 * w) - want).max()
+    assert err < 5e-5, err
+
+
 def _forward_pair(pkg, orc, arch, seed, h, w, perturb=True):
     M = pkg.model
     wts = M.make_weights(arch, seed=seed, perturb=perturb)
