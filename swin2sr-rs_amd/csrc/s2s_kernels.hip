@@ -2460,20 +2460,24 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
 // with cpu::finish (src/cpu.rs:1925-1941) as k_conv_last_finish is.
 //
 // VALU, as k_conv_last_finish (12 outputs would fill 3/4 of an MFMA tile): a
-// workgroup owns an 8 x 64 tile of input pixels, lane = column, wave w = rows
-// 2w, 2w + 1, 24 accumulators per lane; the 12 x 68 halo and the chunk's
-// weights move through LDS 8 channels at a time, double-buffered, the weights
-// read as broadcast float4s (one tap, 4 channels, 12 outputs). Only pixels
-// whose outputs survive the crop are computed.
-#define UL_ROWS 8
+// workgroup owns a 4 RPW x 64 tile of input pixels, lane = column, wave w =
+// rows RPW w .. RPW w + RPW - 1, 12 RPW accumulators per lane; the halo and
+// the chunk's weights move through LDS 8 channels at a time, double-buffered,
+// the weights read as broadcast float4s (one tap, 4 channels, 12 outputs),
+// each serving the wave's RPW rows. RPW = 2 (8-row tiles) where that still
+// gives two workgroups per CU, else 1 (a 256^2 input at x2 has 128 8-row
+// tiles: half the CUs idle). Only pixels whose outputs survive the crop are
+// computed.
 #define UL_COLS 64
 #define UL_CC 8
+template <int RPW>
 __global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in,
                                                     const float *__restrict__ wt,
                                                     const float *__restrict__ bias,
                                                     float *__restrict__ out, int H, int W,
                                                     int feat, int oh, int ow, float inv_range,
                                                     float m0, float m1, float m2) {
+    constexpr int UL_ROWS = 4 * RPW;
     constexpr int TH = UL_ROWS + 4, TW = UL_COLS + 4;
     constexpr int Q = UL_CC / 4;               // float4s per pixel per chunk
     constexpr int NV = TH * TW * Q;
@@ -2535,9 +2539,9 @@ __global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in
         }
     };
 
-    float acc[2][12];
+    float acc[RPW][12];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr)
+    for (int rr = 0; rr < RPW; ++rr)
 #pragma unroll
         for (int s = 0; s < 12; ++s) acc[rr][s] = bias[s];
     load(0);
@@ -2548,8 +2552,8 @@ __global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in
         const float4 *t = tile[k & 1];
         const float4 *ws = wsh[k & 1];
         // one tap and 4 channels at a time: their 48 weights (12 broadcast
-        // float4 reads) serve the wave's 2 rows (the tap loop stays rolled, so
-        // only one tap's operands are live)
+        // float4 reads) serve the wave's RPW rows (the tap loop stays rolled,
+        // so only one tap's operands are live)
 #pragma unroll 1
         for (int tap = 0; tap < 25; ++tap) {
             const int ty = tap / 5, tx = tap - 5 * (tap / 5);
@@ -2565,8 +2569,8 @@ __global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in
                     wk[4 * f + 3] = w4.w;
                 }
 #pragma unroll
-                for (int rr = 0; rr < 2; ++rr) {
-                    const float4 v = t[((2 * wave + rr + ty) * TW + lane + tx) * Q + qq];
+                for (int rr = 0; rr < RPW; ++rr) {
+                    const float4 v = t[((RPW * wave + rr + ty) * TW + lane + tx) * Q + qq];
                     const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc)
@@ -2587,8 +2591,8 @@ __global__ __launch_bounds__(256, 2) void k_up_last(const float *__restrict__ in
     const size_t plane = (size_t)oh * ow;
     const float mk[3] = {m0, m1, m2};
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-        const int y = y0 + 2 * wave + rr;
+    for (int rr = 0; rr < RPW; ++rr) {
+        const int y = y0 + RPW * wave + rr;
         if (2 * y >= oh) break;
 #pragma unroll
         for (int sy = 0; sy < 2; ++sy)
@@ -3374,8 +3378,15 @@ hipError_t launch_conv_last_finish(const float *in, const float *wt, const float
     return hipGetLastError();
 }
 
+// rows per wave of k_up_last: 2 while 8-row tiles give two workgroups per CU
+static int up_last_rpw(int oh, int ow) {
+    const long long tiles8 = (long long)((ow / 2 + UL_COLS - 1) / UL_COLS) * ((oh / 2 + 7) / 8);
+    return tiles8 >= 2LL * cu_count() ? 2 : 1;
+}
+
 dim3 up_last_grid(int oh, int ow) {
-    return dim3((ow / 2 + UL_COLS - 1) / UL_COLS, (oh / 2 + UL_ROWS - 1) / UL_ROWS);
+    const int rows = 4 * up_last_rpw(oh, ow);
+    return dim3((ow / 2 + UL_COLS - 1) / UL_COLS, (oh / 2 + rows - 1) / rows);
 }
 
 hipError_t launch_up_last(const float *in, const float *wt, const float *bias, const float *wedge,
@@ -3385,7 +3396,8 @@ hipError_t launch_up_last(const float *in, const float *wt, const float *bias, c
     // every computed input pixel inside the plane
     if (feat % UL_CC || oh % 2 || ow % 2 || oh / 2 > H || ow / 2 > W) return hipErrorInvalidValue;
     const float ir = 1.0f / img_range;
-    hipLaunchKernelGGL(k_up_last, up_last_grid(oh, ow), dim3(256), 0, st, in, wt, bias, out, H, W,
+    hipLaunchKernelGGL(up_last_rpw(oh, ow) == 2 ? k_up_last<2> : k_up_last<1>, up_last_grid(oh, ow),
+                       dim3(256), 0, st, in, wt, bias, out, H, W,
                        feat, oh, ow, ir, mean[0], mean[1], mean[2]);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -357,13 +357,15 @@ def test_forward_small_model(pkg, orc, h, w):
     assert d8 <= 1
 
 
-@pytest.mark.parametrize("scale,h,w", [(2, 13, 21), (4, 9, 11), (8, 9, 11)])
+@pytest.mark.parametrize("scale,h,w", [(2, 13, 21), (4, 9, 11), (8, 9, 11), (2, 520, 520)])
 def test_pixelshuffle_head_compositions(pkg, orc, scale, h, w):
     """The classical head's composed last stage at every octave count: x2 runs
     the last octave and conv_last composed (k_up_last), x4 the last two octaves
     (the 5x5 conv GEMM through pixel_shuffle(4)), x8 one ordinary octave before
     those two; each with its top-row / left-column edge pass, on images small
-    enough that the edges are a large part of the output."""
+    enough that the edges are a large part of the output. x2 also at 520^2,
+    where k_up_last takes its 8-row tiles (4-row tiles below 2 workgroups per
+    CU)."""
     M = pkg.model
     arch = M.Arch(upsampler="pixelshuffle", scale=scale, embed=24, heads=2, depths=[1])
     want, got, got2 = _forward_pair(pkg, orc, arch, 5 + scale, h, w, perturb=True)
