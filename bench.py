@@ -143,14 +143,14 @@ def kernel_work(arch, h, w, hp=None, wp=None):
     work["conv_up1"] = ("mfma", 2 * 4 * P * F * 4 * F, f * (P * F + 4 * P * F))
     work["conv_up2"] = ("mfma", 2 * 16 * P * F * 4 * F, f * (4 * P * F + 16 * P * F))
     work["conv_hr"] = ("mfma", 2 * 16 * P * F * 9 * F, f * 2 * 16 * P * F)
-    # pixelshuffle_aux: conv_aux F -> 3, conv_after_aux 3 -> F, the aux image's
-    # denormalisation; the bicubic resample of the padded input to s x the
-    # plane (4 channels)
+    # pixelshuffle_aux: conv_aux F -> 3 on the VALU with the aux image's
+    # denormalisation (the plane in, the aux plane and image out),
+    # conv_after_aux 3 -> F; the bicubic resample of the padded input to s x
+    # the plane (4 channels)
     Q = (hp * s) * (wp * s)
     work["bicubic"] = ("hbm", 0, f * (4 * P + 4 * Q))
-    work["conv_aux"] = ("mfma", 2 * P * 3 * 9 * F, f * (P * F + 4 * P))
+    work["conv_aux"] = ("valu", 2 * P * 3 * 9 * F, f * (P * F + 4 * P + 3 * P))
     work["conv_after_aux"] = ("mfma", 2 * P * F * 27, f * (4 * P + P * F))
-    work["aux_finish"] = ("hbm", 0, f * (4 * P + 3 * P))
     # ... and its bicubic branch through conv_last, composed: a 5x5 conv of the
     # 3 bicubic channels to the 3 outputs over the cropped image (VALU), added
     # into it (the bicubic plane read, the image read and written)

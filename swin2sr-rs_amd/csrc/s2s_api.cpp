@@ -915,7 +915,6 @@ int s2s_ctx::forward_launches(int h, int w, const float *d_in, float *d_out) {
 int s2s_ctx::head(int h, int w, float *d_out) {
     const int win = arch.window, s = arch.scale;
     const int hp = (h / win + 1) * win, wp = (w / win + 1) * win;
-    const int P = hp * wp;
     const int oh = h * s, ow = w * s;
     GemmArgs g{};
     // conv_before_upsample + LeakyReLU(0.01) into the first feature plane
@@ -941,17 +940,18 @@ int s2s_ctx::head(int h, int w, float *d_out) {
         if (aux) {
             // the aux image and its conv back to features (reference
             // network_swin2sr.py:948-958)
-            // four output channels, the fourth with zero weights and bias: the
-            // aux plane's channel 3, which conv_after_aux reads as zero padding
-            g = conv_gemm(fplanes[0], hp, wp, feat, ax_w, ax_b, aux4, 4, 4);
-            if (gemm("conv_aux", g, ALOAD_IM2COL, EPI_STORE)) return -1;
+            // conv_aux (feat -> 3) on the VALU with the aux image's finish: the
+            // conv's output to the aux plane (its channel 3 zero, which
+            // conv_after_aux reads as zero padding) and the denormalised aux
+            // image (an N = 3 GEMM would use 3 of its 64 columns)
+            if (run("conv_aux", conv_last_grid(hp, wp), dim3(256), [&] {
+                    return launch_conv_aux(fplanes[0], ax_w, ax_b, aux4, auxp, hp, wp, feat,
+                                           arch.img_range, arch.mean, stream);
+                }))
+                return -1;
             g = conv_gemm(aux4, hp, wp, 4, caa_w, caa_b, fplanes[0], feat, feat);
             g.slope = 0.01f;
             if (gemm("conv_after_aux", g, ALOAD_IM2COL, EPI_LRELU)) return -1;
-            if (run("aux_finish", dim3((P + 255) / 256), dim3(256), [&] {
-                    return launch_aux_finish(aux4, auxp, P, arch.img_range, arch.mean, stream);
-                }))
-                return -1;
         }
         int H = hp, W = wp;
         for (int oc = 0; oc < octaves - fused_octaves(); ++oc) {
@@ -1371,7 +1371,7 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
             }
             if (up == S2S_PIXELSHUFFLE_AUX)
                 f += (4 * 25 * 3 * 4 + 12)                     // conv_last o conv_bicubic composed,
-                     + (4 * 9 * F4 + 4) + (F_ * 9 * 4 + F_);  // aux, after_aux
+                     + (9 * F_ * 3 + 3) + (F_ * 9 * 4 + F_);  // aux, after_aux
         }
     } else if (up == S2S_PIXELSHUFFLE_DIRECT) {
         const uint64_t n3 = 3 * (uint64_t)A.scale * A.scale;
@@ -1740,18 +1740,18 @@ int s2s_create(const s2s_arch *arch, const s2s_tensor *tensors, size_t n_tensors
                 }
             }
             if (A.upsampler == S2S_PIXELSHUFFLE_AUX) {
-                // conv_aux with a fourth, zero output row (it writes the aux
-                // plane's zero channel 3 itself)
-                const s2s_tensor *aw, *ab;
+                // conv_aux in conv_last's layout [tap][ci][3] (the same kernel)
+                const s2s_tensor *aw;
                 rc = rc || ts.get("conv_aux.weight", {3, F, 3, 3}, &aw);
-                rc = rc || ts.get("conv_aux.bias", {3}, &ab);
                 if (!rc) {
-                    std::vector<float> w4 = conv_relayout(aw->data, 3, F, nullptr);
-                    w4.resize((size_t)4 * 9 * round4(F), 0.f);
-                    std::vector<float> b4(ab->data, ab->data + 3);
-                    b4.push_back(0.f);
-                    rc = ctx->upload(w4, &ctx->ax_w) || ctx->upload(b4, &ctx->ax_b);
+                    std::vector<float> t((size_t)9 * F * 3);
+                    for (int co = 0; co < 3; ++co)
+                        for (int ci = 0; ci < F; ++ci)
+                            for (int tap = 0; tap < 9; ++tap)
+                                t[((size_t)tap * F + ci) * 3 + co] = aw->data[((size_t)co * F + ci) * 9 + tap];
+                    rc = ctx->upload(t, &ctx->ax_w);
                 }
+                rc = rc || up("conv_aux.bias", {3}, &ctx->ax_b);
                 rc = rc || upconv("conv_after_aux.0.weight", F, 3, &ctx->caa_w, nullptr);
                 rc = rc || up("conv_after_aux.0.bias", {F}, &ctx->caa_b);
             }

@@ -318,9 +318,13 @@ hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, in
 // [4][25][3][4] (c = 3 unused), biases [4][3].
 hipError_t launch_bic_last_add(const float *bic, int qh, int qw, const float *w, const float *bias,
                                float *out, int oh, int ow, float img_range, hipStream_t st);
-// [P][4] -> planar [3][P], v / img_range + mean (the compressed head's aux image).
-hipError_t launch_aux_finish(const float *in, float *out, int P, float img_range,
-                             const float *mean, hipStream_t st);
+// The compressed head's conv_aux (feat -> 3, 3x3, zero pad; weights [tap][ci][3]
+// as conv_last's) over the H x W plane with cpu::finish_aux: the conv's output
+// to aux4 [H*W][4] (channel 3 zero) and the aux image v / img_range + mean to
+// auxp [3][H][W].
+hipError_t launch_conv_aux(const float *in, const float *wt, const float *bias, float *aux4,
+                           float *auxp, int H, int W, int feat, float img_range, const float *mean,
+                           hipStream_t st);
 hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *tab, float *cpbt,
                       int win, int heads, hipStream_t st);
 hipError_t launch_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *reg,

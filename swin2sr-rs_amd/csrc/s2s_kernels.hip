@@ -2325,16 +2325,24 @@ __global__ __launch_bounds__(256, 2) void k_embed(const float *__restrict__ in4,
 // while this one is multiplied. The chunk's weights (layout [tap][ci][3])
 // travel with it into LDS and are read as broadcast float4s, 12 at a time (one
 // tap, 4 channels), for the wave's 4 output rows.
+//
+// AUX: the compressed head's conv_aux (feat -> 3 on the padded plane,
+// reference src/gpu.rs:703-706) with cpu::finish_aux: over the whole H x W
+// plane (oh = H, ow = W), the conv's output to aux4 [H*W][4] (channel 3 zero,
+// which conv_after_aux reads as zero padding) and the aux image
+// v / img_range + mean to out [3][H][W].
 #define CL_ROWS 16
 #define CL_COLS 64
 #define CL_CC 8
+template <bool AUX>
 __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__restrict__ in,
                                                              const float *__restrict__ wt,
                                                              const float *__restrict__ bias,
                                                              float *__restrict__ out, int H, int W,
                                                              int feat, int oh, int ow,
                                                              float inv_range, float m0, float m1,
-                                                             float m2) {
+                                                             float m2, float *__restrict__ aux4,
+                                                             float img_range) {
     constexpr int TH = CL_ROWS + 2, TW = CL_COLS + 2;
     constexpr int Q = CL_CC / 4;                 // float4s per pixel per chunk
     constexpr int NV = TH * TW * Q;
@@ -2441,9 +2449,16 @@ __global__ __launch_bounds__(256, 2) void k_conv_last_finish(const float *__rest
         const int y = y0 + 4 * wave + rr;
         if (y >= oh) break;
         const size_t o = (size_t)y * ow + x;
-        out[o] = acc[rr][0] * inv_range + m0;
-        out[plane + o] = acc[rr][1] * inv_range + m1;
-        out[2 * plane + o] = acc[rr][2] * inv_range + m2;
+        if (AUX) {
+            *reinterpret_cast<float4 *>(aux4 + o * 4) = make_float4(acc[rr][0], acc[rr][1], acc[rr][2], 0.f);
+            out[o] = acc[rr][0] / img_range + m0;
+            out[plane + o] = acc[rr][1] / img_range + m1;
+            out[2 * plane + o] = acc[rr][2] / img_range + m2;
+        } else {
+            out[o] = acc[rr][0] * inv_range + m0;
+            out[plane + o] = acc[rr][1] * inv_range + m1;
+            out[2 * plane + o] = acc[rr][2] * inv_range + m2;
+        }
     }
 }
 
@@ -2816,18 +2831,6 @@ hipError_t launch_bic_last_add(const float *bic, int qh, int qw, const float *w,
     hipLaunchKernelGGL(k_bic_last_add, grid, dim3(256), 0, st, bic, qh, qw, w, bias, out, oh, ow,
                        1.0f / img_range);
     return hipGetLastError();
-}
-
-// reference cpu::finish_aux (src/cpu.rs:1925-1941): the aux image, denormalised,
-// planar at the padded geometry.
-__global__ void k_aux_finish(const float *__restrict__ in, float *__restrict__ out, int P,
-                             float img_range, float m0, float m1, float m2) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= P) return;
-    const float4 v = *reinterpret_cast<const float4 *>(in + (size_t)i * 4);
-    out[i] = v.x / img_range + m0;
-    out[(size_t)P + i] = v.y / img_range + m1;
-    out[2 * (size_t)P + i] = v.z / img_range + m2;
 }
 
 // The continuous position bias table (reference tools/convert.py:141-167 and
@@ -3373,8 +3376,18 @@ hipError_t launch_conv_last_finish(const float *in, const float *wt, const float
                                    float img_range, const float *mean, hipStream_t st) {
     if (feat % CL_CC) return hipErrorInvalidValue;
     const dim3 grid = conv_last_grid(oh, ow);
-    hipLaunchKernelGGL(k_conv_last_finish, grid, dim3(256), 0, st, in, wt, bias, out, H, W, feat,
-                       oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2]);
+    hipLaunchKernelGGL(k_conv_last_finish<false>, grid, dim3(256), 0, st, in, wt, bias, out, H, W,
+                       feat, oh, ow, 1.0f / img_range, mean[0], mean[1], mean[2], nullptr, img_range);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_aux(const float *in, const float *wt, const float *bias, float *aux4,
+                           float *auxp, int H, int W, int feat, float img_range, const float *mean,
+                           hipStream_t st) {
+    if (feat % CL_CC) return hipErrorInvalidValue;
+    const dim3 grid = conv_last_grid(H, W);
+    hipLaunchKernelGGL(k_conv_last_finish<true>, grid, dim3(256), 0, st, in, wt, bias, auxp, H, W,
+                       feat, H, W, 1.0f / img_range, mean[0], mean[1], mean[2], aux4, img_range);
     return hipGetLastError();
 }
 
@@ -3852,13 +3865,6 @@ hipError_t launch_bicubic4(const float *in, float *out, int h, int w, int oh, in
                            hipStream_t st) {
     const int n = oh * ow;
     hipLaunchKernelGGL(k_bicubic4, dim3((n + 255) / 256), dim3(256), 0, st, in, out, h, w, oh, ow);
-    return hipGetLastError();
-}
-
-hipError_t launch_aux_finish(const float *in, float *out, int P, float img_range,
-                             const float *mean, hipStream_t st) {
-    hipLaunchKernelGGL(k_aux_finish, dim3((P + 255) / 256), dim3(256), 0, st, in, out, P,
-                       img_range, mean[0], mean[1], mean[2]);
     return hipGetLastError();
 }
 
