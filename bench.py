@@ -430,6 +430,38 @@ def bench_image(args, pkg, name):
         sys.exit(1)
     log(f"bench: replayed output equals the eager forward's bit for bit (sha256 {digest})")
 
+    # serving figure, reported beside `value` (which stays the one-image rate):
+    # the same image twice per step through s2s_forward_device_batch, the two
+    # alternating between the context's stream and its second lane, so one
+    # image's kernel boundaries overlap the other's kernels; both outputs
+    # checked against the one-image output bit for bit
+    lanes = None
+    if args.lanes:
+        din2 = hip.DeviceBuffer.from_array(x)
+        douts = [hip.DeviceBuffer(3 * h * s * w * s) for _ in range(2)]
+        ins, outs = [din.ptr, din2.ptr], [d.ptr for d in douts]
+        for _ in range(3):  # eager, captured per lane, replayed
+            be.forward_device_batch(h, w, ins, outs)
+        hip.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            be.forward_device_batch(h, w, ins, outs)
+        hip.synchronize()
+        lane_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        ok = all(np.array_equal(d.download(shape), out) for d in douts)
+        for b in [din2] + douts:
+            b.free()
+        if not ok:
+            log("bench: FAILED: a two-lane output differs from the one-image forward's")
+            be.close()
+            sys.exit(1)
+        lanes = {"images_per_step": 2, "ms_per_step": round(lane_ms, 4),
+                 "ms_per_image": round(lane_ms / 2, 4),
+                 "mpix_s": round(2 * (h * s) * (w * s) / 1e3 / lane_ms, 4),
+                 "outputs_equal_one_image_forward": True}
+        log(f"bench: two lanes (s2s_forward_device_batch, 2 images per step): {lane_ms:.3f} ms per "
+            f"step, {lanes['mpix_s']:.3f} output Mpix/s")
+
     win = arch.window
     result = {
         "metric": METRIC if headline else f"output Mpix/s {label} fp32 @1 GPU",
@@ -447,6 +479,8 @@ def bench_image(args, pkg, name):
         "kernel_timing": TIMING_NOTE,
         "output_check": {"replay_equals_eager": True, "sha256_16": digest},
     }
+    if lanes:
+        result["two_lane_serving"] = lanes
     if headline:
         # the crate's own boundary hands over host slices: s2s_forward uploads
         # the input, runs, downloads the output (PCIe included); reported, never
@@ -614,6 +648,9 @@ def main():
                          "single-RSTB micro-bench; lightweight-x2, classical-x2, realworld-x4: "
                          "configs 0, 2, 3 whole-image; compressed-x4-tiled: config 4; "
                          "copy-ceiling: the runtime's device copy at several sizes")
+    ap.add_argument("--lanes", type=int, default=1, choices=[0, 1],
+                    help="also time two images per step through the two-lane batched entry "
+                         "(reported as two_lane_serving; value stays the one-image rate)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="before the warm-up, one device-to-device copy of this many MiB: the "
                          "plain copy kernel of known size that scales rocprofv3's FETCH_SIZE / "

@@ -147,6 +147,22 @@ int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out
  * `s2s_forward` runs this pass on its own device copies. */
 int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_out);
 
+/* `n` images of one size on device-resident buffers (`d_in[i]`, `d_out[i]` as
+ * for `s2s_forward_device`), alternating between the context's stream and a
+ * second lane the context makes on first use: a stream of its own, buffer
+ * plans of its own (a second `s2s_plan_bytes` worth of device memory, kept
+ * until `s2s_destroy`) and graphs of its own, over the same uploaded weights.
+ * One image's kernel boundaries (each launch's start and its last, partial
+ * round, where CUs idle) then overlap the other's kernels. No reference
+ * counterpart (the crate forwards one image at a time): it is the serving
+ * entry, for callers with several images in HBM. The lane starts after the
+ * work already on the context's stream, and the context's stream waits for
+ * the lane, so `s2s_stream` / `s2s_sync` order the whole batch; not
+ * synchronised on return. Each output equals `s2s_forward_device`'s for its
+ * input bit for bit. */
+int s2s_forward_device_batch(s2s_ctx *ctx, int n, int h, int w, const float *const *d_in,
+                             float *const *d_out);
+
 /* `s2s_forward_device` without allocating anything: every intermediate
  * buffer is carved out of a static device workspace of 256 MiB per GPU
  * (a file-scope array the library holds on each GPU it runs on until the

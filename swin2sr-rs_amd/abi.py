@@ -56,6 +56,8 @@ EXPORTS = {
     "s2s_selftest": (C.c_int, [C.POINTER(Arch_), C.POINTER(Tensor_), C.c_size_t]),
     "s2s_forward": (C.c_int, [C.c_void_p, C.c_int, C.c_int, FP, FP]),
     "s2s_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "s2s_forward_device_batch": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                           C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
     "s2s_forward_device_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                              C.c_void_p]),
     "s2s_aux": (C.c_int, [C.c_void_p, C.POINTER(FP), C.POINTER(C.c_size_t)]),
@@ -216,6 +218,16 @@ class HipBackend:
     def forward_device(self, h: int, w: int, d_in: int, d_out: int):
         check(self._lib.s2s_forward_device(self._ctx, h, w, C.c_void_p(d_in), C.c_void_p(d_out)),
               "s2s_forward_device")
+
+    def forward_device_batch(self, h: int, w: int, d_ins, d_outs):
+        """n images of one size (device pointers), over the context's stream
+        and its second lane; ordered on the context's stream."""
+        n = len(d_ins)
+        assert len(d_outs) == n
+        ins = (C.c_void_p * max(n, 1))(*[C.c_void_p(p) for p in d_ins])
+        outs = (C.c_void_p * max(n, 1))(*[C.c_void_p(p) for p in d_outs])
+        check(self._lib.s2s_forward_device_batch(self._ctx, n, h, w, ins, outs),
+              "s2s_forward_device_batch")
 
     def forward_device_noalloc(self, h: int, w: int, d_in: int, d_out: int):
         """The forward on the library's static per-GPU workspace (no allocation)."""

@@ -185,13 +185,15 @@ struct s2s_ctx {
     // SWIN2SR_HIP_ALLOC_LIMIT at s2s_create, or s2s_set_alloc_limit
     uint64_t alloc_limit = 0;
 
-    // The device forward as a HIP graph: the second time in a row that the
-    // same call comes (image size, input and output pointers, buffer plan),
-    // its launches are captured into a graph, which is then replayed while the
-    // same call keeps coming (about 1.6 us less per kernel than stream
-    // launches on MI355X); any other call launches eagerly. Off while
-    // profiling, for s2s_forward_device_noalloc, while a caller captures the
-    // context's stream itself, and with SWIN2SR_HIP_GRAPHS=0.
+    // The device forward as HIP graphs: the second time a call comes (image
+    // size, input and output pointers, buffer plan) among the last few seen,
+    // its launches are captured into a graph, which is replayed whenever that
+    // call comes again (about 1.6 us less per kernel than stream launches on
+    // MI355X); a call seen once launches eagerly. Up to kGraphs graphs are
+    // kept, the least recently used replaced first (so a tiled image's few
+    // crop shapes, or a lane's alternating images, each keep theirs). Off
+    // while profiling, for s2s_forward_device_noalloc, while a caller captures
+    // the context's stream itself, and with SWIN2SR_HIP_GRAPHS=0.
     struct GraphKey {
         int h = 0, w = 0;
         const float *in = nullptr;
@@ -201,11 +203,19 @@ struct s2s_ctx {
             return h == k.h && w == k.w && in == k.in && out == k.out && plan == k.plan;
         }
     };
+    static constexpr size_t kGraphs = 4;
+    struct GraphEntry {
+        GraphKey key;
+        hipGraphExec_t exec = nullptr;
+        uint64_t used = 0;
+    };
     bool graphs = true;
     uint64_t plan_gen = 1;  // bumped whenever a plan's buffers change
-    GraphKey seen{}, gkey{};
-    hipGraphExec_t gexec = nullptr;
+    std::vector<GraphKey> seen;       // calls seen once, oldest first (at most kGraphs)
+    std::vector<GraphEntry> gcache;   // captured calls (at most kGraphs)
+    uint64_t gtick = 0;
     void drop_graph();
+    void drop_graph_entry(size_t i);
 
     bool prof = false;
     std::string prof_only;  // bracket only launches of this name ("" = all)
@@ -214,6 +224,14 @@ struct s2s_ctx {
     std::map<ProfKey, ProfRow> rows;
 
     std::vector<float> aux_host;
+
+    // A second execution lane for s2s_forward_device_batch: its own stream,
+    // buffer plans and graphs over this context's weights (made on first
+    // use; it owns none of the weights), and the events that fork it off this
+    // context's stream and join it back.
+    s2s_ctx *lane = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    int make_lane();
 
     ~s2s_ctx();
     int upload(const std::vector<float> &host, float **dev);
@@ -323,19 +341,26 @@ void free_list(AllocList &l) {
 
 }  // namespace
 
-// The exec graph's last launch may still be queued on the stream: HIP does not
+// An exec graph's last launch may still be queued on the stream: HIP does not
 // promise to defer the destruction of an exec graph in flight, so the stream
-// drains first (this runs only when a graph is replaced or a plan changes).
+// drains first (this runs only when a graph is evicted or a plan changes).
+void s2s_ctx::drop_graph_entry(size_t i) {
+    if (stream) (void)hipStreamSynchronize(stream);
+    (void)hipGraphExecDestroy(gcache[i].exec);
+    gcache.erase(gcache.begin() + (long)i);
+}
+
 void s2s_ctx::drop_graph() {
-    if (gexec) {
-        if (stream) (void)hipStreamSynchronize(stream);
-        (void)hipGraphExecDestroy(gexec);
-    }
-    gexec = nullptr;
-    gkey = GraphKey{};
+    if (!gcache.empty() && stream) (void)hipStreamSynchronize(stream);
+    for (GraphEntry &e : gcache) (void)hipGraphExecDestroy(e.exec);
+    gcache.clear();
+    seen.clear();
 }
 
 s2s_ctx::~s2s_ctx() {
+    delete lane;  // (its own stream drained, its plans freed; the weights are ours)
+    if (fork_ev) (void)hipEventDestroy(fork_ev);
+    if (join_ev) (void)hipEventDestroy(join_ev);
     if (stream) (void)hipStreamSynchronize(stream);
     drop_graph();
     for (auto &p : pending) {
@@ -349,6 +374,47 @@ s2s_ctx::~s2s_ctx() {
     if (pin_in) (void)hipHostFree(pin_in);
     if (pin_out) (void)hipHostFree(pin_out);
     if (stream) (void)hipStreamDestroy(stream);
+}
+
+// The lane: a copy of this context's weights, architecture and switches, with
+// every resource the context owns taken out (the weights' allocation list,
+// plans, staging, graphs, profiler state) and a stream of its own.
+int s2s_ctx::make_lane() {
+    if (lane) return 0;
+    s2s_ctx *L = new s2s_ctx(*this);
+    L->weight_allocs = AllocList{};
+    L->body_allocs = AllocList{};
+    L->head_allocs = AllocList{};
+    L->bhp = L->bwp = L->ih = L->iw = 0;
+    L->cur = L->wk = L->body = L->qkv = L->o = L->hid = nullptr;
+    L->in_dev = L->in4 = L->out_dev = nullptr;
+    L->fplanes.clear();
+    L->aux4 = L->auxp = L->bic4 = nullptr;
+    L->pin_in = L->pin_out = nullptr;
+    L->pin_in_floats = L->pin_out_floats = 0;
+    L->plan_gen = 1;
+    L->seen.clear();
+    L->gcache.clear();
+    L->gtick = 0;
+    L->prof = false;
+    L->prof_only.clear();
+    L->pending.clear();
+    L->free_events.clear();
+    L->rows.clear();
+    L->aux_host.clear();
+    L->lane = nullptr;
+    L->fork_ev = L->join_ev = nullptr;
+    L->stream = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking);
+    if (e == hipSuccess && !fork_ev) e = hipEventCreateWithFlags(&fork_ev, hipEventDisableTiming);
+    if (e == hipSuccess && !join_ev) e = hipEventCreateWithFlags(&join_ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        delete L;
+        return fail(hip_msg("s2s_forward_device_batch: the second lane", e));
+    }
+    lane = L;
+    return 0;
 }
 
 int s2s_ctx::upload(const std::vector<float> &host, float **dev) {
@@ -851,17 +917,28 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out, bool 
     }
     if (!may_graph || prof || !graphs) return forward_launches(h, w, d_in, d_out);
     const GraphKey k{h, w, d_in, d_out, plan_gen};
-    if (gexec && k == gkey) {
-        HIPCHK("hipGraphLaunch", hipGraphLaunch(gexec, stream));
-        return 0;
-    }
-    if (!(k == seen)) {
-        seen = k;
+    for (GraphEntry &e : gcache)
+        if (e.key == k) {
+            e.used = ++gtick;
+            HIPCHK("hipGraphLaunch", hipGraphLaunch(e.exec, stream));
+            return 0;
+        }
+    const auto sk = std::find(seen.begin(), seen.end(), k);
+    if (sk == seen.end()) {
+        if (seen.size() >= kGraphs) seen.erase(seen.begin());
+        seen.push_back(k);
         return forward_launches(h, w, d_in, d_out);
     }
-    // the same call twice in a row: capture its launches (nothing runs while
-    // capturing), then launch the graph
-    drop_graph();
+    // the call's second sighting: capture its launches (nothing runs while
+    // capturing), then launch the graph; the least recently used graph makes
+    // room
+    seen.erase(sk);
+    if (gcache.size() >= kGraphs) {
+        size_t lru = 0;
+        for (size_t i = 1; i < gcache.size(); ++i)
+            if (gcache[i].used < gcache[lru].used) lru = i;
+        drop_graph_entry(lru);
+    }
     HIPCHK("hipStreamBeginCapture", hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     const int rc = forward_launches(h, w, d_in, d_out);
     hipGraph_t gr = nullptr;
@@ -871,17 +948,18 @@ int s2s_ctx::forward_device(int h, int w, const float *d_in, float *d_out, bool 
         (void)hipGetLastError();
         return rc ? rc : fail(hip_msg("hipStreamEndCapture", ec));
     }
-    const hipError_t ei = hipGraphInstantiate(&gexec, gr, nullptr, nullptr, 0);
+    hipGraphExec_t ex = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
     (void)hipGraphDestroy(gr);
     if (ei != hipSuccess) {
-        // no graph on this context from now on: the same launches, eagerly
-        gexec = nullptr;
+        // no graphs on this context from now on: the same launches, eagerly
         graphs = false;
         (void)hipGetLastError();
+        drop_graph();
         return forward_launches(h, w, d_in, d_out);
     }
-    gkey = k;
-    HIPCHK("hipGraphLaunch", hipGraphLaunch(gexec, stream));
+    gcache.push_back(GraphEntry{k, ex, ++gtick});
+    HIPCHK("hipGraphLaunch", hipGraphLaunch(ex, stream));
     return 0;
 }
 
@@ -1825,6 +1903,7 @@ int s2s_plan_bytes(s2s_ctx *ctx, int h, int w, uint64_t *bytes) {
 int s2s_set_alloc_limit(s2s_ctx *ctx, uint64_t bytes) {
     if (!ctx) return fail("null context");
     ctx->alloc_limit = bytes;
+    if (ctx->lane) ctx->lane->alloc_limit = bytes;
     return 0;
 }
 
@@ -1836,6 +1915,35 @@ int s2s_forward_device(s2s_ctx *ctx, int h, int w, const float *d_in, float *d_o
     if (!ctx) return fail("null context");
     HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
     return ctx->forward_device(h, w, d_in, d_out);
+}
+
+// n independent images of one size, alternating between the context's stream
+// and a second lane's (its own stream, plans and graphs over the same
+// weights), so that one image's kernel boundaries (each launch's start and
+// tail, which leave CUs idle) overlap the other's kernels. The lane waits for
+// the work already on the context's stream and the context's stream then
+// waits for the lane, so ordering and synchronisation through s2s_stream /
+// s2s_sync stay as for s2s_forward_device.
+int s2s_forward_device_batch(s2s_ctx *ctx, int n, int h, int w, const float *const *d_in,
+                             float *const *d_out) {
+    if (!ctx || n < 0 || (n > 0 && (!d_in || !d_out)))
+        return fail("s2s_forward_device_batch: null argument");
+    for (int i = 0; i < n; ++i)
+        if (!d_in[i] || !d_out[i]) return fail("s2s_forward_device_batch: null image pointer");
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    if (n <= 1) return n == 1 ? ctx->forward_device(h, w, d_in[0], d_out[0]) : 0;
+    if (ctx->make_lane()) return -1;
+    s2s_ctx *L = ctx->lane;
+    HIPCHK("hipEventRecord(fork)", hipEventRecord(ctx->fork_ev, ctx->stream));
+    HIPCHK("hipStreamWaitEvent(fork)", hipStreamWaitEvent(L->stream, ctx->fork_ev, 0));
+    int rc = 0;
+    for (int i = 0; i < n && !rc; ++i) rc = ((i & 1) ? L : ctx)->forward_device(h, w, d_in[i], d_out[i]);
+    // joined after a failure too, so that whatever the lane launched is covered
+    hipError_t e = hipEventRecord(ctx->join_ev, L->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(hip_msg("s2s_forward_device_batch: joining the lane", e));
+    return 0;
 }
 
 // The forward with every intermediate buffer carved out of this GPU's static

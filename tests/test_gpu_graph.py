@@ -171,11 +171,12 @@ def _async_copy(hip, stream, dst, src, nbytes):
 
 
 def test_graph_replaced_while_a_replay_is_in_flight(pkg):
-    """Calls A, A, A, B, B, A (two input/output pairs of one size) enqueued
-    with no synchronisation between them: the third A is a replay still queued
-    when the second B captures a new graph and the library destroys A's. Each
-    call's output, snapshotted by a copy ordered on the stream right after it,
-    equals the eager context's bit for bit."""
+    """Calls A, A, A, B, B, A and then six calls' pairs each twice (input/output
+    pairs of one size) enqueued with no synchronisation between them: the
+    context keeps four graphs, so captures past the fourth evict the least
+    recently used one while replays are still queued. Each call's output,
+    snapshotted by a copy ordered on the stream right after it, equals the
+    eager context's bit for bit."""
     M, hip = pkg.model, pkg.hip
     arch = M.classical(4)
     wts = M.make_weights(arch, seed=8, perturb=True)
@@ -190,8 +191,12 @@ def test_graph_replaced_while_a_replay_is_in_flight(pkg):
         want = {"A": eager.forward(h, w, xa), "B": eager.forward(h, w, xb)}
         pairs = {"A": (hip.DeviceBuffer.from_array(xa), hip.DeviceBuffer(n_out)),
                  "B": (hip.DeviceBuffer.from_array(xb), hip.DeviceBuffer(n_out))}
+        for i, k in enumerate("CDEFGH"):
+            xk = M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=13 + i)))
+            want[k] = eager.forward(h, w, xk)
+            pairs[k] = (hip.DeviceBuffer.from_array(xk), hip.DeviceBuffer(n_out))
         bufs = [b for p in pairs.values() for b in p]
-        seq = ["A", "A", "A", "B", "B", "A"]
+        seq = ["A", "A", "A", "B", "B", "A"] + [k for k in "CDEFGH" for _ in range(2)] + ["A", "H", "A", "A"]
         snaps = [hip.DeviceBuffer(n_out) for _ in seq]
         bufs += snaps
         st = graph.stream()
