@@ -130,6 +130,20 @@ int s2s_set_alloc_limit(s2s_ctx *ctx, uint64_t bytes);
  * download has completed. */
 int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out);
 
+/* `n` host images through `s2s_forward`'s path (sizes may differ: a tiled
+ * image's crops), alternating between the context and the second lane of
+ * `s2s_forward_device_batch` and pipelined, so that one lane computes while
+ * the other's image is downloaded and copied out. `in_adjusted[i]`, `out[i]`
+ * as for `s2s_forward` with `h[i]`, `w[i]`; `aux_out` may be NULL, or hold per
+ * image a NULL or a caller-owned `[3][hp][wp]` buffer that receives that
+ * image's aux image (the compressed head's; `s2s_aux` afterwards returns the
+ * last image's). No reference counterpart: it is what a tile loop calls with a
+ * whole image's tiles (reference `run_tiled`, src/backend.rs:92-165, calls
+ * `Backend::forward` once per tile); each result equals `s2s_forward`'s for
+ * its input bit for bit. Synchronous: returns when every output is written. */
+int s2s_forward_batch(s2s_ctx *ctx, int n, const int *h, const int *w, const float *const *in_adjusted,
+                      float *const *out, float *const *aux_out);
+
 /* The same pass on device-resident buffers (no host copies): `d_in` is a
  * device `[3][h][w]` mean-adjusted plane, `d_out` a device
  * `[3][h*scale][w*scale]` buffer. Enqueued on the context's stream and NOT

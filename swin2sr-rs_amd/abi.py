@@ -56,6 +56,9 @@ EXPORTS = {
     "s2s_selftest": (C.c_int, [C.POINTER(Arch_), C.POINTER(Tensor_), C.c_size_t]),
     "s2s_forward": (C.c_int, [C.c_void_p, C.c_int, C.c_int, FP, FP]),
     "s2s_forward_device": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "s2s_forward_batch": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                    C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                    C.POINTER(C.c_void_p)]),
     "s2s_forward_device_batch": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int,
                                            C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
     "s2s_forward_device_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p,
@@ -214,6 +217,31 @@ class HipBackend:
         assert out.shape == (3, h * s, w * s) and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
         check(self._lib.s2s_forward(self._ctx, h, w, fptr(x), fptr(out)), "s2s_forward")
         return out
+
+    def forward_batch(self, shapes, inputs, aux=False):
+        """`forward` over several images (a tiled image's crops) at once, on the
+        context's two lanes: a list of new output images, and with `aux` a list
+        of each image's aux image (None where the head makes none)."""
+        n = len(inputs)
+        s = self.arch.scale
+        xs = [np.ascontiguousarray(x, dtype=np.float32) for x in inputs]
+        for (h, w), x in zip(shapes, xs):
+            assert x.shape == (3, h, w), x.shape
+        outs = [np.empty((3, h * s, w * s), np.float32) for h, w in shapes]
+        win = self.arch.window
+        has_aux = aux and self.arch.upsampler == "pixelshuffle_aux"
+        auxs = ([np.empty((3, (h // win + 1) * win, (w // win + 1) * win), np.float32) for h, w in shapes]
+                if has_aux else None)
+        vp = lambda a: C.c_void_p(a.ctypes.data)
+        hs = (C.c_int * max(n, 1))(*[h for h, _ in shapes])
+        ws = (C.c_int * max(n, 1))(*[w for _, w in shapes])
+        ins = (C.c_void_p * max(n, 1))(*[vp(x) for x in xs])
+        os_ = (C.c_void_p * max(n, 1))(*[vp(o) for o in outs])
+        ax = (C.c_void_p * max(n, 1))(*[vp(a) for a in auxs]) if has_aux else None
+        check(self._lib.s2s_forward_batch(self._ctx, n, hs, ws, ins, os_, ax), "s2s_forward_batch")
+        if aux:
+            return outs, (auxs if has_aux else [None] * n)
+        return outs
 
     def forward_device(self, h: int, w: int, d_in: int, d_out: int):
         check(self._lib.s2s_forward_device(self._ctx, h, w, C.c_void_p(d_in), C.c_void_p(d_out)),

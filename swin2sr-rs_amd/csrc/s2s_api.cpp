@@ -2053,59 +2053,137 @@ static void copy_out(float *dst, const float *src, size_t n) {
 // pinned staging image and uploaded as one DMA; the output comes back in
 // chunks, each copied out of the pinned image while the next is still in
 // flight, so the host copy overlaps the link.
-int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out) {
-    if (!ctx || !in_adjusted || !out) return fail("s2s_forward: null argument");
-    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
-    if (h < ctx->arch.window || w < ctx->arch.window) return ctx->forward_device(h, w, nullptr, nullptr);
+// One image through the host path, in two halves so that a batch can keep two
+// lanes busy: `host_enqueue` copies the caller's pageable input into the
+// pinned staging image, uploads it as one DMA, enqueues the forward and the
+// output's download in 2 MiB chunks, each with an event; `host_complete`
+// touches every page of the caller's output once (a freshly allocated array
+// takes its page faults while the device runs), then copies each finished
+// chunk out of the pinned image with streaming stores while the next is in
+// flight, and downloads the compressed head's aux image.
+struct HostJob {
+    int h = 0, w = 0;
+    size_t nout = 0;
+    std::vector<hipEvent_t> done;
+};
+
+static int host_enqueue(s2s_ctx *ctx, int h, int w, const float *in_adjusted, HostJob &job) {
     if (ctx->plan_image(h, w) || ctx->stage_buffers(h, w)) return -1;
     const int s = ctx->arch.scale;
     const size_t nin = (size_t)3 * h * w, nout = (size_t)3 * h * s * w * s;
+    job.h = h;
+    job.w = w;
+    job.nout = nout;
     std::memcpy(ctx->pin_in, in_adjusted, nin * 4);
     HIPCHK("hipMemcpyAsync(input)", hipMemcpyAsync(ctx->in_dev, ctx->pin_in, nin * 4,
                                                    hipMemcpyHostToDevice, ctx->stream));
     if (ctx->forward_device(h, w, ctx->in_dev, ctx->out_dev)) return -1;
     constexpr size_t kChunk = (size_t)1 << 19;  // floats per download chunk (2 MiB)
     const size_t nchunks = (nout + kChunk - 1) / kChunk;
-    std::vector<hipEvent_t> done(nchunks, nullptr);
-    int rc = 0;
-    for (size_t i = 0; i < nchunks && rc == 0; ++i) {
+    job.done.assign(nchunks, nullptr);
+    for (size_t i = 0; i < nchunks; ++i) {
         const size_t off = i * kChunk, len = std::min(kChunk, nout - off);
         hipError_t e = hipMemcpyAsync(ctx->pin_out + off, ctx->out_dev + off, len * 4,
                                       hipMemcpyDeviceToHost, ctx->stream);
-        if (e == hipSuccess) e = (done[i] = ctx->event()) ? hipSuccess : hipErrorOutOfMemory;
-        if (e == hipSuccess) e = hipEventRecord(done[i], ctx->stream);
-        if (e != hipSuccess) rc = fail(hip_msg("hipMemcpyAsync(output)", e));
+        if (e == hipSuccess) e = (job.done[i] = ctx->event()) ? hipSuccess : hipErrorOutOfMemory;
+        if (e == hipSuccess) e = hipEventRecord(job.done[i], ctx->stream);
+        if (e != hipSuccess) return fail(hip_msg("hipMemcpyAsync(output)", e));
     }
-    // While the device runs: touch every page of the caller's output once, so
-    // that a freshly allocated array takes its page faults here, off the path
-    // from the last kernel to the return (the copies below then only stream)
+    return 0;
+}
+
+// (returns the job's events to the context whatever happens)
+static int host_complete(s2s_ctx *ctx, HostJob &job, float *out) {
+    constexpr size_t kChunk = (size_t)1 << 19;
+    int rc = 0;
+    for (hipEvent_t e : job.done)
+        if (!e) rc = -1;  // (host_enqueue failed part-way; its error is set)
     if (rc == 0)
-        for (size_t i = 0; i < nout; i += 1024) out[i] = 0.f;
-    for (size_t i = 0; i < nchunks; ++i) {
-        if (!done[i]) continue;
+        for (size_t i = 0; i < job.nout; i += 1024) out[i] = 0.f;
+    for (size_t i = 0; i < job.done.size(); ++i) {
+        if (!job.done[i]) continue;
         if (rc == 0) {
-            const hipError_t e = hipEventSynchronize(done[i]);
+            const hipError_t e = hipEventSynchronize(job.done[i]);
             if (e != hipSuccess) {
                 rc = fail(hip_msg("hipEventSynchronize(output)", e));
             } else {
-                const size_t off = i * kChunk, len = std::min(kChunk, nout - off);
+                const size_t off = i * kChunk, len = std::min(kChunk, job.nout - off);
                 copy_out(out + off, ctx->pin_out + off, len);
             }
         }
-        ctx->free_events.push_back(done[i]);
+        ctx->free_events.push_back(job.done[i]);
     }
+    job.done.clear();
     if (rc) return rc;
     ctx->aux_host.clear();
     if (ctx->arch.upsampler == S2S_PIXELSHUFFLE_AUX) {
         // the compressed head's second image, at the padded geometry
         // (reference src/gpu.rs:752-758)
         const int win = ctx->arch.window;
-        const size_t P = (size_t)(h / win + 1) * win * ((w / win + 1) * win);
+        const size_t P = (size_t)(job.h / win + 1) * win * ((job.w / win + 1) * win);
         ctx->aux_host.resize(3 * P);
         HIPCHK("hipMemcpyAsync(aux)", hipMemcpyAsync(ctx->aux_host.data(), ctx->auxp, 3 * P * 4,
                                                      hipMemcpyDeviceToHost, ctx->stream));
     }
     HIPCHK("hipStreamSynchronize", hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int s2s_forward(s2s_ctx *ctx, int h, int w, const float *in_adjusted, float *out) {
+    if (!ctx || !in_adjusted || !out) return fail("s2s_forward: null argument");
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    if (h < ctx->arch.window || w < ctx->arch.window) return ctx->forward_device(h, w, nullptr, nullptr);
+    HostJob job;
+    const int rc = host_enqueue(ctx, h, w, in_adjusted, job);
+    const int rc2 = host_complete(ctx, job, out);
+    return rc ? rc : rc2;
+}
+
+// n host images (sizes may differ: a tiled image's crops) through the host
+// path, alternating between the context and its second lane (s2s_forward_device_batch's),
+// pipelined: while one lane's image is copied out on the host, the other lane
+// computes. Each image's result equals s2s_forward's; aux_out[i], if given,
+// receives image i's aux image (the compressed head's, at its padded geometry),
+// and s2s_aux afterwards returns the last image's.
+int s2s_forward_batch(s2s_ctx *ctx, int n, const int *h, const int *w, const float *const *in_adjusted,
+                      float *const *out, float *const *aux_out) {
+    if (!ctx || n < 0 || (n > 0 && (!h || !w || !in_adjusted || !out)))
+        return fail("s2s_forward_batch: null argument");
+    for (int i = 0; i < n; ++i) {
+        if (!in_adjusted[i] || !out[i]) return fail("s2s_forward_batch: null image pointer");
+        if (h[i] < ctx->arch.window || w[i] < ctx->arch.window)
+            return ctx->forward_device(h[i], w[i], nullptr, nullptr);  // its error message
+    }
+    HIPCHK("hipSetDevice", hipSetDevice(ctx->device));
+    if (n > 1 && ctx->make_lane()) return -1;
+    s2s_ctx *lanes[2] = {ctx, ctx->lane};
+    HostJob jobs[2];
+    auto lane_aux = [&](int i) -> int {
+        s2s_ctx *L = lanes[i & 1];
+        if (!aux_out || !aux_out[i] || L->aux_host.empty()) return 0;
+        std::memcpy(aux_out[i], L->aux_host.data(), L->aux_host.size() * 4);
+        return 0;
+    };
+    // enqueue 0 (and 1); then complete i and enqueue i + 2 on the same lane
+    int rc = 0, last = -1;
+    for (int i = 0; i < n && i < 2 && !rc; ++i) rc = host_enqueue(lanes[i], h[i], w[i], in_adjusted[i], jobs[i]);
+    for (int i = 0; i < n; ++i) {
+        const int rc_c = host_complete(lanes[i & 1], jobs[i & 1], out[i]);
+        if (rc || rc_c) {
+            rc = rc ? rc : rc_c;
+            // drain the other lane's outstanding job (its events back to it)
+            if (i + 1 < n && !jobs[(i + 1) & 1].done.empty()) {
+                std::vector<float> scratch(jobs[(i + 1) & 1].nout);
+                (void)host_complete(lanes[(i + 1) & 1], jobs[(i + 1) & 1], scratch.data());
+            }
+            break;
+        }
+        lane_aux(i);
+        last = i;
+        if (i + 2 < n) rc = host_enqueue(lanes[i & 1], h[i + 2], w[i + 2], in_adjusted[i + 2], jobs[i & 1]);
+    }
+    if (rc) return rc;
+    if (last >= 1 && (last & 1)) ctx->aux_host = ctx->lane->aux_host;
     return 0;
 }
 

@@ -228,9 +228,13 @@ def run_with_fallback(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: in
     raise RuntimeError(f"gave up after 64 tile reductions at tile {tile}")
 
 
-def run_tiled(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: int) -> np.ndarray:
+def run_tiled(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: int,
+              batch: bool = False) -> np.ndarray:
     """reference src/backend.rs:92-165. `img` is `[3][h][w]` in [0,1] (not
-    mean-adjusted); the result is `[3][h*s][w*s]`."""
+    mean-adjusted); the result is `[3][h*s][w*s]`. With `batch` and a backend
+    that has `forward_batch` (the HIP backend: its two lanes), the image's
+    crops go through one batched call, then are pasted in the same order;
+    every tile's result is what `forward` gives for it."""
     _, h, w = img.shape
     s = arch.scale
     if tile == 0:
@@ -239,17 +243,30 @@ def run_tiled(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: int) -> np
     tile = max(tile // win, 1) * win
     pad = _round_pad(pad, win)
     out = np.zeros((3, h * s, w * s), np.float32)
+
+    def paste(job, res):
+        ty, tx, y0, x0 = job
+        oy0, ox0 = ty - y0, tx - x0
+        ch = min(ty + tile, h) - ty
+        cw = min(tx + tile, w) - tx
+        # the copy is on the OUTPUT grid: ch*s rows of cw*s pixels
+        out[:, ty * s:(ty + ch) * s, tx * s:(tx + cw) * s] = \
+            res[:, oy0 * s:(oy0 + ch) * s, ox0 * s:(ox0 + cw) * s]
+
+    jobs, shapes, crops = [], [], []
     for ty in range(0, h, tile):
         for tx in range(0, w, tile):
             y0, x0 = max(ty - pad, 0), max(tx - pad, 0)
             y1, x1 = min(ty + tile + pad, h), min(tx + tile + pad, w)
             th, tw = y1 - y0, x1 - x0
-            sub = np.ascontiguousarray(img[:, y0:y1, x0:x1])
-            res = backend.forward(th, tw, M.adjust(arch, sub))
-            oy0, ox0 = ty - y0, tx - x0
-            ch = min(ty + tile, h) - ty
-            cw = min(tx + tile, w) - tx
-            # the copy is on the OUTPUT grid: ch*s rows of cw*s pixels
-            out[:, ty * s:(ty + ch) * s, tx * s:(tx + cw) * s] = \
-                res[:, oy0 * s:(oy0 + ch) * s, ox0 * s:(ox0 + cw) * s]
+            sub = M.adjust(arch, np.ascontiguousarray(img[:, y0:y1, x0:x1]))
+            if batch and hasattr(backend, "forward_batch"):
+                jobs.append((ty, tx, y0, x0))
+                shapes.append((th, tw))
+                crops.append(sub)
+            else:
+                paste((ty, tx, y0, x0), backend.forward(th, tw, sub))
+    if jobs:
+        for job, res in zip(jobs, backend.forward_batch(shapes, crops)):
+            paste(job, res)
     return out

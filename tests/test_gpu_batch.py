@@ -1,4 +1,4 @@
-"""The batched device entry (s2s_forward_device_batch): n images of one size
+"""The batched entries. s2s_forward_device_batch: n images of one size
 alternating between the context's stream and its second lane (a stream, buffer
 plans and graphs of its own over the same weights), against the same images
 forwarded one by one on a plain context, bit for bit - over repeated calls
@@ -6,7 +6,9 @@ forwarded one by one on a plain context, bit for bit - over repeated calls
 size change between batches, and single-image calls on the same context in
 between. The reference forwards one image at a time (src/backend.rs:29-49);
 equality with the single-image path, whose parity with the oracle the other
-GPU tests establish, is the bar."""
+GPU tests establish, is the bar. s2s_forward_batch (host images of mixed
+sizes, a tiled image's crops) and the tile loop over it are held to the same
+bar."""
 import numpy as np
 import pytest
 
@@ -111,3 +113,61 @@ def test_batch_waits_for_the_contexts_stream(pkg):
             b.free()
     finally:
         be.close()
+
+
+def test_host_batch_matches_single_forwards(pkg):
+    """s2s_forward_batch (host images of mixed sizes, pipelined over the two
+    lanes) against s2s_forward per image on a plain context, bit for bit: odd
+    and even batches, a batch of one and of none, repeated so each lane
+    replays its graphs; with the compressed head, each image's aux image too,
+    and s2s_aux afterwards is the last image's."""
+    M = pkg.model
+    for arch, seed in ((M.classical(4), 61), (M.compressed(), 62)):
+        wts = M.make_weights(arch, seed=seed, perturb=True)
+        shapes = [(40, 56), (24, 32), (40, 56), (32, 40), (24, 32)]
+        xs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=70 + i)))
+              for i, (h, w) in enumerate(shapes)]
+        single = pkg.HipBackend(arch, wts)
+        batch = pkg.HipBackend(arch, wts)
+        try:
+            want, want_aux = [], []
+            for (h, w), x in zip(shapes, xs):
+                want.append(single.forward(h, w, x))
+                want_aux.append(single.aux())
+            aux_head = arch.upsampler == "pixelshuffle_aux"
+            assert (want_aux[0] is not None) == aux_head
+            for sel in ([0, 1, 2, 3, 4], [1, 3], [2, 0, 4, 1], [3], [], [4, 3, 2, 1, 0]):
+                outs, auxs = batch.forward_batch([shapes[i] for i in sel], [xs[i] for i in sel], aux=True)
+                assert len(outs) == len(sel)
+                for k, i in enumerate(sel):
+                    assert np.array_equal(outs[k], want[i]), (arch.upsampler, sel, k)
+                    if aux_head:
+                        assert np.array_equal(auxs[k].ravel(), want_aux[i]), (sel, k)
+                    else:
+                        assert auxs[k] is None
+                if sel and aux_head:
+                    assert np.array_equal(batch.aux(), want_aux[sel[-1]]), sel
+            # a single-image call on the same context afterwards
+            assert np.array_equal(batch.forward(*shapes[2], xs[2]), want[2])
+        finally:
+            batch.close()
+            single.close()
+
+
+def test_tiled_image_batched_matches_sequential(pkg):
+    """The tile loop with its crops in one batched call gives the image the
+    sequential loop gives (compressed head, tiles of 32 with 8 of context on a
+    ragged 88x120 image: corner, edge, interior and clipped crops)."""
+    M = pkg.model
+    arch = M.compressed()
+    wts = M.make_weights(arch, seed=63, perturb=True)
+    img = M.to_unit(M.input_texture_dct(88, 120, seed=63))
+    be = pkg.HipBackend(arch, wts)
+    try:
+        seq = pkg.tiling.run_tiled(arch, be, img, 32, 8)
+        bat = pkg.tiling.run_tiled(arch, be, img, 32, 8, batch=True)
+        bat2 = pkg.tiling.run_tiled(arch, be, img, 32, 8, batch=True)
+    finally:
+        be.close()
+    assert seq.shape == (3, 352, 480) and np.isfinite(seq).all()
+    assert np.array_equal(bat, seq) and np.array_equal(bat2, seq)
