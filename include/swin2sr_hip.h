@@ -384,6 +384,14 @@ int s2s_test_conv3x3_nearest2(int h, int w, int c, const float *x, const float *
 int s2s_test_conv3x3_shuffle2(int h, int w, int c_in, int feat, const float *x,
                               const float *wgt, const float *bias, float *out);
 
+/* One RSTB stage of a context on host buffers (the config-1 micro-bench's op
+ * sequence: the stage's Swin blocks with shifts 0/4 alternating, the 3x3 close
+ * with its folded 1x1, the stage residual; reference src/cpu.rs:1516-1581):
+ * `s2s_rstb_device` between an upload of `x` and a download into `out`, both
+ * channel-last `[hp*wp][embed]` on an explicit (not re-padded) plane whose
+ * sides are multiples of the window. Synchronous. */
+int s2s_test_rstb(s2s_ctx *ctx, int stage, int hp, int wp, const float *x, float *out);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

@@ -92,6 +92,7 @@ EXPORTS = {
     "s2s_test_conv3x3_winograd": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP,
                                             C.c_int, FP, C.c_float, FP]),
     "s2s_test_conv3x3_shuffle2": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, FP]),
+    "s2s_test_rstb": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, FP, FP]),
     "s2s_test_conv3x3_nearest2": (C.c_int, [C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_float, FP]),
 }
 
@@ -266,6 +267,14 @@ class HipBackend:
     def rstb_device(self, stage: int, hp: int, wp: int, d_in: int, d_out: int):
         check(self._lib.s2s_rstb_device(self._ctx, stage, hp, wp, C.c_void_p(d_in),
                                         C.c_void_p(d_out)), "s2s_rstb_device")
+
+    def test_rstb(self, stage: int, hp: int, wp: int, x_hwc: np.ndarray) -> np.ndarray:
+        """One RSTB stage on host buffers (channel-last `[hp*wp][embed]`)."""
+        x = np.ascontiguousarray(x_hwc, dtype=np.float32)
+        assert x.size == hp * wp * self.arch.embed, x.shape
+        out = np.empty((hp * wp, self.arch.embed), np.float32)
+        check(self._lib.s2s_test_rstb(self._ctx, stage, hp, wp, fptr(x), fptr(out)), "s2s_test_rstb")
+        return out
 
     def aux(self) -> Optional[np.ndarray]:
         p = FP()

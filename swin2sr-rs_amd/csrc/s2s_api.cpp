@@ -1465,6 +1465,8 @@ int weights_device_bytes(const s2s_arch &A, const TensorSet &ts, uint64_t *bytes
 // Exported ABI
 // ---------------------------------------------------------------------------
 
+int s2s_ctx_embed(s2s_ctx *ctx) { return ctx ? ctx->arch.embed : 0; }
+
 extern "C" {
 
 const char *s2s_last_error(void) { return g_err.c_str(); }

@@ -333,3 +333,6 @@ hipError_t launch_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *re
 // The ABI's thread-local error slot (defined in s2s_api.cpp): records `msg`
 // for s2s_last_error() and returns -1. Internal to the library.
 __attribute__((visibility("hidden"))) int s2s_fail(const char *msg);
+// A context's embed width (channels of its planes); 0 for a null context.
+struct s2s_ctx;
+__attribute__((visibility("hidden"))) int s2s_ctx_embed(struct s2s_ctx *ctx);

@@ -517,4 +517,20 @@ int s2s_test_conv3x3_nearest2(int h, int w, int c, const float *x, const float *
     return 0;
 }
 
+int s2s_test_rstb(s2s_ctx *ctx, int stage, int hp, int wp, const float *x, float *out) {
+    if (!ctx || !x || !out) return fail("s2s_test_rstb: null argument");
+    const int c = s2s_ctx_embed(ctx);
+    if (c <= 0 || hp <= 0 || wp <= 0) return fail("s2s_test_rstb: bad shape");
+    const size_t n = (size_t)hp * wp * c;
+    Dev d;
+    float *dx = d.up(x, n);
+    float *dy = d.alloc<float>(n);
+    if (!dx || !dy) return fail("hipMalloc failed: out of memory");
+    if (int rc = s2s_rstb_device(ctx, stage, hp, wp, dx, dy)) return rc;
+    hipError_t e = hipStreamSynchronize((hipStream_t)s2s_stream(ctx));
+    if (e != hipSuccess) return fail(std::string("hipStreamSynchronize failed: ") + hipGetErrorString(e));
+    if (hipMemcpy(out, dy, n * 4, hipMemcpyDeviceToHost) != hipSuccess) return fail("hipMemcpy failed");
+    return 0;
+}
+
 }  // extern "C"

@@ -461,7 +461,8 @@ def test_forward_refuses_plane_past_buffer_limit(pkg):
 
 
 def test_rstb_device(pkg, orc):
-    """One RSTB (config 1's op sequence) on an explicit unpadded plane."""
+    """One RSTB (config 1's op sequence) on an explicit unpadded plane, through
+    the device entry and the host-buffer test entry (bit-identical)."""
     hip = pkg.hip
     M = pkg.model
     arch = M.Arch(upsampler="pixelshuffle", scale=2, embed=180, heads=6, depths=[6])
@@ -477,10 +478,14 @@ def test_rstb_device(pkg, orc):
         be.rstb_device(0, hp, wp, dx.ptr, dy.ptr)
         hip.synchronize()
         got = hwc_to_nchw(dy.download((hp * wp, 180)), hp, wp)
+        # the host-buffer entry runs the same launches
+        assert np.array_equal(be.test_rstb(0, hp, wp, nchw_to_hwc(x)), dy.download((hp * wp, 180)))
         # in place (d_in == d_out) is allowed by the ABI
         be.rstb_device(0, hp, wp, dx.ptr, dx.ptr)
         hip.synchronize()
         assert np.array_equal(dx.download((hp * wp, 180)), dy.download((hp * wp, 180)))
+        dx.free()
+        dy.free()
     finally:
         be.close()
     err = np.abs(got - want).max() / max(1.0, np.abs(want).max())
