@@ -171,3 +171,34 @@ def test_tiled_image_batched_matches_sequential(pkg):
         be.close()
     assert seq.shape == (3, 352, 480) and np.isfinite(seq).all()
     assert np.array_equal(bat, seq) and np.array_equal(bat2, seq)
+
+
+def test_batch_entries_refuse_bad_arguments(pkg):
+    """Errors come back through s2s_last_error and leave the context usable:
+    an image smaller than a window anywhere in a host batch, null image
+    pointers, a negative count; then both entries still run."""
+    import ctypes as C
+
+    M = pkg.model
+    arch = M.classical(4)
+    wts = M.make_weights(arch, seed=64, perturb=True)
+    be = pkg.HipBackend(arch, wts)
+    try:
+        x = M.adjust(arch, M.to_unit(M.input_sinusoids(24, 32, seed=64)))
+        want = be.forward(24, 32, x)
+        small = np.zeros((3, 4, 32), np.float32)
+        with pytest.raises(pkg.abi.S2SError, match="s2s_forward_batch"):
+            be.forward_batch([(24, 32), (4, 32)], [x, small])
+        lib, ctx = be._lib, be._ctx
+        hs = (C.c_int * 1)(24)
+        ws = (C.c_int * 1)(32)
+        nul = (C.c_void_p * 1)(None)
+        assert lib.s2s_forward_batch(ctx, 1, hs, ws, nul, nul, None) != 0
+        assert "null" in pkg.abi.last_error()
+        assert lib.s2s_forward_batch(ctx, -1, hs, ws, nul, nul, None) != 0
+        assert lib.s2s_forward_device_batch(ctx, -1, 24, 32, nul, nul) != 0
+        outs = be.forward_batch([(24, 32), (24, 32)], [x, x])
+        assert all(np.array_equal(o, want) for o in outs)
+        assert np.array_equal(be.forward(24, 32, x), want)
+    finally:
+        be.close()
