@@ -654,8 +654,32 @@ def bench_copy_ceiling(args, pkg):
                       "sizes": res}), flush=True)
 
 
+def bench_mfma_peak(args, pkg):
+    """The fp32 matrix ceiling the MFMA-bound kernels are read against, beside
+    the 157.3 TFLOP/s spec figure: the library's probe kernel (one 512-thread
+    workgroup per CU, every wave issuing independent v_mfma_f32_16x16x4f32 and
+    nothing else), `steps` launches timed with events, at two loop lengths
+    (the longer one's rate is the ceiling; the pair shows the launch is
+    amortised). The implied shader clock is the rate over 64 FLOPs per cycle
+    per SIMD. One JSON line."""
+    res = {}
+    for iters in (5000, 40000):
+        ms, tf, ghz = pkg.abi.mfma_peak(iters, max(args.steps, 1))
+        res[str(iters)] = {"ms_per_launch": round(ms, 4), "TFLOPs": round(tf, 2),
+                           "frac_of_spec": round(tf * 1e12 / MFMA_FP32_PEAK, 4),
+                           "implied_clock_GHz": round(ghz, 3)}
+        log(f"bench: mfma peak probe, {4 * iters} MFMAs per wave: {ms:.3f} ms, {tf:.2f} TFLOP/s "
+            f"({100 * tf * 1e12 / MFMA_FP32_PEAK:.1f}% of 157.3), implied clock {ghz:.3f} GHz")
+    print(json.dumps({"metric": "fp32 MFMA TFLOP/s under pure MFMA load @1 GPU", "unit": "TFLOP/s",
+                      "n_gpus": 1, "steps": args.steps, "higher_is_better": True, "dtype": "f32",
+                      "data": "register operands",
+                      "config": {"workload": "k_mfma_peak: one 512-thread workgroup per CU, 4 independent "
+                                             "v_mfma_f32_16x16x4f32 per loop iteration per wave"},
+                      "loops": res}), flush=True)
+
+
 WORKLOADS = ["classical-x4", "rstb", "lightweight-x2", "classical-x2", "realworld-x4",
-             "compressed-x4-tiled", "copy-ceiling"]
+             "compressed-x4-tiled", "copy-ceiling", "mfma-peak"]
 
 
 def main():
@@ -671,7 +695,8 @@ def main():
                     help="classical-x4: the BASELINE metric (default); rstb: config 1's "
                          "single-RSTB micro-bench; lightweight-x2, classical-x2, realworld-x4: "
                          "configs 0, 2, 3 whole-image; compressed-x4-tiled: config 4; "
-                         "copy-ceiling: the runtime's device copy at several sizes")
+                         "copy-ceiling: the runtime's device copy at several sizes; "
+                         "mfma-peak: the fp32 matrix rate under pure MFMA load")
     ap.add_argument("--lanes", type=int, default=1, choices=[0, 1],
                     help="also time two images per step through the two-lane batched entry "
                          "(reported as two_lane_serving; value stays the one-image rate); with "
@@ -695,6 +720,8 @@ def main():
         bench_tiled(args, pkg)
     elif args.workload == "copy-ceiling":
         bench_copy_ceiling(args, pkg)
+    elif args.workload == "mfma-peak":
+        bench_mfma_peak(args, pkg)
     else:
         bench_image(args, pkg, args.workload)
 

@@ -392,6 +392,15 @@ int s2s_test_conv3x3_shuffle2(int h, int w, int c_in, int feat, const float *x,
  * sides are multiples of the window. Synchronous. */
 int s2s_test_rstb(s2s_ctx *ctx, int stage, int hp, int wp, const float *x, float *out);
 
+/* The device's fp32 matrix rate under pure MFMA load, measured (no reference
+ * counterpart: the reference quotes no device ceiling; the roofline fractions
+ * are read against it beside the spec figure): one 512-thread workgroup per CU,
+ * every wave issuing 4 * iters independent v_mfma_f32_16x16x4f32 and nothing
+ * else, `reps` launches timed with events after one warm-up. `*ms` is the time
+ * per launch, `*tflops` 2048 FLOPs per MFMA over it, `*ghz` the shader clock
+ * that rate implies at 64 fp32 matrix FLOPs per cycle per SIMD. */
+int s2s_test_mfma_peak(int iters, int reps, double *ms, double *tflops, double *ghz);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

@@ -93,6 +93,8 @@ EXPORTS = {
                                             C.c_int, FP, C.c_float, FP]),
     "s2s_test_conv3x3_shuffle2": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, FP, FP, FP, FP]),
     "s2s_test_rstb": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, FP, FP]),
+    "s2s_test_mfma_peak": (C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                     C.POINTER(C.c_double)]),
     "s2s_test_conv3x3_nearest2": (C.c_int, [C.c_int, C.c_int, C.c_int, FP, FP, FP, C.c_float, FP]),
 }
 
@@ -348,6 +350,15 @@ def selftest(arch: M.Arch, weights: Optional[Dict[str, np.ndarray]] = None):
 def unit_floats(hp, wp, heads, head_dim):
     """Floats of the window attention's unit layout of qkv for a plane."""
     return (hp // 8) * (wp // 8) * ((heads + 1) // 2) * 64 * (6 * head_dim + 2)
+
+
+def mfma_peak(iters: int = 20000, reps: int = 5) -> Tuple[float, float, float]:
+    """(ms per launch, TFLOP/s, implied shader clock in GHz) of the fp32 MFMA
+    peak probe."""
+    ms, tf, ghz = C.c_double(), C.c_double(), C.c_double()
+    check(load_library().s2s_test_mfma_peak(iters, reps, C.byref(ms), C.byref(tf), C.byref(ghz)),
+          "s2s_test_mfma_peak")
+    return ms.value, tf.value, ghz.value
 
 
 def test_qkv_windows(hp, wp, heads, head_dim, shift, x, wqkv, bqkv):

@@ -329,6 +329,10 @@ hipError_t launch_cpb(const float *w0, const float *b0, const float *w2, float *
                       int win, int heads, hipStream_t st);
 hipError_t launch_window_map(int hp, int wp, int shift, int32_t *yx, uint8_t *reg,
                              hipStream_t st);
+// The fp32 MFMA peak probe: `blocks` workgroups of 512 threads, each wave
+// issuing 4 * iters independent v_mfma_f32_16x16x4f32; one float per thread
+// to `out` (blocks * 512 floats).
+hipError_t launch_mfma_peak(float *out, int blocks, int iters, hipStream_t st);
 
 // The ABI's thread-local error slot (defined in s2s_api.cpp): records `msg`
 // for s2s_last_error() and returns -1. Internal to the library.

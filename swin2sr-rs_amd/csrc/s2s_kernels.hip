@@ -2998,6 +2998,34 @@ hipError_t launch_gemm_variant(const GemmArgs &g, int aload, int epi, int varian
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_mfma_peak: the fp32 matrix peak of the device, measured. Every wave issues
+// `iters` rounds of four independent v_mfma_f32_16x16x4f32 (four accumulator
+// tiles, so no MFMA waits for the previous one's result) and nothing else in
+// its loop; one 512-thread workgroup per CU puts two such waves on each SIMD.
+// The result (one float per thread) is stored so the work is not removed.
+// Timed by the caller: 2048 FLOPs per MFMA over the elapsed time is the
+// matrix rate the chip sustains under pure MFMA load, and at 64 FLOPs per
+// cycle per SIMD the implied shader clock.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void k_mfma_peak(float *out, int iters, float x) {
+    f4v a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0, a3 = a0;
+    const float p = x + (float)threadIdx.x, q = x - (float)threadIdx.x;
+    for (int i = 0; i < iters; ++i) {
+        a0 = MFMA16(p, q, a0);
+        a1 = MFMA16(q, p, a1);
+        a2 = MFMA16(p, p, a2);
+        a3 = MFMA16(q, q, a3);
+    }
+    out[(size_t)blockIdx.x * 512 + threadIdx.x] = a0[0] + a1[1] + a2[2] + a3[3];
+}
+
+hipError_t launch_mfma_peak(float *out, int blocks, int iters, hipStream_t st) {
+    if (blocks <= 0 || iters <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mfma_peak, dim3((unsigned)blocks), dim3(512), 0, st, out, iters, 1.0f);
+    return hipGetLastError();
+}
+
 // ---- k_bsgemm dispatch ----------------------------------------------------
 
 static int cu_count() {

@@ -517,6 +517,36 @@ int s2s_test_conv3x3_nearest2(int h, int w, int c, const float *x, const float *
     return 0;
 }
 
+int s2s_test_mfma_peak(int iters, int reps, double *ms, double *tflops, double *ghz) {
+    if (iters <= 0 || reps <= 0 || !ms || !tflops || !ghz) return fail("s2s_test_mfma_peak: bad argument");
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return fail("s2s_test_mfma_peak: no device");
+    Dev d;
+    float *out = d.alloc<float>((size_t)cus * 512);
+    if (!out) return fail("hipMalloc failed: out of memory");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = launch_mfma_peak(out, cus, iters, 0);  // warm-up
+    if (e == hipSuccess) e = hipEventRecord(e0, 0);
+    for (int r = 0; r < reps && e == hipSuccess; ++r) e = launch_mfma_peak(out, cus, iters, 0);
+    if (e == hipSuccess) e = hipEventRecord(e1, 0);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float t = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return fail(std::string("s2s_test_mfma_peak: ") + hipGetErrorString(e));
+    *ms = (double)t / reps;
+    // 8 waves per workgroup, 4 MFMAs per iteration, 2048 FLOPs each
+    *tflops = (double)cus * 8 * 4 * (double)iters * 2048.0 / (*ms * 1e-3) / 1e12;
+    // 4 SIMDs per CU, 64 fp32 matrix FLOPs per cycle each
+    *ghz = *tflops * 1e12 / ((double)cus * 4 * 64) / 1e9;
+    return 0;
+}
+
 int s2s_test_rstb(s2s_ctx *ctx, int stage, int hp, int wp, const float *x, float *out) {
     if (!ctx || !x || !out) return fail("s2s_test_rstb: null argument");
     const int c = s2s_ctx_embed(ctx);

@@ -603,3 +603,12 @@ def test_other_heads_against_oracle(pkg, orc, upsampler, scale, h, w):
     assert np.abs(M.to_rgb8(got).astype(int) - M.to_rgb8(want).astype(int)).max() <= 1
     if want_aux is not None:
         assert np.abs(aux.reshape(want_aux.shape) - want_aux).max() < 1e-4
+
+
+def test_mfma_peak_probe(pkg):
+    """The fp32 matrix peak probe returns a rate no device can exceed: at most
+    the 157.3 TFLOP/s spec figure (2.4 GHz x 256 CUs x 4 SIMDs x 64 FLOPs per
+    cycle) plus timing noise, and a positive one; its implied clock matches."""
+    ms, tf, ghz = pkg.abi.mfma_peak(2000, 3)
+    assert ms > 0 and 0 < tf <= 157.3 * 1.03, (ms, tf)
+    assert abs(ghz - tf * 1e12 / (256 * 4 * 64) / 1e9) < 0.05 * ghz, (tf, ghz)
