@@ -115,6 +115,55 @@ impl Gpu {
     }
 }
 
+impl Gpu {
+    /// Several images at once, e.g. all of an image's tiles: `s2s_forward_batch`
+    /// pipelines them over the context's two lanes (one computes while the
+    /// other's result is copied out). Each result equals `forward`'s for its
+    /// input; `aux()` afterwards is the last image's. No counterpart in the
+    /// crate: its `run_tiled` calls `Backend::forward` once per tile
+    /// (src/backend.rs:92-165); a tile loop that gathers an image's crops
+    /// first can call this instead and paste the results in the same order.
+    pub fn forward_batch(&mut self, items: &[(usize, usize, &[f32])]) -> Result<Vec<Vec<f32>>, String> {
+        let mut hs = Vec::with_capacity(items.len());
+        let mut ws = Vec::with_capacity(items.len());
+        let mut ins = Vec::with_capacity(items.len());
+        let mut outs = Vec::with_capacity(items.len());
+        for &(h, w, input) in items {
+            if input.len() != 3 * h * w {
+                return Err(format!("forward_batch: {} input floats for a {h}x{w} image", input.len()));
+            }
+            hs.push(h as c_int);
+            ws.push(w as c_int);
+            ins.push(input.as_ptr());
+            outs.push(vec![0f32; 3 * h * self.scale * w * self.scale]);
+        }
+        let optrs: Vec<*mut f32> = outs.iter_mut().map(|o| o.as_mut_ptr()).collect();
+        check(
+            unsafe {
+                s2s_forward_batch(
+                    self.ctx,
+                    items.len() as c_int,
+                    hs.as_ptr(),
+                    ws.as_ptr(),
+                    ins.as_ptr(),
+                    optrs.as_ptr(),
+                    std::ptr::null(),
+                )
+            },
+            "forward_batch",
+        )?;
+        self.aux = None;
+        if self.want_aux && !items.is_empty() {
+            let (mut p, mut n) = (std::ptr::null(), 0usize);
+            check(unsafe { s2s_aux(self.ctx, &mut p, &mut n) }, "aux")?;
+            if n > 0 {
+                self.aux = Some(unsafe { std::slice::from_raw_parts(p, n) }.to_vec());
+            }
+        }
+        Ok(outs)
+    }
+}
+
 impl Backend for Gpu {
     fn name(&self) -> &'static str {
         "hip"

@@ -52,6 +52,15 @@ extern "C" {
     pub fn s2s_set_alloc_limit(ctx: *mut S2sCtx, bytes: u64) -> c_int;
     pub fn s2s_forward(ctx: *mut S2sCtx, h: c_int, w: c_int, inp: *const f32, out: *mut f32) -> c_int;
     pub fn s2s_forward_device(ctx: *mut S2sCtx, h: c_int, w: c_int, d_in: *const f32, d_out: *mut f32) -> c_int;
+    pub fn s2s_forward_batch(
+        ctx: *mut S2sCtx,
+        n: c_int,
+        h: *const c_int,
+        w: *const c_int,
+        inp: *const *const f32,
+        out: *const *mut f32,
+        aux_out: *const *mut f32,
+    ) -> c_int;
     pub fn s2s_aux(ctx: *mut S2sCtx, ptr: *mut *const f32, n: *mut usize) -> c_int;
     pub fn s2s_last_error() -> *const c_char;
     pub fn s2s_device_info(name: *mut c_char, cap: usize, arch: *mut c_char, acap: usize) -> c_int;
