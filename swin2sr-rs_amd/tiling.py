@@ -194,19 +194,20 @@ def is_out_of_memory(err: str) -> bool:
 
 
 def run_with_fallback(arch: M.Arch, backend, img: np.ndarray, tile: int, pad: int,
-                      quiet: bool = False, log=None):
+                      quiet: bool = False, log=None, batch: bool = False):
     """reference src/main.rs:579-662: `run_tiled`, and while the backend fails
     with an out-of-memory error, again with the tile halved - a failed
     whole-image pass (`tile == 0`) falls back to half the image's longer side -
     down to one window. Only out-of-memory errors are retried; a retry out of
-    `tile == 0` (the only exact mode) is announced even when `quiet`.
+    `tile == 0` (the only exact mode) is announced even when `quiet`. `batch`
+    is passed to `run_tiled` (an image's crops in one batched call).
     Returns (image, tile used)."""
     log = log or (lambda m: print(m, file=sys.stderr, flush=True))
     win = arch.window
     _, h, w = img.shape
     for _ in range(64):
         try:
-            return run_tiled(arch, backend, img, tile, pad), tile
+            return run_tiled(arch, backend, img, tile, pad, batch=batch), tile
         except Exception as e:  # the backend's error type carries the message
             msg = str(e)
             if not (is_out_of_memory(msg) and (tile > win or tile == 0)):

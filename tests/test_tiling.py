@@ -131,6 +131,45 @@ def test_run_with_fallback_halves_until_the_tile_fits(pkg, orc):
     assert notes == []
 
 
+class BatchingBackend:
+    """A backend with `forward_batch` (the HIP backend's two-lane entry) over
+    another one, recording each batch's shapes; out of memory above a crop
+    size, like CappedBackend (test code only)."""
+
+    def __init__(self, inner, max_side=1 << 30):
+        self.inner, self.max_side, self.batches = inner, max_side, []
+
+    def forward(self, h, w, x):
+        raise AssertionError("the batched tile loop calls forward_batch only")
+
+    def forward_batch(self, shapes, xs):
+        self.batches.append(list(shapes))
+        if max(max(s) for s in shapes) > self.max_side:
+            raise RuntimeError("hipMalloc(qkv) failed: out of memory")
+        return [self.inner.forward(h, w, x) for (h, w), x in zip(shapes, xs)]
+
+
+def test_batched_tile_loop_is_the_sequential_one(pkg, orc):
+    """run_tiled with `batch`: the image's crops go to one forward_batch call
+    in the sequential loop's order, and the image is the sequential loop's;
+    through run_with_fallback the out-of-memory retry halves the tile as for
+    forward."""
+    M, T = pkg.model, pkg.tiling
+    a = tiny(pkg)
+    inner = OracleBackend(orc, a, M.make_weights(a, seed=10, perturb=True))
+    img = M.to_unit(M.input_uniform(40, 56, seed=11))
+    seq = T.run_tiled(a, inner, img, 16, 8)
+    bb = BatchingBackend(inner)
+    assert np.array_equal(T.run_tiled(a, bb, img, 16, 8, batch=True), seq)
+    assert len(bb.batches) == 1 and len(bb.batches[0]) == 3 * 4
+    assert bb.batches[0][0] == (24, 24) and bb.batches[0][-1] == (16, 16)
+    # tile 0 stays one whole-image forward
+    assert np.array_equal(T.run_tiled(a, inner, img, 0, 8, batch=True), T.run_tiled(a, inner, img, 0, 8))
+    capped = BatchingBackend(inner, max_side=32)
+    got, tile = T.run_with_fallback(a, capped, img, 32, 8, quiet=True, batch=True)
+    assert tile == 16 and np.array_equal(got, seq)
+
+
 def test_run_with_fallback_retries_only_out_of_memory(pkg, orc):
     M, T = pkg.model, pkg.tiling
     a = tiny(pkg)
