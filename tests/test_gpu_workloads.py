@@ -175,3 +175,35 @@ def test_config4_compressed_tiled(pkg, orc):
         oy, ox = (ty * 256 - y0) * 4, (tx * 256 - x0) * 4
         assert np.array_equal(out[:, ty * 1024:(ty + 1) * 1024, tx * 1024:(tx + 1) * 1024],
                               got[:, oy:oy + 1024, ox:ox + 1024])
+
+
+@pytest.mark.parametrize("kind", ["mean", "white", "checker"])
+def test_degenerate_images(pkg, orc, kind):
+    """Degenerate images against the oracle: every pixel at the normalisation
+    mean (the adjusted input is exactly 0: every activation comes from the
+    conv biases alone, the same at every interior pixel, so every window's
+    tokens are equal and its softmax is uniform up to the position bias), a
+    constant white image, and a one-pixel black/white checkerboard (the
+    largest step between neighbours), through classical x4 and the
+    lightweight x2 model at 24 x 40."""
+    M = pkg.model
+    h, w = 24, 40
+    for arch, seed in ((M.classical(4), 81), (M.lightweight(2), 82)):
+        wts = M.make_weights(arch, seed=seed)
+        if kind == "mean":
+            img = np.broadcast_to(np.asarray(arch.mean, np.float32)[:, None, None], (3, h, w)).copy()
+        elif kind == "white":
+            img = np.ones((3, h, w), np.float32)
+        else:
+            yy, xx = np.mgrid[0:h, 0:w]
+            img = np.broadcast_to(((yy + xx) % 2).astype(np.float32), (3, h, w)).copy()
+        x = M.adjust(arch, img)
+        if kind == "mean":
+            assert not np.any(x)
+        be = pkg.HipBackend(arch, wts)
+        try:
+            got = be.forward(h, w, x)
+        finally:
+            be.close()
+        want, _ = orc.forward(arch, wts, h, w, x)
+        check_image(M, got, want)
