@@ -263,3 +263,42 @@ def test_capture_around_a_new_size_is_refused(pkg):
             h_.hipGraphDestroy(g)
         graph.close()
         eager.close()
+
+
+def test_many_replays_and_batches_are_identical(pkg):
+    """Determinism under repetition: classical x4 at 64 x 64, 200 graph replays
+    and 100 two-lane batches of the same input, every output equal to the
+    first eager forward's bit for bit (the kernels have no atomics and a fixed
+    reduction order, so any difference would be a race or a hardware fault)."""
+    M, hip = pkg.model, pkg.hip
+    arch = M.classical(4)
+    wts = M.make_weights(arch, seed=91, perturb=True)
+    h = w = 64
+    x = M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=91)))
+    shape = (3, h * 4, w * 4)
+    be = make_backend(pkg, arch, wts, graphs=True)
+    bufs = []
+    try:
+        din = hip.DeviceBuffer.from_array(x)
+        dout = hip.DeviceBuffer(3 * h * 4 * w * 4)
+        d2 = [hip.DeviceBuffer(3 * h * 4 * w * 4) for _ in range(2)]
+        bufs += [din, dout] + d2
+        be.forward_device(h, w, din.ptr, dout.ptr)
+        hip.stream_synchronize(be.stream())
+        want = dout.download(shape)
+        st = be.stream()
+        for rep in range(200):
+            be.forward_device(h, w, din.ptr, dout.ptr)
+            if rep % 20 == 19:
+                hip.stream_synchronize(st)
+                assert np.array_equal(dout.download(shape), want), rep
+        for rep in range(100):
+            be.forward_device_batch(h, w, [din.ptr, din.ptr], [d.ptr for d in d2])
+            if rep % 10 == 9:
+                hip.stream_synchronize(st)
+                for k, d in enumerate(d2):
+                    assert np.array_equal(d.download(shape), want), (rep, k)
+    finally:
+        for b in bufs:
+            b.free()
+        be.close()
