@@ -2,7 +2,8 @@
 allocating one (s2s_forward_device) through the C ABI: the same kernels on a
 static per-GPU workspace, so the outputs must agree bit for bit - on two calls
 in a row, the second on a smaller image (the workspace keeps the first call's
-contents), and for a head that writes the compressed model's aux planes. A
+contents), for every head (the compressed model's aux planes, the x2 composed
+octave, pixelshuffledirect, nearest+conv) and the lightweight width. A
 plane past the workspace is refused with an error and the context still runs."""
 import numpy as np
 import pytest
@@ -27,16 +28,26 @@ def _pair(pkg, be, arch, h, w, seed):
     return got, want
 
 
-@pytest.mark.parametrize("which", ["classical-x4", "compressed-x4"])
+@pytest.mark.parametrize("which", ["classical-x4", "compressed-x4", "classical-x2", "lightweight-x2",
+                                   "realworld-x4"])
 def test_noalloc_forward_matches_the_allocating_one(pkg, which):
     M = pkg.model
+    sizes = [(120, 96, 1), (40, 56, 2)]
     if which == "classical-x4":
         arch = M.classical(4)
-    else:
+    elif which == "compressed-x4":
         arch = M.Arch(upsampler="pixelshuffle_aux", scale=4, embed=180, heads=6, depths=[2, 2])
+    elif which == "classical-x2":
+        arch = M.Arch(upsampler="pixelshuffle", scale=2, embed=180, heads=6, depths=[2, 2])
+    elif which == "lightweight-x2":
+        arch = M.lightweight(2)
+    else:
+        # the nearest+conv head's planes are 16 times the body's: smaller images
+        arch = M.Arch(upsampler="nearest+conv", scale=4, embed=180, heads=6, depths=[2, 2])
+        sizes = [(64, 72, 1), (40, 56, 2)]
     be = pkg.HipBackend(arch, M.make_weights(arch, seed=7, perturb=True))
     try:
-        for h, w, seed in [(120, 96, 1), (40, 56, 2)]:
+        for h, w, seed in sizes:
             got, want = _pair(pkg, be, arch, h, w, seed)
             assert np.isfinite(got).all()
             assert np.array_equal(got, want), (h, w)
