@@ -8,7 +8,6 @@
 enum {
     ALOAD_ROWS = 0,       // A[m*lda + k]
     ALOAD_IM2COL = 1,     // 3x3 im2col of the channel-last H x W plane A[H*W][cin]
-    ALOAD_IM2COL_UP2 = 2, // 3x3 im2col of the nearest-2x upsampling of A[(H/2)*(W/2)][cin]
     ALOAD_IM2COL5 = 3,    // 5x5 im2col of the channel-last H x W plane (k = tap*cin + ci)
     ALOAD_SUB2 = 4        // a 3x3 conv of the nearest-2x upsampling of the H x W plane A,
                           // as four 2x2 convs of A, one per output phase (a, b): row m =

@@ -169,6 +169,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // centred 3x3 and 5x5, (a - 1, b - 1) for SUB2's phase (a, b)
     constexpr bool SUB2 = ALOAD == ALOAD_SUB2;
     constexpr bool IC = ALOAD == ALOAD_IM2COL || ALOAD == ALOAD_IM2COL5 || SUB2;
+    static_assert(IC || ALOAD == ALOAD_ROWS, "operand loader");
     constexpr int RAD = ALOAD == ALOAD_IM2COL5 ? 2 : 1;
     constexpr int FS = SUB2 ? 2 : 2 * RAD + 1;
     constexpr int WTM = MT / WM / 32;
@@ -230,12 +231,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     // branch.
     // A through a resource based at the first row (pixel) this tile can
     // touch, so the offsets stay small whatever the size of the plane
-    const int pb = ALOAD == ALOAD_ROWS     ? m0
-                   : IC ? max(m0 - RAD * (g.W + 1), 0)
-                                           : max((m0 / g.W - 1) >> 1, 0) * (g.W >> 1);
+    const int pb = ALOAD == ALOAD_ROWS ? m0 : max(m0 - RAD * (g.W + 1), 0);
     const int arow = ALOAD == ALOAD_ROWS ? g.lda : g.cin;
-    const size_t afloats = ALOAD == ALOAD_ROWS ? (size_t)g.M * g.lda
-                                               : (size_t)g.H * g.W * g.cin / (ALOAD == ALOAD_IM2COL_UP2 ? 4 : 1);
+    const size_t afloats = ALOAD == ALOAD_ROWS ? (size_t)g.M * g.lda : (size_t)g.H * g.W * g.cin;
     const __amdgpu_buffer_rsrc_t ra_rs =
         buf_rsrc(g.A + (size_t)pb * arow, (afloats - (size_t)pb * arow) * 4);
     const __amdgpu_buffer_rsrc_t rb_rs = buf_rsrc(g.B, (size_t)g.N * g.ldb * 4);
@@ -276,11 +274,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             tmask[i] = msk;
         }
     }
-    // (tap, ci) of k = k0 + kq for the chunk at k0, and the tap's shift; for
-    // IM2COL also tapoff = ((dy * W + dx) * cin + ci) * 4, the byte offset of
-    // that element from its row's pixel (unchanged when ci wraps into the
-    // next tap of the same kernel row; + (W - FS) * cin * 4 into the next row)
-    int tap = 0, ci = kq, dy = oy, dx = ox;
+    // (tap, ci) of k = k0 + kq for the chunk at k0, the tap's column dx, and
+    // tapoff = ((dy * W + dx) * cin + ci) * 4 for the tap at (dy, dx): the
+    // byte offset of that element from its row's pixel (unchanged when ci
+    // wraps into the next tap of the same kernel row; + (W - FS) * cin * 4
+    // into the next row)
+    int tap = 0, ci = kq, dx = ox;
     int tapoff = IC ? ((oy * g.W + ox) * g.cin + kq) * 4 : 0;
     auto norm_k = [&]() __attribute__((always_inline)) {
         if (ALOAD == ALOAD_ROWS) return;
@@ -289,7 +288,6 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             ++tap;
             if (++dx >= ox + FS) {
                 dx = ox;
-                ++dy;
                 tapoff += (g.W - FS) * g.cin * 4;
             }
         }
@@ -305,14 +303,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             int off;
             if (ALOAD == ALOAD_ROWS) {
                 off = (am[i] < g.M && kok) ? ((am[i] - pb) * g.lda + k0 + kq) * 4 : BUF_OOB;
-            } else if (IC) {
-                off = ((tmask[i] >> tsel) & 1u) ? aro[i] + tapoff : BUF_OOB;
             } else {
-                const int sy = ay[i] + dy, sx = ax[i] + dx;
-                const bool ok = am[i] < g.M && kok && (unsigned)sy < (unsigned)g.H &&
-                                (unsigned)sx < (unsigned)g.W;
-                const int px = (sy >> 1) * (g.W >> 1) + (sx >> 1) - pb;
-                off = ok ? (px * g.cin + ci) * 4 : BUF_OOB;
+                off = ((tmask[i] >> tsel) & 1u) ? aro[i] + tapoff : BUF_OOB;
             }
             ra[i] = buf_load4(ra_rs, off);
         }
@@ -2901,7 +2893,7 @@ static const int kVariants[GEMM_NVARIANTS][4] = {
 
 template <int MT, int NT, int WM, int WN, int ALOAD>
 static hipError_t run_gemm_e(const GemmArgs &g, int epi, hipStream_t st) {
-    if constexpr (ALOAD == ALOAD_IM2COL_UP2 || ALOAD == ALOAD_SUB2) {
+    if constexpr (ALOAD == ALOAD_SUB2) {
         // the real-world head's conv_up1 / conv_up2 (+ LeakyReLU 0.2)
         if (epi == EPI_LRELU) return run_gemm_t<MT, NT, WM, WN, ALOAD, EPI_LRELU>(g, st);
         return hipErrorInvalidValue;
@@ -2936,7 +2928,6 @@ static hipError_t run_gemm_v(const GemmArgs &g, int aload, int epi, hipStream_t 
     switch (aload) {
     case ALOAD_ROWS: return run_gemm_e<MT, NT, WM, WN, ALOAD_ROWS>(g, epi, st);
     case ALOAD_IM2COL: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL>(g, epi, st);
-    case ALOAD_IM2COL_UP2: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL_UP2>(g, epi, st);
     case ALOAD_IM2COL5: return run_gemm_e<MT, NT, WM, WN, ALOAD_IM2COL5>(g, epi, st);
     case ALOAD_SUB2: return run_gemm_e<MT, NT, WM, WN, ALOAD_SUB2>(g, epi, st);
     default: return hipErrorInvalidValue;
@@ -2950,9 +2941,8 @@ const char *gemm_kernel_name(const GemmArgs &g, int aload, int epi) {
          "gemm_rows_lrelu", "gemm_rows_shuffle", "gemm_rows_shuffle_finish", "gemm_rows_qkv_win"},
         {"conv3x3_store", "conv3x3_gelu", "conv3x3_res", "conv3x3_ln", "conv3x3_ln_res",
          "conv3x3_lrelu", "conv3x3_shuffle", "conv3x3_shuffle_finish", "conv3x3_qkv_win"},
-        {"conv3x3_up2_store", "conv3x3_up2_gelu", "conv3x3_up2_res", "conv3x3_up2_ln",
-         "conv3x3_up2_ln_res", "conv3x3_up2_lrelu", "conv3x3_up2_shuffle",
-         "conv3x3_up2_shuffle_finish", "conv3x3_up2_qkv_win"},
+        {"gemm_unknown", "gemm_unknown", "gemm_unknown", "gemm_unknown", "gemm_unknown",
+         "gemm_unknown", "gemm_unknown", "gemm_unknown", "gemm_unknown"},  // (2: no loader)
         {"conv5x5_store", "conv5x5_gelu", "conv5x5_res", "conv5x5_ln", "conv5x5_ln_res",
          "conv5x5_lrelu", "conv5x5_shuffle", "conv5x5_shuffle_finish", "conv5x5_qkv_win"},
         {"conv_sub2_store", "conv_sub2_gelu", "conv_sub2_res", "conv_sub2_ln", "conv_sub2_ln_res",
