@@ -119,10 +119,12 @@ def test_host_batch_matches_single_forwards(pkg):
     """s2s_forward_batch (host images of mixed sizes, pipelined over the two
     lanes) against s2s_forward per image on a plain context, bit for bit: odd
     and even batches, a batch of one and of none, repeated so each lane
-    replays its graphs; with the compressed head, each image's aux image too,
+    replays its graphs, for the classical, compressed, lightweight and
+    real-world heads; with the compressed head, each image's aux image too,
     and s2s_aux afterwards is the last image's."""
     M = pkg.model
-    for arch, seed in ((M.classical(4), 61), (M.compressed(), 62)):
+    for arch, seed in ((M.classical(4), 61), (M.compressed(), 62), (M.lightweight(2), 65),
+                       (M.Arch(upsampler="nearest+conv", scale=4, embed=180, heads=6, depths=[2, 2]), 66)):
         wts = M.make_weights(arch, seed=seed, perturb=True)
         shapes = [(40, 56), (24, 32), (40, 56), (32, 40), (24, 32)]
         xs = [M.adjust(arch, M.to_unit(M.input_sinusoids(h, w, seed=70 + i)))
