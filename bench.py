@@ -716,8 +716,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this backend runs a whole image on one device and has "
-              "no multi-GPU path (see DESIGN.md for how it would shard); run with --gpus 1.",
-              file=sys.stderr)
+              "no multi-GPU path (images and tiles are independent, so several GPUs would each "
+              "take their share of them); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     pkg = ge.load_package()
